@@ -1,0 +1,195 @@
+#!/usr/bin/env python3
+"""Benchmark: causal GQA attention forward + backward on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config qwen7b_s512]
+
+One step = the attention layer's forward (RoPE, QK^T, causal softmax, PV,
+saving the row log-sum-exp) followed by its backward (dP, softmax gradient,
+dQ/dK/dV with the GQA reduction, inverse RoPE) on device-resident bf16
+tensors: BASELINE.json configs[1] (Qwen2.5-7B: B=1, S=512, 28 Q / 4 KV heads,
+head_dim 128, theta 1e6).  Prints ONE JSON line.
+
+value  = algorithmic FLOPs per step / wall time per step, where algorithmic
+         FLOPs = 12 * D * Hq * sum_b L_b (L_b + 1) / 2 (4 D per unmasked
+         (query, key, head) triple forward, 8 D backward; no credit for the
+         score recompute, softmax or RoPE).
+roofline = the dominant kernel (largest share of device time), timed with
+         hipEvents on the stream it is launched on, against the 2.5 PFLOP/s
+         dense bf16 MFMA peak of MI355X.
+cpu_baseline = the C restatement of the reference CPU path (oracle/), fp32,
+         on this host's cores, over a bounded sample.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "glacier.tune_amd"))
+
+PEAK_BF16_TFLOPS = 2500.0
+METRIC = "causal GQA attn fwd+bwd TFLOP/s + % bf16 MFMA peak, Qwen2.5-7B shape S=512"
+
+CONFIGS = {
+    # name: (lengths, Hq, Hkv, D, theta)
+    "qwen7b_s512": ([512], 28, 4, 128, 1.0e6),
+    "qwen05b_s512": ([512], 14, 2, 64, 1.0e6),
+    "qwen7b_s4096": ([4096], 28, 4, 128, 1.0e6),
+    "llama3_b2_s2048": ([2048, 2048], 32, 8, 128, 5.0e5),
+}
+
+# Algorithmic FLOPs per unmasked (query, key, head) triple, per kernel: the
+# forward does QK^T and PV (4 D); the dK/dV kernel is credited with dP, dV,
+# dK (6 D) and the dQ kernel with dQ (2 D).  Sum: 12 D.
+FLOPS_PER_PAIR = {"attn_fwd": 4, "attn_bwd_dkdv": 6, "attn_bwd_dq": 2}
+
+
+def pairs(lengths):
+    return sum(L * (L + 1) // 2 for L in lengths)
+
+
+def cpu_baseline(lengths, Hq, Hkv, D, theta, budget_s=12.0):
+    """Times oracle.layer_fwd_bwd (fp32, the reference CPU path restated)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+
+    threads = max(1, min(16, os.cpu_count() or 1, Hq))
+    oracle.set_threads(threads)
+    S = lengths[0]
+    q = oracle.fill_normal((S, Hq, D), 1)
+    k = oracle.fill_normal((S, Hkv, D), 2)
+    v = oracle.fill_normal((S, Hkv, D), 3)
+    dO = oracle.fill_normal((S, Hq, D), 4, 0.0, 0.01)
+    oracle.layer_fwd_bwd(q, k, v, dO, theta)  # warm-up
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 5 and (not times or time.perf_counter() < t_end):
+        t0 = time.perf_counter()
+        oracle.layer_fwd_bwd(q, k, v, dO, theta)
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    flops = 12.0 * D * Hq * pairs([S])
+    return {
+        "value": round(flops / med / 1e12, 6),
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"median of {len(times)} full layer fwd+bwd passes (RoPE, attention fwd "
+                   f"materialising P, attention bwd, inverse RoPE) at S={S}, Hq={Hq}, "
+                   f"Hkv={Hkv}, D={D}, fp32; {med * 1e3:.1f} ms each; OpenMP over query heads"),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", default="qwen7b_s512", choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; use --gpus 1 "
+                                   "(the path shards by KV-head group, see DESIGN.md)"}))
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import glacier_attn as ga
+
+    lengths, Hq, Hkv, D, theta = CONFIGS[args.config]
+    T = sum(lengths)
+    cu = None if len(lengths) == 1 else np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+    q = torch.randn(T, Hq, D, device=dev, generator=g).bfloat16()
+    k = torch.randn(T, Hkv, D, device=dev, generator=g).bfloat16()
+    v = torch.randn(T, Hkv, D, device=dev, generator=g).bfloat16()
+    dO = (0.01 * torch.randn(T, Hq, D, device=dev, generator=g)).bfloat16()
+    out = torch.empty_like(q)
+    lse = torch.empty(Hq, T, device=dev, dtype=torch.float32)
+    q_rot = torch.empty_like(q)
+    k_rot = torch.empty_like(k)
+    dq = torch.empty_like(q)
+    dk = torch.empty_like(k)
+    dv = torch.empty_like(v)
+    eng = ga.GpuAttentionEngine(0, ga.PREC_BF16)
+
+    def step():
+        eng.forward(q, k, v, theta, cu_seqlens=cu, out=out, lse=lse, q_rot=q_rot, k_rot=k_rot)
+        eng.backward(dO, q_rot, k_rot, v, out, lse, theta, cu_seqlens=cu, dq=dq, dk=dk, dv=dv)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(args.steps):
+        step()
+    stop.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(stop) / args.steps
+
+    flops = 12.0 * D * Hq * pairs(lengths)
+    tflops = flops / (ms * 1e-3) / 1e12
+
+    # Per-kernel device time (hipEvents recorded around each launch on the
+    # stream it runs on), in a separate pass so the events do not perturb `ms`.
+    eng.set_kernel_timing(True)
+    for _ in range(args.steps):
+        step()
+    times = eng.kernel_times()
+    eng.set_kernel_timing(False)
+    avg = {name: (tot / n if n else 0.0) for name, (tot, n) in times.items()}
+    dom = max(FLOPS_PER_PAIR, key=lambda n: times[n][0])
+    dom_flops = FLOPS_PER_PAIR[dom] * D * Hq * pairs(lengths)
+    achieved = dom_flops / (avg[dom] * 1e-3) / 1e12
+    roofline = {
+        "bound": "mfma",
+        "kernel": dom,
+        "achieved": round(achieved, 3),
+        "peak": PEAK_BF16_TFLOPS,
+        "unit": "TFLOP/s",
+        "frac": round(achieved / PEAK_BF16_TFLOPS, 5),
+        "traffic": None,
+        "kernel_avg_us": {n: round(a * 1e3, 3) for n, a in avg.items()},
+    }
+
+    cpu = None
+    if not args.no_cpu and len(lengths) == 1:
+        cpu = cpu_baseline(lengths, Hq, Hkv, D, theta)
+
+    res = {
+        "metric": METRIC,
+        "value": round(tflops, 3),
+        "unit": "TFLOP/s",
+        "pct_bf16_peak": round(100.0 * tflops / PEAK_BF16_TFLOPS, 3),
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded normal q/k/v, dO*0.01; device-resident)",
+        "config": {
+            "workload": f"{args.config}: causal GQA attention layer fwd+bwd (BASELINE.json configs[1])"
+            if args.config == "qwen7b_s512" else f"{args.config}: causal GQA attention layer fwd+bwd",
+            "seq_lens": lengths, "n_heads_q": Hq, "n_heads_kv": Hkv, "head_dim": D,
+            "rope_theta": theta, "io": "bf16 device tensors, fp32 lse", "parallelism": "1 GPU",
+            "algorithmic_gflop_per_step": round(flops / 1e9, 4),
+        },
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(res), flush=True)
+    eng.close()
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,146 @@
+// attn_launch.hpp -- host-side interface between the engine and the kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include <type_traits>
+#include <utility>
+#include <vector>
+
+namespace glacier {
+
+constexpr int kTile = 64;      // queries or keys per workgroup tile
+constexpr int kWaves = 4;      // waves per workgroup, 16 rows each
+constexpr int kThreads = 256;  // kWaves * 64
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.69314718055994531f;
+constexpr float kNegBig = -1.0e30f;  // running-max start value (finite)
+
+// One 64-row tile of one packed sequence.
+struct TileDesc {
+  int32_t tok0;   // first token of the sequence in the [T][H][D] tensors
+  int32_t len;    // tokens in the sequence
+  int32_t tile;   // tile index inside the sequence (rows 64*tile ..)
+  int32_t ptok0;  // first column of the sequence in the padded transposed scratch
+};
+
+constexpr int kPrecFp32 = 0;
+constexpr int kPrecBf16 = 1;
+
+// Kernel kinds, in launch order.
+enum KernelId : int {
+  kKernKvPrep = 0,
+  kKernFwd = 1,
+  kKernBwdPrep = 2,
+  kKernDq = 3,
+  kKernDkdv = 4,
+  kKernReduce = 5,
+  kKernCount = 6,
+};
+
+// Optional per-kernel hipEvent timing on the launch stream.
+class KernelTimer {
+ public:
+  bool enabled = false;
+  ~KernelTimer() { reset(); }
+  void reset() {
+    for (auto& p : pending_) {
+      (void)hipEventDestroy(p.second.first);
+      (void)hipEventDestroy(p.second.second);
+    }
+    pending_.clear();
+    for (int i = 0; i < kKernCount; ++i) {
+      total_ms_[i] = 0.0;
+      launches_[i] = 0;
+    }
+  }
+  void record(int id, hipEvent_t a, hipEvent_t b) { pending_.push_back({id, {a, b}}); }
+  // Folds finished event pairs into the totals (call after a synchronize).
+  hipError_t collect() {
+    for (auto& p : pending_) {
+      float ms = 0.0f;
+      hipError_t e = hipEventElapsedTime(&ms, p.second.first, p.second.second);
+      if (e != hipSuccess) return e;
+      total_ms_[p.first] += ms;
+      launches_[p.first] += 1;
+      (void)hipEventDestroy(p.second.first);
+      (void)hipEventDestroy(p.second.second);
+    }
+    pending_.clear();
+    return hipSuccess;
+  }
+  double total_ms(int id) const { return total_ms_[id]; }
+  int64_t launches(int id) const { return launches_[id]; }
+
+ private:
+  std::vector<std::pair<int, std::pair<hipEvent_t, hipEvent_t>>> pending_;
+  double total_ms_[kKernCount] = {};
+  int64_t launches_[kKernCount] = {};
+};
+
+// Records a start event now and a stop event when it goes out of scope.
+class ScopedTiming {
+ public:
+  ScopedTiming(KernelTimer* tm, int id, hipStream_t st) : tm_(tm), id_(id), st_(st) {
+    if (tm_ != nullptr && tm_->enabled) {
+      if (hipEventCreate(&a_) == hipSuccess && hipEventCreate(&b_) == hipSuccess &&
+          hipEventRecord(a_, st_) == hipSuccess) {
+        on_ = true;
+      }
+    }
+  }
+  ~ScopedTiming() {
+    if (on_ && hipEventRecord(b_, st_) == hipSuccess) tm_->record(id_, a_, b_);
+  }
+
+ private:
+  KernelTimer* tm_;
+  int id_;
+  hipStream_t st_;
+  hipEvent_t a_ = nullptr, b_ = nullptr;
+  bool on_ = false;
+};
+
+// Everything one forward launch needs (device pointers).
+struct FwdLaunch {
+  int precision;
+  bool io_bf16;
+  int head_dim, n_heads_q, n_heads_kv, total_tokens;
+  int n_tiles, ptot;
+  float scale_log2;
+  const void *q, *k, *v;
+  void *out, *q_rot, *k_rot;
+  float* lse;
+  void *kc, *vt;                 // scratch: rotated K (token-major), V^T
+  const TileDesc* tiles_fwd;     // longest query tiles first
+  const TileDesc* tiles_any;
+  const float *cos_t, *sin_t;    // [max len][D/2]
+};
+
+struct BwdLaunch {
+  int precision;
+  bool io_bf16;
+  int head_dim, n_heads_q, n_heads_kv, total_tokens;
+  int n_tiles, ptot;
+  float scale_log2, scale;
+  const void *d_out, *q_rot, *k_rot, *v, *out;
+  const float* lse;
+  void *dq, *dk, *dv;
+  float* dvec;                   // [Hq][T] row terms dO.O
+  void *dot_t, *qt, *kt;         // transposed scratch
+  void *doc, *qc, *kc, *vc;      // compute-dtype copies (fp32 tensors, bf16 math)
+  float *wk, *wv;                // per-query-head dK/dV partials [T][Hq][D]
+  const TileDesc* tiles_fwd;
+  const TileDesc* tiles_kv;      // key tiles with the most query tiles first
+  const TileDesc* tiles_any;
+  const int32_t* pos_of;         // position of each token inside its sequence
+  const float *cos_t, *sin_t;
+};
+
+hipError_t launch_forward(const FwdLaunch& a, hipStream_t st, KernelTimer* tm);
+hipError_t launch_backward(const BwdLaunch& a, hipStream_t st, KernelTimer* tm);
+size_t compute_elem_size(int precision, bool io_bf16);
+
+}  // namespace glacier

@@ -1,0 +1,620 @@
+// engine.cpp -- host side of libglacier_attn.so.
+//
+// GpuAttentionEngine mirrors the attention half of Glacier.Tune's
+// GpuLoraEngine (src/Glacier.Tune/Gpu/GpuLoraEngine*.cs): the same entry
+// points (SupportsAttention, ForwardAttention, BackwardAttention), the same
+// argument meaning and the same error behaviour (bad arguments are rejected
+// before any device work, device failures surface as errors, scratch grows
+// on demand and is never shrunk, one call at a time per engine).  The
+// extern "C" functions at the bottom are the C ABI declared in
+// include/glacier_attn.h; they translate exceptions into status codes.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../../include/glacier_attn.h"
+#include "attn_launch.hpp"
+
+namespace glacier {
+
+namespace {
+
+thread_local std::string g_last_error;
+
+class Error : public std::runtime_error {
+ public:
+  Error(int code, const std::string& msg) : std::runtime_error(msg), code_(code) {}
+  int code() const { return code_; }
+
+ private:
+  int code_;
+};
+
+[[noreturn]] void fail(int code, const std::string& msg) { throw Error(code, msg); }
+
+void check_hip(hipError_t e, const char* what) {
+  if (e == hipSuccess) return;
+  if (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation)
+    fail(GLACIER_ATTN_ERR_OUT_OF_MEMORY, std::string(what) + ": " + hipGetErrorString(e));
+  fail(GLACIER_ATTN_ERR_DEVICE, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+// Device allocation that only grows (x2 on growth), like the capacity
+// fields of GpuLoraEngine.EnsureAttnCapacity (GpuLoraEngine.Memory.cs:60-114).
+struct DeviceBuffer {
+  void* ptr = nullptr;
+  size_t cap = 0;
+  ~DeviceBuffer() { release(); }
+  void release() {
+    if (ptr != nullptr) (void)hipFree(ptr);
+    ptr = nullptr;
+    cap = 0;
+  }
+  void* ensure(size_t bytes, const char* what) {
+    if (bytes <= cap && ptr != nullptr) return ptr;
+    release();
+    size_t want = std::max<size_t>(bytes * 2, 256);
+    hipError_t e = hipMalloc(&ptr, want);
+    if (e != hipSuccess) {
+      ptr = nullptr;
+      (void)hipGetLastError();
+      fail(GLACIER_ATTN_ERR_OUT_OF_MEMORY,
+           std::string("hipMalloc(") + what + ", " + std::to_string(want) + " bytes): " +
+               hipGetErrorString(e));
+    }
+    cap = want;
+    return ptr;
+  }
+};
+
+struct Shape {
+  int total_tokens = 0;
+  int n_heads_q = 0, n_heads_kv = 0, head_dim = 0;
+  float rope_freq_base = 0.0f;
+  int precision = 0;
+  bool io_bf16 = false;
+  std::vector<int32_t> cu;  // n_seqs + 1 offsets
+};
+
+// Tile lists of one sequence layout, resident on the device.
+struct TileSet {
+  int n_tiles = 0, ptot = 0, max_len = 0;
+  DeviceBuffer tiles;  // [3][n_tiles] TileDesc: fwd order, kv order, natural
+  DeviceBuffer pos;    // [T] int32
+};
+
+}  // namespace
+
+class GpuAttentionEngine {
+ public:
+  GpuAttentionEngine(int device_ordinal, int precision)
+      : device_(device_ordinal), precision_(precision) {
+    int n = 0;
+    check_hip(hipGetDeviceCount(&n), "hipGetDeviceCount");
+    if (device_ordinal < 0 || device_ordinal >= n)
+      fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT,
+           "device ordinal " + std::to_string(device_ordinal) + " out of range (" +
+               std::to_string(n) + " devices)");
+    check_hip(hipSetDevice(device_), "hipSetDevice");
+    check_hip(hipStreamCreateWithFlags(&own_stream_, hipStreamNonBlocking), "hipStreamCreate");
+  }
+
+  ~GpuAttentionEngine() {
+    (void)hipSetDevice(device_);
+    if (own_stream_ != nullptr) {
+      (void)hipStreamSynchronize(own_stream_);
+      (void)hipStreamDestroy(own_stream_);
+    }
+  }
+
+  // GpuLoraEngine.SupportsAttention (GpuLoraEngine.cs:111-112): the shapes
+  // the GPU kernels take; anything else stays on the CPU path.
+  static bool SupportsAttention(int seq_len, int head_dim) {
+    return (head_dim == 64 || head_dim == 128) && seq_len >= 1 &&
+           seq_len <= GLACIER_ATTN_MAX_SEQ_LEN;
+  }
+
+  std::mutex& lock() { return mutex_; }
+  hipStream_t stream() const { return has_user_stream_ ? user_stream_ : own_stream_; }
+  void set_stream(hipStream_t s) {
+    user_stream_ = s;
+    has_user_stream_ = true;
+  }
+  void use_own_stream() { has_user_stream_ = false; }
+  int precision() const { return precision_; }
+  KernelTimer& timer() { return timer_; }
+  void activate() { check_hip(hipSetDevice(device_), "hipSetDevice"); }
+
+  // ---- device entry points --------------------------------------------
+  // LaunchRopeBatch + LaunchAttnTrainFwd (GpuLoraEngine.Forward.cs:401-465).
+  void LaunchAttnTrainFwd(const Shape& s, const void* q, const void* k, const void* v,
+                          void* out, float* lse, void* q_rot, void* k_rot) {
+    if (s.total_tokens == 0) return;
+    const TileSet& ts = tiles_for(s);
+    EnsureRopeTable(ts.max_len, s.head_dim, s.rope_freq_base);
+    const size_t esz = compute_elem_size(s.precision, s.io_bf16);
+    FwdLaunch a{};
+    a.precision = s.precision;
+    a.io_bf16 = s.io_bf16;
+    a.head_dim = s.head_dim;
+    a.n_heads_q = s.n_heads_q;
+    a.n_heads_kv = s.n_heads_kv;
+    a.total_tokens = s.total_tokens;
+    a.n_tiles = ts.n_tiles;
+    a.ptot = ts.ptot;
+    a.scale_log2 = kLog2e / std::sqrt(static_cast<float>(s.head_dim));
+    a.q = q; a.k = k; a.v = v;
+    a.out = out; a.lse = lse; a.q_rot = q_rot; a.k_rot = k_rot;
+    a.kc = kc_.ensure((size_t)s.total_tokens * s.n_heads_kv * s.head_dim * esz, "K scratch");
+    a.vt = vt_.ensure((size_t)s.n_heads_kv * s.head_dim * ts.ptot * esz, "V^T scratch");
+    const TileDesc* t = static_cast<const TileDesc*>(ts.tiles.ptr);
+    a.tiles_fwd = t;
+    a.tiles_any = t + 2 * ts.n_tiles;
+    a.cos_t = static_cast<const float*>(rope_cos_.ptr);
+    a.sin_t = static_cast<const float*>(rope_sin_.ptr);
+    check_hip(launch_forward(a, stream(), &timer_), "attention forward launch");
+  }
+
+  // LaunchAttnTrainBwd + inverse LaunchRopeBatch (GpuLoraEngine.Backward.cs:354-412, :452).
+  void LaunchAttnTrainBwd(const Shape& s, const void* d_out, const void* q_rot,
+                          const void* k_rot, const void* v, const void* out,
+                          const float* lse, void* dq, void* dk, void* dv) {
+    if (s.total_tokens == 0) return;
+    const TileSet& ts = tiles_for(s);
+    EnsureRopeTable(ts.max_len, s.head_dim, s.rope_freq_base);
+    const size_t esz = compute_elem_size(s.precision, s.io_bf16);
+    const size_t T = s.total_tokens, Hq = s.n_heads_q, Hkv = s.n_heads_kv, D = s.head_dim;
+    const bool copies = !s.io_bf16 && s.precision == kPrecBf16;
+    BwdLaunch a{};
+    a.precision = s.precision;
+    a.io_bf16 = s.io_bf16;
+    a.head_dim = s.head_dim;
+    a.n_heads_q = s.n_heads_q;
+    a.n_heads_kv = s.n_heads_kv;
+    a.total_tokens = s.total_tokens;
+    a.n_tiles = ts.n_tiles;
+    a.ptot = ts.ptot;
+    a.scale = 1.0f / std::sqrt(static_cast<float>(s.head_dim));
+    a.scale_log2 = kLog2e * a.scale;
+    a.d_out = d_out; a.q_rot = q_rot; a.k_rot = k_rot; a.v = v; a.out = out;
+    a.lse = lse; a.dq = dq; a.dk = dk; a.dv = dv;
+    a.dvec = static_cast<float*>(dvec_.ensure(Hq * T * sizeof(float), "dO.O scratch"));
+    a.dot_t = dot_t_.ensure(Hq * D * ts.ptot * esz, "dO^T scratch");
+    a.qt = qt_.ensure(Hq * D * ts.ptot * esz, "Q^T scratch");
+    a.kt = kt_.ensure(Hkv * D * ts.ptot * esz, "K^T scratch");
+    if (copies) {
+      a.doc = doc_.ensure(T * Hq * D * esz, "dO scratch");
+      a.qc = qc_.ensure(T * Hq * D * esz, "Q scratch");
+      a.kc = kc_.ensure(T * Hkv * D * esz, "K scratch");
+      a.vc = vc_.ensure(T * Hkv * D * esz, "V scratch");
+    }
+    a.wk = static_cast<float*>(wk_.ensure(T * Hq * D * sizeof(float), "dK partials"));
+    a.wv = static_cast<float*>(wv_.ensure(T * Hq * D * sizeof(float), "dV partials"));
+    const TileDesc* t = static_cast<const TileDesc*>(ts.tiles.ptr);
+    a.tiles_fwd = t;
+    a.tiles_kv = t + ts.n_tiles;
+    a.tiles_any = t + 2 * ts.n_tiles;
+    a.pos_of = static_cast<const int32_t*>(ts.pos.ptr);
+    a.cos_t = static_cast<const float*>(rope_cos_.ptr);
+    a.sin_t = static_cast<const float*>(rope_sin_.ptr);
+    check_hip(launch_backward(a, stream(), &timer_), "attention backward launch");
+  }
+
+  // ---- host entry points (fp32 host tensors) ----------------------------
+  // GpuLoraEngine.ForwardAttention (GpuLoraEngine.Forward.cs:467-512).
+  void ForwardAttention(int /*layerIndex*/, float* q, float* k, const float* v,
+                        float* attnOut, float* attnLse, const Shape& s) {
+    if (s.total_tokens == 0) return;
+    const size_t qb = (size_t)s.total_tokens * s.n_heads_q * s.head_dim * sizeof(float);
+    const size_t kb = (size_t)s.total_tokens * s.n_heads_kv * s.head_dim * sizeof(float);
+    const size_t lb = (size_t)s.n_heads_q * s.total_tokens * sizeof(float);
+    EnsureAttnCapacity(s);
+    hipStream_t st = stream();
+    check_hip(hipMemcpyAsync(h_q_.ptr, q, qb, hipMemcpyHostToDevice, st), "copy q to device");
+    check_hip(hipMemcpyAsync(h_k_.ptr, k, kb, hipMemcpyHostToDevice, st), "copy k to device");
+    check_hip(hipMemcpyAsync(h_v_.ptr, v, kb, hipMemcpyHostToDevice, st), "copy v to device");
+    const bool save = attnLse != nullptr;
+    LaunchAttnTrainFwd(s, h_q_.ptr, h_k_.ptr, h_v_.ptr, h_out_.ptr,
+                       save ? static_cast<float*>(h_lse_.ptr) : nullptr,
+                       save ? h_qr_.ptr : nullptr, save ? h_kr_.ptr : nullptr);
+    check_hip(hipMemcpyAsync(attnOut, h_out_.ptr, qb, hipMemcpyDeviceToHost, st), "copy out to host");
+    if (save) {
+      check_hip(hipMemcpyAsync(attnLse, h_lse_.ptr, lb, hipMemcpyDeviceToHost, st), "copy lse to host");
+      check_hip(hipMemcpyAsync(q, h_qr_.ptr, qb, hipMemcpyDeviceToHost, st), "copy q_rot to host");
+      check_hip(hipMemcpyAsync(k, h_kr_.ptr, kb, hipMemcpyDeviceToHost, st), "copy k_rot to host");
+    }
+    check_hip(hipStreamSynchronize(st), "forward attention");
+  }
+
+  // GpuLoraEngine.BackwardAttention (GpuLoraEngine.Backward.cs:414-458).
+  void BackwardAttention(int /*layerIndex*/, const float* dAttnOut, const float* q,
+                         const float* k, const float* v, const float* attnOut,
+                         const float* attnLse, float* dq, float* dk, float* dv,
+                         const Shape& s) {
+    if (s.total_tokens == 0) return;
+    const size_t qb = (size_t)s.total_tokens * s.n_heads_q * s.head_dim * sizeof(float);
+    const size_t kb = (size_t)s.total_tokens * s.n_heads_kv * s.head_dim * sizeof(float);
+    const size_t lb = (size_t)s.n_heads_q * s.total_tokens * sizeof(float);
+    EnsureAttnCapacity(s);
+    hipStream_t st = stream();
+    check_hip(hipMemcpyAsync(h_dout_.ptr, dAttnOut, qb, hipMemcpyHostToDevice, st), "copy dO to device");
+    check_hip(hipMemcpyAsync(h_q_.ptr, q, qb, hipMemcpyHostToDevice, st), "copy q to device");
+    check_hip(hipMemcpyAsync(h_k_.ptr, k, kb, hipMemcpyHostToDevice, st), "copy k to device");
+    check_hip(hipMemcpyAsync(h_v_.ptr, v, kb, hipMemcpyHostToDevice, st), "copy v to device");
+    check_hip(hipMemcpyAsync(h_out_.ptr, attnOut, qb, hipMemcpyHostToDevice, st), "copy out to device");
+    check_hip(hipMemcpyAsync(h_lse_.ptr, attnLse, lb, hipMemcpyHostToDevice, st), "copy lse to device");
+    LaunchAttnTrainBwd(s, h_dout_.ptr, h_q_.ptr, h_k_.ptr, h_v_.ptr, h_out_.ptr,
+                       static_cast<const float*>(h_lse_.ptr), h_dq_.ptr, h_dk_.ptr, h_dv_.ptr);
+    check_hip(hipMemcpyAsync(dq, h_dq_.ptr, qb, hipMemcpyDeviceToHost, st), "copy dq to host");
+    check_hip(hipMemcpyAsync(dk, h_dk_.ptr, kb, hipMemcpyDeviceToHost, st), "copy dk to host");
+    check_hip(hipMemcpyAsync(dv, h_dv_.ptr, kb, hipMemcpyDeviceToHost, st), "copy dv to host");
+    check_hip(hipStreamSynchronize(st), "backward attention");
+  }
+
+ private:
+  // Device copies of the host tensors (GpuLoraEngine.Memory.cs:60-114).
+  void EnsureAttnCapacity(const Shape& s) {
+    const size_t qb = (size_t)s.total_tokens * s.n_heads_q * s.head_dim * sizeof(float);
+    const size_t kb = (size_t)s.total_tokens * s.n_heads_kv * s.head_dim * sizeof(float);
+    const size_t lb = (size_t)s.n_heads_q * s.total_tokens * sizeof(float);
+    h_q_.ensure(qb, "q"); h_qr_.ensure(qb, "q_rot"); h_out_.ensure(qb, "attn_out");
+    h_dout_.ensure(qb, "d_attn_out"); h_dq_.ensure(qb, "dq");
+    h_k_.ensure(kb, "k"); h_kr_.ensure(kb, "k_rot"); h_v_.ensure(kb, "v");
+    h_dk_.ensure(kb, "dk"); h_dv_.ensure(kb, "dv");
+    h_lse_.ensure(lb, "lse");
+  }
+
+  // cos/sin per (position, pair) computed on the host with exactly the fp32
+  // operations of RoPEKernel.cs:64-68 (glibc powf/cosf/sinf), uploaded once
+  // per (length capacity, head_dim, theta).
+  void EnsureRopeTable(int max_len, int head_dim, float base) {
+    if (max_len <= rope_len_ && head_dim == rope_dim_ && base == rope_base_) return;
+    const int len = std::max(max_len, std::min(2 * rope_len_, GLACIER_ATTN_MAX_SEQ_LEN));
+    const int half = head_dim / 2;
+    std::vector<float> cs((size_t)len * half), sn((size_t)len * half);
+    std::vector<float> freq(half);
+    for (int i = 0; i < half; i++)
+      freq[i] = 1.0f / powf(base, static_cast<float>(2 * i) / static_cast<float>(head_dim));
+    for (int pos = 0; pos < len; pos++)
+      for (int i = 0; i < half; i++) {
+        const float theta = static_cast<float>(pos) * freq[i];
+        cs[(size_t)pos * half + i] = cosf(theta);
+        sn[(size_t)pos * half + i] = sinf(theta);
+      }
+    const size_t bytes = cs.size() * sizeof(float);
+    rope_cos_.ensure(bytes, "rope cos");
+    rope_sin_.ensure(bytes, "rope sin");
+    check_hip(hipStreamSynchronize(stream()), "rope table");
+    check_hip(hipMemcpy(rope_cos_.ptr, cs.data(), bytes, hipMemcpyHostToDevice), "rope cos upload");
+    check_hip(hipMemcpy(rope_sin_.ptr, sn.data(), bytes, hipMemcpyHostToDevice), "rope sin upload");
+    rope_len_ = len;
+    rope_dim_ = head_dim;
+    rope_base_ = base;
+  }
+
+  const TileSet& tiles_for(const Shape& s) {
+    auto it = tile_cache_.find(s.cu);
+    if (it != tile_cache_.end()) return *it->second;
+    auto ts = std::make_unique<TileSet>();
+    std::vector<TileDesc> nat;
+    std::vector<int32_t> pos(s.total_tokens);
+    int ptok = 0;
+    const int n = static_cast<int>(s.cu.size()) - 1;
+    for (int b = 0; b < n; ++b) {
+      const int tok0 = s.cu[b], len = s.cu[b + 1] - s.cu[b];
+      if (len <= 0) continue;
+      const int nt = (len + kTile - 1) / kTile;
+      for (int t = 0; t < nt; ++t) nat.push_back(TileDesc{tok0, len, t, ptok});
+      for (int i = 0; i < len; ++i) pos[tok0 + i] = i;
+      ptok += nt * kTile;
+      ts->max_len = std::max(ts->max_len, len);
+    }
+    ts->n_tiles = static_cast<int>(nat.size());
+    ts->ptot = ptok;
+    if (ts->n_tiles > 65535)
+      fail(GLACIER_ATTN_ERR_UNSUPPORTED, "more than 65535 tiles of 64 tokens in one call");
+    // Longest query tiles first (they see the most keys), and key tiles with
+    // the most query tiles first, so the long workgroups start earliest.
+    std::vector<TileDesc> fwd = nat, kv = nat;
+    std::stable_sort(fwd.begin(), fwd.end(),
+                     [](const TileDesc& x, const TileDesc& y) { return x.tile > y.tile; });
+    auto remaining = [](const TileDesc& x) { return (x.len + kTile - 1) / kTile - x.tile; };
+    std::stable_sort(kv.begin(), kv.end(), [&](const TileDesc& x, const TileDesc& y) {
+      return remaining(x) > remaining(y);
+    });
+    std::vector<TileDesc> all;
+    all.insert(all.end(), fwd.begin(), fwd.end());
+    all.insert(all.end(), kv.begin(), kv.end());
+    all.insert(all.end(), nat.begin(), nat.end());
+    ts->tiles.ensure(all.size() * sizeof(TileDesc), "tile table");
+    ts->pos.ensure(pos.size() * sizeof(int32_t), "position table");
+    check_hip(hipStreamSynchronize(stream()), "tile table");
+    check_hip(hipMemcpy(ts->tiles.ptr, all.data(), all.size() * sizeof(TileDesc),
+                        hipMemcpyHostToDevice), "tile table upload");
+    check_hip(hipMemcpy(ts->pos.ptr, pos.data(), pos.size() * sizeof(int32_t),
+                        hipMemcpyHostToDevice), "position table upload");
+    if (tile_cache_.size() >= 64) tile_cache_.clear();
+    auto& ref = *ts;
+    tile_cache_[s.cu] = std::move(ts);
+    return ref;
+  }
+
+  int device_;
+  int precision_;
+  hipStream_t own_stream_ = nullptr;
+  hipStream_t user_stream_ = nullptr;
+  bool has_user_stream_ = false;
+  std::mutex mutex_;
+  KernelTimer timer_;
+  std::map<std::vector<int32_t>, std::unique_ptr<TileSet>> tile_cache_;
+  DeviceBuffer rope_cos_, rope_sin_;
+  int rope_len_ = 0, rope_dim_ = 0;
+  float rope_base_ = 0.0f;
+  // device-path scratch
+  DeviceBuffer kc_, vt_, dvec_, dot_t_, qt_, kt_, doc_, qc_, vc_, wk_, wv_;
+  // host-path device copies
+  DeviceBuffer h_q_, h_k_, h_v_, h_out_, h_lse_, h_qr_, h_kr_, h_dout_, h_dq_, h_dk_, h_dv_;
+};
+
+namespace {
+
+// Validates a shape before anything touches the GPU.  Throws Error.
+Shape make_shape(int total_tokens, int n_seqs, const int32_t* cu, int hq, int hkv,
+                 int d, float base, int precision, int io) {
+  Shape s;
+  if (n_seqs < 1) fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, "n_seqs must be >= 1");
+  if (total_tokens < 0) fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, "total_tokens must be >= 0");
+  if (hq <= 0 || hkv <= 0)
+    fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, "head counts must be positive");
+  if (hq % hkv != 0)
+    fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT,
+         "n_heads_q (" + std::to_string(hq) + ") must be a multiple of n_heads_kv (" +
+             std::to_string(hkv) + ")");
+  if (d <= 0 || d > 1024)
+    fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT,
+         "GPU training attention requires 1 <= headDim <= 1024, got " + std::to_string(d) + ".");
+  if (!(base > 0.0f) || !std::isfinite(base))
+    fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, "rope_freq_base must be positive and finite");
+  if (precision != GLACIER_ATTN_PREC_FP32 && precision != GLACIER_ATTN_PREC_BF16)
+    fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, "unknown precision " + std::to_string(precision));
+  if (io != GLACIER_ATTN_IO_F32 && io != GLACIER_ATTN_IO_BF16)
+    fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, "unknown io dtype " + std::to_string(io));
+  if (io == GLACIER_ATTN_IO_BF16 && precision != GLACIER_ATTN_PREC_BF16)
+    fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, "bf16 device tensors need GLACIER_ATTN_PREC_BF16");
+  s.cu.resize(n_seqs + 1);
+  if (cu == nullptr) {
+    if (n_seqs != 1)
+      fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, "cu_seqlens is required when n_seqs > 1");
+    s.cu[0] = 0;
+    s.cu[1] = total_tokens;
+  } else {
+    if (cu[0] != 0) fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, "cu_seqlens[0] must be 0");
+    for (int b = 0; b <= n_seqs; ++b) {
+      if (b > 0 && cu[b] < cu[b - 1])
+        fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, "cu_seqlens must be non-decreasing");
+      s.cu[b] = cu[b];
+    }
+    if (cu[n_seqs] != total_tokens)
+      fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, "cu_seqlens[n_seqs] must equal total_tokens");
+  }
+  int max_len = 0;
+  for (int b = 0; b < n_seqs; ++b) max_len = std::max(max_len, s.cu[b + 1] - s.cu[b]);
+  if (d != 64 && d != 128)
+    fail(GLACIER_ATTN_ERR_UNSUPPORTED,
+         "head_dim " + std::to_string(d) + " is not supported by the GPU kernels (64 or 128)");
+  if (max_len > GLACIER_ATTN_MAX_SEQ_LEN)
+    fail(GLACIER_ATTN_ERR_UNSUPPORTED, "sequence of " + std::to_string(max_len) +
+                                           " tokens exceeds GLACIER_ATTN_MAX_SEQ_LEN");
+  if ((long long)total_tokens * hq * d >= (1LL << 40))
+    fail(GLACIER_ATTN_ERR_UNSUPPORTED, "tensor too large");
+  s.total_tokens = total_tokens;
+  s.n_heads_q = hq;
+  s.n_heads_kv = hkv;
+  s.head_dim = d;
+  s.rope_freq_base = base;
+  s.precision = precision;
+  s.io_bf16 = io == GLACIER_ATTN_IO_BF16;
+  return s;
+}
+
+Shape shape_of(const glacier_attn_desc* desc) {
+  if (desc == nullptr) fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, "desc is NULL");
+  return make_shape(desc->total_tokens, desc->n_seqs, desc->cu_seqlens, desc->n_heads_q,
+                    desc->n_heads_kv, desc->head_dim, desc->rope_freq_base,
+                    desc->precision, desc->io_dtype);
+}
+
+void need(const void* p, const char* name) {
+  if (p == nullptr) fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, std::string(name) + " is NULL");
+}
+
+template <typename F>
+int guarded(F&& f) {
+  try {
+    f();
+    g_last_error.clear();
+    return GLACIER_ATTN_OK;
+  } catch (const Error& e) {
+    g_last_error = e.what();
+    return e.code();
+  } catch (const std::bad_alloc&) {
+    g_last_error = "host allocation failed";
+    return GLACIER_ATTN_ERR_OUT_OF_MEMORY;
+  } catch (const std::exception& e) {
+    g_last_error = e.what();
+    return GLACIER_ATTN_ERR_DEVICE;
+  }
+}
+
+const char* const kKernelNames[kKernCount] = {
+    "kv_prep", "attn_fwd", "bwd_prep", "attn_bwd_dq", "attn_bwd_dkdv", "dkdv_reduce",
+};
+
+}  // namespace
+}  // namespace glacier
+
+struct glacier_attn_ctx {
+  std::unique_ptr<glacier::GpuAttentionEngine> eng;
+};
+
+using glacier::fail;
+using glacier::guarded;
+using glacier::need;
+
+extern "C" {
+
+int glacier_attn_create(int device_ordinal, int precision, glacier_attn_ctx** out) {
+  return guarded([&] {
+    need(out, "out");
+    *out = nullptr;
+    if (precision != GLACIER_ATTN_PREC_FP32 && precision != GLACIER_ATTN_PREC_BF16)
+      fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, "unknown precision " + std::to_string(precision));
+    auto ctx = std::make_unique<glacier_attn_ctx>();
+    ctx->eng = std::make_unique<glacier::GpuAttentionEngine>(device_ordinal, precision);
+    *out = ctx.release();
+  });
+}
+
+void glacier_attn_destroy(glacier_attn_ctx* ctx) { delete ctx; }
+
+const char* glacier_attn_last_error(void) { return glacier::g_last_error.c_str(); }
+
+int glacier_attn_supports(int seq_len, int head_dim) {
+  return glacier::GpuAttentionEngine::SupportsAttention(seq_len, head_dim) ? 1 : 0;
+}
+
+int glacier_attn_forward_host(glacier_attn_ctx* ctx, int layer_index, float* q, float* k,
+                              const float* v, float* attn_out, float* attn_lse, int seq_len,
+                              int n_heads_q, int n_heads_kv, int head_dim,
+                              float rope_freq_base) {
+  return guarded([&] {
+    const int prec = ctx != nullptr ? ctx->eng->precision() : GLACIER_ATTN_PREC_FP32;
+    glacier::Shape s = glacier::make_shape(seq_len, 1, nullptr, n_heads_q, n_heads_kv, head_dim,
+                                           rope_freq_base, prec, GLACIER_ATTN_IO_F32);
+    need(ctx, "ctx");
+    need(q, "q"); need(k, "k"); need(v, "v"); need(attn_out, "attn_out");
+    std::lock_guard<std::mutex> g(ctx->eng->lock());
+    ctx->eng->activate();
+    ctx->eng->ForwardAttention(layer_index, q, k, v, attn_out, attn_lse, s);
+  });
+}
+
+int glacier_attn_backward_host(glacier_attn_ctx* ctx, int layer_index, const float* d_attn_out,
+                               const float* q, const float* k, const float* v,
+                               const float* attn_out, const float* attn_lse, float* dq,
+                               float* dk, float* dv, int seq_len, int n_heads_q,
+                               int n_heads_kv, int head_dim, float rope_freq_base) {
+  return guarded([&] {
+    const int prec = ctx != nullptr ? ctx->eng->precision() : GLACIER_ATTN_PREC_FP32;
+    glacier::Shape s = glacier::make_shape(seq_len, 1, nullptr, n_heads_q, n_heads_kv, head_dim,
+                                           rope_freq_base, prec, GLACIER_ATTN_IO_F32);
+    need(ctx, "ctx");
+    need(d_attn_out, "d_attn_out"); need(q, "q"); need(k, "k"); need(v, "v");
+    need(attn_out, "attn_out"); need(attn_lse, "attn_lse");
+    need(dq, "dq"); need(dk, "dk"); need(dv, "dv");
+    std::lock_guard<std::mutex> g(ctx->eng->lock());
+    ctx->eng->activate();
+    ctx->eng->BackwardAttention(layer_index, d_attn_out, q, k, v, attn_out, attn_lse, dq, dk, dv,
+                                s);
+  });
+}
+
+int glacier_attn_forward(glacier_attn_ctx* ctx, const glacier_attn_desc* desc, const void* q,
+                         const void* k, const void* v, void* out, float* lse, void* q_rot,
+                         void* k_rot) {
+  return guarded([&] {
+    glacier::Shape s = glacier::shape_of(desc);
+    need(ctx, "ctx");
+    if (s.total_tokens > 0) {
+      need(q, "q"); need(k, "k"); need(v, "v"); need(out, "out");
+    }
+    std::lock_guard<std::mutex> g(ctx->eng->lock());
+    ctx->eng->activate();
+    ctx->eng->LaunchAttnTrainFwd(s, q, k, v, out, lse, q_rot, k_rot);
+  });
+}
+
+int glacier_attn_backward(glacier_attn_ctx* ctx, const glacier_attn_desc* desc,
+                          const void* d_out, const void* q_rot, const void* k_rot, const void* v,
+                          const void* out, const float* lse, void* dq, void* dk, void* dv) {
+  return guarded([&] {
+    glacier::Shape s = glacier::shape_of(desc);
+    need(ctx, "ctx");
+    if (s.total_tokens > 0) {
+      need(d_out, "d_out"); need(q_rot, "q_rot"); need(k_rot, "k_rot"); need(v, "v");
+      need(out, "out"); need(lse, "lse"); need(dq, "dq"); need(dk, "dk"); need(dv, "dv");
+    }
+    std::lock_guard<std::mutex> g(ctx->eng->lock());
+    ctx->eng->activate();
+    ctx->eng->LaunchAttnTrainBwd(s, d_out, q_rot, k_rot, v, out, lse, dq, dk, dv);
+  });
+}
+
+int glacier_attn_set_stream(glacier_attn_ctx* ctx, void* hip_stream) {
+  return guarded([&] {
+    need(ctx, "ctx");
+    std::lock_guard<std::mutex> g(ctx->eng->lock());
+    ctx->eng->set_stream(static_cast<hipStream_t>(hip_stream));
+  });
+}
+
+int glacier_attn_use_own_stream(glacier_attn_ctx* ctx) {
+  return guarded([&] {
+    need(ctx, "ctx");
+    std::lock_guard<std::mutex> g(ctx->eng->lock());
+    ctx->eng->use_own_stream();
+  });
+}
+
+int glacier_attn_synchronize(glacier_attn_ctx* ctx) {
+  return guarded([&] {
+    need(ctx, "ctx");
+    std::lock_guard<std::mutex> g(ctx->eng->lock());
+    ctx->eng->activate();
+    glacier::check_hip(hipStreamSynchronize(ctx->eng->stream()), "synchronize");
+  });
+}
+
+int glacier_attn_set_kernel_timing(glacier_attn_ctx* ctx, int enable) {
+  return guarded([&] {
+    need(ctx, "ctx");
+    std::lock_guard<std::mutex> g(ctx->eng->lock());
+    ctx->eng->activate();
+    glacier::check_hip(hipStreamSynchronize(ctx->eng->stream()), "synchronize");
+    ctx->eng->timer().reset();
+    ctx->eng->timer().enabled = enable != 0;
+  });
+}
+
+int glacier_attn_kernel_count(void) { return glacier::kKernCount; }
+
+const char* glacier_attn_kernel_name(int id) {
+  if (id < 0 || id >= glacier::kKernCount) return nullptr;
+  return glacier::kKernelNames[id];
+}
+
+int glacier_attn_kernel_time(glacier_attn_ctx* ctx, int id, double* total_ms, int64_t* launches) {
+  return guarded([&] {
+    need(ctx, "ctx");
+    need(total_ms, "total_ms");
+    need(launches, "launches");
+    if (id < 0 || id >= glacier::kKernCount)
+      fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, "kernel id out of range");
+    std::lock_guard<std::mutex> g(ctx->eng->lock());
+    ctx->eng->activate();
+    glacier::check_hip(hipStreamSynchronize(ctx->eng->stream()), "synchronize");
+    glacier::check_hip(ctx->eng->timer().collect(), "kernel timing");
+    *total_ms = ctx->eng->timer().total_ms(id);
+    *launches = ctx->eng->timer().launches(id);
+  });
+}
+
+}  // extern "C"

@@ -1,0 +1,306 @@
+"""Python front end of libglacier_attn.so (ctypes; no torch types cross the ABI).
+
+`GpuAttentionEngine` mirrors the attention methods of Glacier.Tune's
+GpuLoraEngine with the same names and argument meaning:
+
+    supports_attention(seq_len, head_dim)            GpuLoraEngine.cs:111-112
+    forward_attention(layer, q, k, v, out, lse, ...) GpuLoraEngine.Forward.cs:467-512
+    backward_attention(layer, dO, q, k, v, out, lse, dq, dk, dv, ...)
+                                                     GpuLoraEngine.Backward.cs:414-458
+
+on host float32 numpy arrays, plus `forward` / `backward` on device-resident
+torch tensors (passed to the library as raw pointers, enqueued on torch's
+current stream).  Errors raise: InvalidArgument (a ValueError, where the C#
+engine throws ArgumentOutOfRangeException), Unsupported (the shape stays on
+the CPU path), DeviceError, OutOfMemory.  There is no fallback: if the
+library is missing or the device fails, the call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libglacier_attn.so")
+HEADER = os.path.join(os.path.dirname(HERE), "include", "glacier_attn.h")
+
+OK, ERR_INVALID_ARGUMENT, ERR_UNSUPPORTED, ERR_DEVICE, ERR_OUT_OF_MEMORY = 0, 1, 2, 3, 4
+PREC_FP32, PREC_BF16 = 0, 1
+IO_F32, IO_BF16 = 0, 1
+
+
+class GlacierAttnError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"[{code}] {msg}")
+        self.code = code
+
+
+class InvalidArgument(GlacierAttnError, ValueError):
+    pass
+
+
+class Unsupported(GlacierAttnError):
+    pass
+
+
+class DeviceError(GlacierAttnError):
+    pass
+
+
+class OutOfMemory(GlacierAttnError, MemoryError):
+    pass
+
+
+_ERRORS = {ERR_INVALID_ARGUMENT: InvalidArgument, ERR_UNSUPPORTED: Unsupported,
+           ERR_DEVICE: DeviceError, ERR_OUT_OF_MEMORY: OutOfMemory}
+
+
+class Desc(ctypes.Structure):
+    _fields_ = [
+        ("total_tokens", ctypes.c_int32),
+        ("n_seqs", ctypes.c_int32),
+        ("cu_seqlens", ctypes.POINTER(ctypes.c_int32)),
+        ("n_heads_q", ctypes.c_int32),
+        ("n_heads_kv", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("rope_freq_base", ctypes.c_float),
+        ("precision", ctypes.c_int32),
+        ("io_dtype", ctypes.c_int32),
+    ]
+
+
+_lib = None
+
+
+def header_functions() -> list[str]:
+    """Names of every function include/glacier_attn.h declares."""
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(glacier_attn_[a-z_]+)\s*\(", text)))
+
+
+def load():
+    """Loads the built library (raises if it is not built: no fallback)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is not built: run `python glacier.tune_amd/build.py`")
+    L = ctypes.CDLL(LIB_PATH)
+    c_int, c_float, vp = ctypes.c_int, ctypes.c_float, ctypes.c_void_p
+    fp = ctypes.POINTER(ctypes.c_float)
+    L.glacier_attn_create.argtypes = [c_int, c_int, ctypes.POINTER(vp)]
+    L.glacier_attn_destroy.argtypes = [vp]
+    L.glacier_attn_destroy.restype = None
+    L.glacier_attn_last_error.restype = ctypes.c_char_p
+    L.glacier_attn_supports.argtypes = [c_int, c_int]
+    L.glacier_attn_forward_host.argtypes = [vp, c_int, fp, fp, fp, fp, fp, c_int, c_int,
+                                            c_int, c_int, c_float]
+    L.glacier_attn_backward_host.argtypes = [vp, c_int, fp, fp, fp, fp, fp, fp, fp, fp, fp,
+                                             c_int, c_int, c_int, c_int, c_float]
+    L.glacier_attn_forward.argtypes = [vp, ctypes.POINTER(Desc), vp, vp, vp, vp, vp, vp, vp]
+    L.glacier_attn_backward.argtypes = [vp, ctypes.POINTER(Desc), vp, vp, vp, vp, vp, vp, vp,
+                                        vp, vp]
+    L.glacier_attn_set_stream.argtypes = [vp, vp]
+    L.glacier_attn_use_own_stream.argtypes = [vp]
+    L.glacier_attn_synchronize.argtypes = [vp]
+    L.glacier_attn_set_kernel_timing.argtypes = [vp, c_int]
+    L.glacier_attn_kernel_name.restype = ctypes.c_char_p
+    L.glacier_attn_kernel_name.argtypes = [c_int]
+    L.glacier_attn_kernel_time.argtypes = [vp, c_int, ctypes.POINTER(ctypes.c_double),
+                                           ctypes.POINTER(ctypes.c_int64)]
+    _lib = L
+    return L
+
+
+def _check(rc: int) -> None:
+    if rc != OK:
+        msg = load().glacier_attn_last_error().decode(errors="replace")
+        raise _ERRORS.get(rc, GlacierAttnError)(rc, msg)
+
+
+def supports_attention(seq_len: int, head_dim: int) -> bool:
+    return bool(load().glacier_attn_supports(int(seq_len), int(head_dim)))
+
+
+def _fptr(a):
+    if a is None:
+        return None
+    return a.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+
+
+def _host(a, name):
+    if not (isinstance(a, np.ndarray) and a.dtype == np.float32 and a.flags.c_contiguous):
+        raise TypeError(f"{name} must be a C-contiguous float32 numpy array")
+    return a
+
+
+def kernel_names() -> list[str]:
+    L = load()
+    return [L.glacier_attn_kernel_name(i).decode() for i in range(L.glacier_attn_kernel_count())]
+
+
+class GpuAttentionEngine:
+    """One library context: a device, a stream and grow-only scratch."""
+
+    def __init__(self, device_ordinal: int = 0, precision: int = PREC_BF16):
+        L = load()
+        h = ctypes.c_void_p()
+        _check(L.glacier_attn_create(int(device_ordinal), int(precision), ctypes.byref(h)))
+        self._h = h
+        self.precision = precision
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            load().glacier_attn_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    @staticmethod
+    def supports_attention(seq_len: int, head_dim: int) -> bool:
+        return supports_attention(seq_len, head_dim)
+
+    # ---- host (numpy float32) entry points -------------------------------
+    def forward_attention(self, layer_index, q, k, v, attn_out, attn_lse, seq_len,
+                          n_heads_q, n_heads_kv, head_dim, rope_freq_base):
+        """In place like the C# engine: attn_out written; with attn_lse given,
+        q/k become post-RoPE and attn_lse [Hq, S] is written."""
+        for a, n in ((q, "q"), (k, "k"), (v, "v"), (attn_out, "attn_out")):
+            _host(a, n)
+        if attn_lse is not None:
+            _host(attn_lse, "attn_lse")
+        _check(load().glacier_attn_forward_host(
+            self._h, int(layer_index), _fptr(q), _fptr(k), _fptr(v), _fptr(attn_out),
+            _fptr(attn_lse), int(seq_len), int(n_heads_q), int(n_heads_kv), int(head_dim),
+            float(rope_freq_base)))
+
+    def backward_attention(self, layer_index, d_attn_out, q, k, v, attn_out, attn_lse, dq, dk,
+                           dv, seq_len, n_heads_q, n_heads_kv, head_dim, rope_freq_base):
+        for a, n in ((d_attn_out, "d_attn_out"), (q, "q"), (k, "k"), (v, "v"),
+                     (attn_out, "attn_out"), (attn_lse, "attn_lse"), (dq, "dq"), (dk, "dk"),
+                     (dv, "dv")):
+            _host(a, n)
+        _check(load().glacier_attn_backward_host(
+            self._h, int(layer_index), _fptr(d_attn_out), _fptr(q), _fptr(k), _fptr(v),
+            _fptr(attn_out), _fptr(attn_lse), _fptr(dq), _fptr(dk), _fptr(dv), int(seq_len),
+            int(n_heads_q), int(n_heads_kv), int(head_dim), float(rope_freq_base)))
+
+    # ---- device (torch tensor) entry points -------------------------------
+    @staticmethod
+    def _desc(T, hq, hkv, d, base, precision, io, cu):
+        desc = Desc()
+        desc.total_tokens = int(T)
+        desc.n_heads_q, desc.n_heads_kv, desc.head_dim = int(hq), int(hkv), int(d)
+        desc.rope_freq_base = float(base)
+        desc.precision, desc.io_dtype = int(precision), int(io)
+        keep = None
+        if cu is None:
+            desc.n_seqs = 1
+            desc.cu_seqlens = None
+        else:
+            keep = np.ascontiguousarray(np.asarray(cu, dtype=np.int32))
+            desc.n_seqs = len(keep) - 1
+            desc.cu_seqlens = keep.ctypes.data_as(ctypes.POINTER(ctypes.c_int32))
+        return desc, keep
+
+    def _bind_stream(self):
+        import torch
+
+        _check(load().glacier_attn_set_stream(self._h, ctypes.c_void_p(
+            torch.cuda.current_stream().cuda_stream)))
+
+    @staticmethod
+    def _ptr(t):
+        return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+    @staticmethod
+    def _io_of(t):
+        import torch
+
+        if t.dtype == torch.float32:
+            return IO_F32
+        if t.dtype == torch.bfloat16:
+            return IO_BF16
+        raise TypeError(f"unsupported tensor dtype {t.dtype}")
+
+    def forward(self, q, k, v, rope_freq_base, precision=None, cu_seqlens=None, save=True,
+                out=None, lse=None, q_rot=None, k_rot=None):
+        """q [T,Hq,D], k/v [T,Hkv,D] (pre-RoPE, on the GPU, float32 or bfloat16).
+        Returns (out, lse, q_rot, k_rot); the last three are None unless save."""
+        import torch
+
+        prec = self.precision if precision is None else precision
+        T, hq, d = q.shape
+        hkv = k.shape[1]
+        for t in (q, k, v):
+            if not t.is_contiguous() or t.dtype != q.dtype or not t.is_cuda:
+                raise TypeError("q, k, v must be contiguous GPU tensors of one dtype")
+        io = self._io_of(q)
+        out = torch.empty_like(q) if out is None else out
+        if save:
+            lse = torch.empty((hq, T), dtype=torch.float32, device=q.device) if lse is None else lse
+            q_rot = torch.empty_like(q) if q_rot is None else q_rot
+            k_rot = torch.empty_like(k) if k_rot is None else k_rot
+        else:
+            lse = q_rot = k_rot = None
+        desc, _keep = self._desc(T, hq, hkv, d, rope_freq_base, prec, io, cu_seqlens)
+        self._bind_stream()
+        _check(load().glacier_attn_forward(self._h, ctypes.byref(desc), self._ptr(q),
+                                           self._ptr(k), self._ptr(v), self._ptr(out),
+                                           self._ptr(lse), self._ptr(q_rot), self._ptr(k_rot)))
+        return out, lse, q_rot, k_rot
+
+    def backward(self, d_out, q_rot, k_rot, v, out, lse, rope_freq_base, precision=None,
+                 cu_seqlens=None, dq=None, dk=None, dv=None):
+        """Returns (dq, dk, dv); dq/dk w.r.t. the pre-RoPE q/k."""
+        import torch
+
+        prec = self.precision if precision is None else precision
+        T, hq, d = q_rot.shape
+        hkv = k_rot.shape[1]
+        for t in (d_out, q_rot, k_rot, v, out):
+            if not t.is_contiguous() or t.dtype != q_rot.dtype or not t.is_cuda:
+                raise TypeError("backward tensors must be contiguous GPU tensors of one dtype")
+        io = self._io_of(q_rot)
+        dq = torch.empty_like(q_rot) if dq is None else dq
+        dk = torch.empty_like(k_rot) if dk is None else dk
+        dv = torch.empty_like(v) if dv is None else dv
+        desc, _keep = self._desc(T, hq, hkv, d, rope_freq_base, prec, io, cu_seqlens)
+        self._bind_stream()
+        _check(load().glacier_attn_backward(self._h, ctypes.byref(desc), self._ptr(d_out),
+                                            self._ptr(q_rot), self._ptr(k_rot), self._ptr(v),
+                                            self._ptr(out), self._ptr(lse), self._ptr(dq),
+                                            self._ptr(dk), self._ptr(dv)))
+        return dq, dk, dv
+
+    # ---- instrumentation ---------------------------------------------------
+    def set_kernel_timing(self, enable: bool) -> None:
+        _check(load().glacier_attn_set_kernel_timing(self._h, 1 if enable else 0))
+
+    def kernel_times(self) -> dict:
+        """{kernel name: (total ms, launches)} since timing was enabled."""
+        L = load()
+        res = {}
+        for i, name in enumerate(kernel_names()):
+            ms = ctypes.c_double()
+            n = ctypes.c_int64()
+            _check(L.glacier_attn_kernel_time(self._h, i, ctypes.byref(ms), ctypes.byref(n)))
+            res[name] = (ms.value, n.value)
+        return res
+
+    def synchronize(self) -> None:
+        _check(load().glacier_attn_synchronize(self._h))

@@ -1,0 +1,301 @@
+"""GPU parity: libglacier_attn.so (through its C ABI) against the CPU oracle.
+
+Gates, normwise max relative error
+max|gpu - ref| / max|ref| per tensor:
+  fp32-operand mode  <= 1e-4 on O, lse, dQ, dK, dV; post-RoPE q/k bit-exact
+  bf16-MFMA mode     <= 2e-2 on O, dQ, dK, dV (inputs rounded to bf16 on the
+                     host first; the oracle runs on the same rounded values)
+Configs: BASELINE.json configs[0] (Qwen2.5-0.5B, S=512, 14/2, D=64) and
+configs[1] (Qwen2.5-7B, S=512, 28/4, D=128) against the oracle; configs[2]
+(packed varlen) against the oracle per segment; configs[3] (S=4096) and
+configs[4] (Llama-3-8B B=2 S=2048) against a float32 torch reference on the
+GPU (the oracle would take minutes there), plus edge cases.
+"""
+import functools
+import sys
+
+import numpy as np
+import pytest
+
+import glacier_attn as ga
+import oracle
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+FP32_GATE = 1e-4
+BF16_GATE = 2e-2
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def engines():
+    assert torch.cuda.is_available(), "GPU tests need a ROCm GPU"
+    e32 = ga.GpuAttentionEngine(0, ga.PREC_FP32)
+    e16 = ga.GpuAttentionEngine(0, ga.PREC_BF16)
+    yield {ga.PREC_FP32: e32, ga.PREC_BF16: e16}
+    e32.close()
+    e16.close()
+
+
+def make_inputs(S, Hq, Hkv, D, seed=1, bf16=False):
+    q = oracle.fill_normal((S, Hq, D), seed * 10 + 1)
+    k = oracle.fill_normal((S, Hkv, D), seed * 10 + 2)
+    v = oracle.fill_normal((S, Hkv, D), seed * 10 + 3)
+    dO = oracle.fill_normal((S, Hq, D), seed * 10 + 4, 0.0, 0.01)
+    if bf16:
+        q, k, v, dO = (oracle.round_bf16(x) for x in (q, k, v, dO))
+    return q, k, v, dO
+
+
+@functools.lru_cache(maxsize=8)
+def oracle_case(S, Hq, Hkv, D, base, seed, bf16):
+    q, k, v, dO = make_inputs(S, Hq, Hkv, D, seed, bf16)
+    return (q, k, v, dO), oracle.layer_fwd_bwd(q, k, v, dO, base)
+
+
+def run_host(eng, q, k, v, dO, base):
+    """The C# call sequence: ForwardAttention (saving) then BackwardAttention."""
+    S, Hq, D = q.shape
+    Hkv = k.shape[1]
+    q = q.copy(); k = k.copy()
+    out = np.empty_like(q)
+    lse = np.empty((Hq, S), np.float32)
+    eng.forward_attention(0, q, k, v, out, lse, S, Hq, Hkv, D, base)
+    dq = np.zeros_like(q); dk = np.zeros_like(k); dv = np.zeros_like(v)
+    eng.backward_attention(0, dO, q, k, v, out, lse, dq, dk, dv, S, Hq, Hkv, D, base)
+    return dict(q_rot=q, k_rot=k, out=out, lse=lse, dq=dq, dk=dk, dv=dv)
+
+
+def errors(got, ref, keys=("out", "lse", "dq", "dk", "dv")):
+    return {key: oracle.max_rel_err(got[key], ref[key]) for key in keys}
+
+
+CONFIGS = {
+    "qwen05b_s512": (512, 14, 2, 64, 1.0e6),
+    "qwen7b_s512": (512, 28, 4, 128, 1.0e6),
+}
+
+
+@pytest.mark.parametrize("name", list(CONFIGS))
+def test_fp32_mode_matches_oracle(engines, name):
+    S, Hq, Hkv, D, base = CONFIGS[name]
+    _say(f"[fp32 parity] {name} S={S} Hq={Hq} Hkv={Hkv} D={D}")
+    (q, k, v, dO), ref = oracle_case(S, Hq, Hkv, D, base, 1, False)
+    got = run_host(engines[ga.PREC_FP32], q, k, v, dO, base)
+    err = errors(got, ref)
+    _say(f"  errors {err}")
+    assert all(e <= FP32_GATE for e in err.values()), err
+    # post-RoPE write-back: the same fp32 operations as RoPEKernel.cs
+    assert np.array_equal(got["q_rot"], ref["q_rot"])
+    assert np.array_equal(got["k_rot"], ref["k_rot"])
+
+
+@pytest.mark.parametrize("name", list(CONFIGS))
+def test_bf16_mode_matches_oracle(engines, name):
+    S, Hq, Hkv, D, base = CONFIGS[name]
+    _say(f"[bf16 parity] {name}")
+    (q, k, v, dO), ref = oracle_case(S, Hq, Hkv, D, base, 1, True)
+    got = run_host(engines[ga.PREC_BF16], q, k, v, dO, base)
+    err = errors(got, ref)
+    _say(f"  errors {err}")
+    assert all(e <= BF16_GATE for e in err.values()), err
+    assert np.array_equal(got["q_rot"], ref["q_rot"])
+
+
+def _dev(x, dtype):
+    return torch.from_numpy(np.ascontiguousarray(x)).to("cuda").to(dtype).contiguous()
+
+
+def run_device(eng, q, k, v, dO, base, dtype, cu=None):
+    tq, tk, tv, tdo = (_dev(x, dtype) for x in (q, k, v, dO))
+    out, lse, q_rot, k_rot = eng.forward(tq, tk, tv, base, cu_seqlens=cu, save=True)
+    dq, dk, dv = eng.backward(tdo, q_rot, k_rot, tv, out, lse, base, cu_seqlens=cu)
+    torch.cuda.synchronize()
+    f = lambda t: t.float().cpu().numpy()  # noqa: E731
+    return dict(out=f(out), lse=f(lse), q_rot=f(q_rot), k_rot=f(k_rot), dq=f(dq), dk=f(dk), dv=f(dv))
+
+
+@pytest.mark.parametrize("name", list(CONFIGS))
+def test_bf16_device_tensors_match_oracle(engines, name):
+    S, Hq, Hkv, D, base = CONFIGS[name]
+    _say(f"[bf16 device io] {name}")
+    (q, k, v, dO), ref = oracle_case(S, Hq, Hkv, D, base, 1, True)
+    got = run_device(engines[ga.PREC_BF16], q, k, v, dO, base, torch.bfloat16)
+    err = errors(got, ref)
+    _say(f"  errors {err}")
+    assert all(e <= BF16_GATE for e in err.values()), err
+
+
+@pytest.mark.parametrize("S,Hq,Hkv,D", [
+    (1, 2, 1, 64), (2, 4, 4, 128), (17, 7, 1, 128), (63, 4, 2, 64), (64, 2, 2, 64),
+    (65, 6, 3, 128), (100, 8, 2, 64), (129, 14, 2, 128), (200, 2, 1, 64),
+])
+@pytest.mark.parametrize("prec", [ga.PREC_FP32, ga.PREC_BF16])
+def test_small_and_ragged_shapes(engines, S, Hq, Hkv, D, prec):
+    base = 1.0e4
+    bf = prec == ga.PREC_BF16
+    _say(f"[shape] S={S} Hq={Hq} Hkv={Hkv} D={D} prec={prec}")
+    (q, k, v, dO), ref = oracle_case(S, Hq, Hkv, D, base, 3, bf)
+    got = run_host(engines[prec], q, k, v, dO, base)
+    err = errors(got, ref)
+    gate = BF16_GATE if bf else FP32_GATE
+    assert all(e <= gate for e in err.values()), err
+
+
+def test_forward_without_save_leaves_qk_and_matches_saving_forward(engines):
+    S, Hq, Hkv, D, base = 96, 4, 2, 64, 1.0e6
+    _say("[no-save forward]")
+    eng = engines[ga.PREC_BF16]
+    q, k, v, _ = make_inputs(S, Hq, Hkv, D, 5, True)
+    q0, k0 = q.copy(), k.copy()
+    out_a = np.empty_like(q)
+    eng.forward_attention(0, q, k, v, out_a, None, S, Hq, Hkv, D, base)
+    assert np.array_equal(q, q0) and np.array_equal(k, k0)
+    out_b = np.empty_like(q)
+    lse = np.empty((Hq, S), np.float32)
+    eng.forward_attention(0, q, k, v, out_b, lse, S, Hq, Hkv, D, base)
+    assert np.array_equal(out_a, out_b)  # O does not depend on saving
+    assert not np.array_equal(q, q0)     # q became post-RoPE
+
+
+@pytest.mark.parametrize("prec", [ga.PREC_FP32, ga.PREC_BF16])
+def test_recompute_and_backward_are_bitwise_repeatable(engines, prec):
+    """Activation checkpointing re-runs the forward (GgufLoraModel.cs:521-527);
+    the reference demands identical gradients (GradientAndGpuParityTests.cs:143-172)."""
+    S, Hq, Hkv, D, base = 300, 14, 2, 128, 1.0e6
+    _say(f"[determinism] prec={prec}")
+    q, k, v, dO = make_inputs(S, Hq, Hkv, D, 7, prec == ga.PREC_BF16)
+    a = run_host(engines[prec], q, k, v, dO, base)
+    b = run_host(engines[prec], q, k, v, dO, base)
+    for key in a:
+        assert np.array_equal(a[key], b[key]), key
+
+
+def test_varlen_packed_batch_matches_oracle_per_segment(engines):
+    """BASELINE configs[2] shape: 4 packed sequences, lengths U[64,512] (seed 5),
+    block-diagonal causal mask, 7B heads, bf16."""
+    Hq, Hkv, D, base = 28, 4, 128, 1.0e6
+    rng = np.random.default_rng(5)
+    lens = rng.integers(64, 513, size=4)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    T = int(cu[-1])
+    _say(f"[varlen] lens={lens.tolist()}")
+    q, k, v, dO = make_inputs(T, Hq, Hkv, D, 9, True)
+    ref = oracle.layer_fwd_bwd_varlen(q, k, v, dO, cu, base)
+    got = run_device(engines[ga.PREC_BF16], q, k, v, dO, base, torch.bfloat16, cu=cu)
+    err = errors(got, ref)
+    _say(f"  errors {err}")
+    assert all(e <= BF16_GATE for e in err.values()), err
+    # fp32 device tensors with fp32 math on the same packing
+    (q, k, v, dO) = make_inputs(T, Hq, Hkv, D, 9, False)
+    ref = oracle.layer_fwd_bwd_varlen(q, k, v, dO, cu, base)
+    got = run_device(engines[ga.PREC_FP32], q, k, v, dO, base, torch.float32, cu=cu)
+    err = errors(got, ref)
+    assert all(e <= FP32_GATE for e in err.values()), err
+
+
+# ---------------------------------------------------------------------------
+# Large shapes: float32 torch reference on the GPU (plain matmul/softmax).
+# ---------------------------------------------------------------------------
+
+def torch_reference(q, k, v, dO, base, cu):
+    """Float32 reference of the whole layer, per segment, with autograd."""
+    D = q.shape[-1]
+    half = D // 2
+    r = q.shape[1] // k.shape[1]
+    qd = q.detach().float().clone().requires_grad_(True)
+    kd = k.detach().float().clone().requires_grad_(True)
+    vd = v.detach().float().clone().requires_grad_(True)
+    w = base ** (-(2.0 * np.arange(half)) / D)
+    outs, lses = [], []
+    for b in range(len(cu) - 1):
+        s0, s1 = int(cu[b]), int(cu[b + 1])
+        L = s1 - s0
+        th = np.arange(L)[:, None] * w[None, :]
+        c = torch.tensor(np.cos(th), dtype=torch.float32, device=q.device)[:, None, :]
+        s = torch.tensor(np.sin(th), dtype=torch.float32, device=q.device)[:, None, :]
+
+        def rot(x):
+            return torch.cat([x[..., :half] * c - x[..., half:] * s,
+                              x[..., :half] * s + x[..., half:] * c], dim=-1)
+
+        qr = rot(qd[s0:s1]).permute(1, 0, 2).contiguous()                       # [Hq,L,D]
+        kr = rot(kd[s0:s1]).repeat_interleave(r, dim=1).permute(1, 2, 0).contiguous()  # [Hq,D,L]
+        vr = vd[s0:s1].repeat_interleave(r, dim=1).permute(1, 0, 2).contiguous()
+        sc = torch.matmul(qr, kr) / np.sqrt(D)
+        mask = torch.ones(L, L, dtype=torch.bool, device=q.device).tril()
+        sc = sc.masked_fill(~mask, float("-inf"))
+        lses.append(torch.logsumexp(sc, dim=-1))
+        outs.append(torch.matmul(torch.softmax(sc, dim=-1), vr).permute(1, 0, 2))
+    out = torch.cat(outs, 0)
+    out.backward(dO.float())
+    return dict(out=out.detach(), lse=torch.cat(lses, 1).detach(), dq=qd.grad, dk=kd.grad,
+                dv=vd.grad)
+
+
+@pytest.mark.parametrize("name,lens,Hq,Hkv,base", [
+    ("long_s4096", [4096], 28, 4, 1.0e6),
+    ("llama3_b2_s2048", [2048, 2048], 32, 8, 5.0e5),
+])
+def test_large_shapes_match_torch_fp32_reference(engines, name, lens, Hq, Hkv, base):
+    D = 128
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    T = int(cu[-1])
+    _say(f"[large] {name} T={T}")
+    g = torch.Generator(device="cuda").manual_seed(1234)
+    q = torch.randn(T, Hq, D, device="cuda", generator=g).bfloat16()
+    k = torch.randn(T, Hkv, D, device="cuda", generator=g).bfloat16()
+    v = torch.randn(T, Hkv, D, device="cuda", generator=g).bfloat16()
+    dO = (0.01 * torch.randn(T, Hq, D, device="cuda", generator=g)).bfloat16()
+    eng = engines[ga.PREC_BF16]
+    cuarg = None if len(lens) == 1 else cu
+    out, lse, q_rot, k_rot = eng.forward(q, k, v, base, cu_seqlens=cuarg)
+    dq, dk, dv = eng.backward(dO, q_rot, k_rot, v, out, lse, base, cu_seqlens=cuarg)
+    torch.cuda.synchronize()
+    ref = torch_reference(q, k, v, dO, base, cu)
+    got = dict(out=out, lse=lse, dq=dq, dk=dk, dv=dv)
+    err = {key: float((got[key].float() - ref[key]).abs().max() / ref[key].abs().max())
+           for key in got}
+    _say(f"  errors {err}")
+    assert all(e <= BF16_GATE for e in err.values()), err
+
+
+# ---------------------------------------------------------------------------
+# Error behaviour and special values
+# ---------------------------------------------------------------------------
+
+def test_invalid_arguments_raise(engines):
+    eng = engines[ga.PREC_FP32]
+    q = np.zeros((8, 3, 64), np.float32)
+    k = np.zeros((8, 2, 64), np.float32)
+    out = np.empty_like(q)
+    with pytest.raises(ga.InvalidArgument):
+        eng.forward_attention(0, q, k, k, out, None, 8, 3, 2, 64, 1e4)  # Hq % Hkv != 0
+    q = np.zeros((8, 2, 96), np.float32)
+    with pytest.raises(ga.Unsupported):
+        eng.forward_attention(0, q, q, q, np.empty_like(q), None, 8, 2, 2, 96, 1e4)
+    assert not ga.supports_attention(512, 96)
+    assert ga.supports_attention(512, 128)
+
+
+def test_empty_sequence_is_a_no_op(engines):
+    eng = engines[ga.PREC_BF16]
+    q = torch.empty((0, 4, 64), device="cuda", dtype=torch.bfloat16)
+    k = torch.empty((0, 2, 64), device="cuda", dtype=torch.bfloat16)
+    out, lse, q_rot, k_rot = eng.forward(q, k, k, 1e4)
+    assert out.shape == (0, 4, 64)
+
+
+def test_nan_in_upstream_gradient_propagates(engines):
+    S, Hq, Hkv, D, base = 70, 4, 2, 64, 1e4
+    q, k, v, dO = make_inputs(S, Hq, Hkv, D, 11, True)
+    dO[5, 1, 3] = np.nan
+    got = run_host(engines[ga.PREC_BF16], q, k, v, dO, base)
+    assert np.isfinite(got["out"]).all()
+    assert np.isnan(got["dq"][5, 1]).any()
+    assert np.isnan(got["dv"]).any()
