@@ -8,17 +8,21 @@
 // Lane l (g = l / 16, c = l % 16) supplies A[row c][k = KPL*g .. +KPL-1] and
 // B[k = KPL*g .. +KPL-1][col c], and receives D[row 4g + r][col c], r = 0..3.
 //
-// The kernels compute scores transposed, S^T = K Q^T (one wave owns 16
-// queries as the MFMA columns), so a lane's accumulators all belong to ONE
-// query (column c) and hold 4 consecutive keys 16b + 4g + r of each 16-key
-// block b.  Those registers are fed straight back as the B operand of the
-// next product (O^T += V^T P^T, dQ^T += K^T dS^T, dV^T += dO^T P, dK^T +=
-// Q^T dS) by permuting the k index of the MFMA: for bf16 the 8 k-slots of
-// lane group g in 32-key step s are keys {32s + 4g + r} U {32s + 16 + 4g + r};
-// the A operand is read from a transposed LDS tile with the same map (two
-// 8-byte reads).  Row statistics (max, sum, alpha) therefore never leave the
-// lane except for one xor-16/xor-32 exchange, and no accumulator is ever
-// shuffled.
+// Scores are computed transposed where a wave owns 16 queries (S^T = K Q^T,
+// queries as the MFMA columns) and plainly where it owns 16 keys (S = Q K^T,
+// keys as the columns), so a lane's accumulators always belong to ONE column
+// (one query, or one key) and hold 4 consecutive rows 16b + 4g + r of each
+// 16-row block b.  Those registers are fed straight back as the B operand of
+// the next product (O^T += V^T P^T, dQ^T += K^T dS^T, dV^T += dO^T P,
+// dK^T += Q^T dS) by permuting the k index of the MFMA: for bf16 the 8
+// k-slots of lane group g in 32-row step s are rows {32s + 4g + r} U
+// {32s + 16 + 4g + r}.  The matching A operand is read from a ROW-MAJOR LDS
+// tile with the gfx950 transpose read ds_read_b64_tr_b16: in each group of
+// 16 lanes, lane 4a+b addresses row R + a, columns c0 + 4b .. +3, and lane i
+// receives rows R .. R+3 of column c0 + i -- exactly the 4 consecutive rows
+// the permuted k-slots want.  No tile is ever stored transposed, in LDS or
+// in HBM.  Row statistics (max, sum, alpha) never leave the lane except for
+// one xor-16/xor-32 exchange, and no accumulator is ever shuffled.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -33,6 +37,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
+#define GLACIER_LDS __attribute__((address_space(3)))
 
 template <typename T>
 struct Mfma;
@@ -57,16 +62,15 @@ struct Mfma<float> {
   }
 };
 
-// LDS row strides (elements).  Row-major tiles: D + one 16-byte chunk, so
-// the 16 rows read by one MFMA operand fall in different banks.
-// Transposed tiles (64 columns): 64 + one 16-byte chunk.
+// Row stride (elements) of a row-major [64][D] LDS tile, padded so the 16
+// rows read by one MFMA operand fall in different banks: bf16 rows of 288 B
+// (D=128) or 144 B (D=64), fp32 rows of D+4 floats.  (Measured on gfx950 for
+// the 16-byte fragment reads: 148 B/clk/CU at 288 B against 104 at 272 B.)
 template <typename T, int D>
 struct Lds {
   static constexpr int CE = 16 / sizeof(T);  // elements per 16-byte chunk
-  static constexpr int RM = D + CE;
-  static constexpr int TR = kTile + CE;
-  static constexpr int RM_ELEMS = kTile * RM;  // one row-major tile
-  static constexpr int TR_ELEMS = D * TR;      // one transposed tile
+  static constexpr int STRIDE = (sizeof(T) == 2 && D == 128) ? D + 2 * CE : D + CE;
+  static constexpr int TILE = kTile * STRIDE;  // elements of one tile
 };
 
 __device__ inline float to_f32(float x) { return x; }
@@ -79,51 +83,87 @@ __device__ inline float from_f32<float>(float x) { return x; }
 template <>
 __device__ inline bf16 from_f32<bf16>(float x) { return (bf16)x; }
 
-// 16-byte chunk copy global -> LDS, zero when `valid` is false.
-template <typename T>
-__device__ inline void copy16(T* dst, const T* src, bool valid) {
-  uint4 v = valid ? *reinterpret_cast<const uint4*>(src) : make_uint4(0, 0, 0, 0);
-  *reinterpret_cast<uint4*>(dst) = v;
+__device__ inline void load8(const float* p, float (&x)[8]) {
+  float4 a = *reinterpret_cast<const float4*>(p);
+  float4 b = *reinterpret_cast<const float4*>(p + 4);
+  x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+  x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
 }
-
-// Stage a row-major [64][D] tile: rows r < nvalid come from src + r*gstride.
-template <typename T, int D>
-__device__ inline void stage_rm(T* lds, const T* src, long gstride, int nvalid,
-                                int tid) {
-  using L = Lds<T, D>;
-  constexpr int CPR = D / L::CE;                // chunks per row
-  constexpr int ITERS = kTile * CPR / kThreads;
+__device__ inline void load8(const bf16* p, float (&x)[8]) {
+  bf16x8 v = *reinterpret_cast<const bf16x8*>(p);
 #pragma unroll
-  for (int it = 0; it < ITERS; ++it) {
-    int idx = tid + it * kThreads;
-    int r = idx / CPR, ch = idx % CPR;
-    copy16(lds + r * L::RM + ch * L::CE, src + (long)r * gstride + ch * L::CE,
-           r < nvalid);
-  }
+  for (int i = 0; i < 8; ++i) x[i] = (float)v[i];
 }
-
-// Stage a transposed [D][64] tile: row d comes from src + d*gstride (64
-// contiguous, 16-byte aligned, zero-padded columns).
-template <typename T, int D>
-__device__ inline void stage_tr(T* lds, const T* src, long gstride, int tid) {
-  using L = Lds<T, D>;
-  constexpr int CPR = kTile / L::CE;
-  constexpr int ITERS = D * CPR / kThreads;
+__device__ inline void store8(float* p, const float (&x)[8]) {
+  *reinterpret_cast<float4*>(p) = make_float4(x[0], x[1], x[2], x[3]);
+  *reinterpret_cast<float4*>(p + 4) = make_float4(x[4], x[5], x[6], x[7]);
+}
+__device__ inline void store8(bf16* p, const float (&x)[8]) {
+  bf16x8 v;
 #pragma unroll
-  for (int it = 0; it < ITERS; ++it) {
-    int idx = tid + it * kThreads;
-    int r = idx / CPR, ch = idx % CPR;
-    copy16(lds + r * L::TR + ch * L::CE, src + (long)r * gstride + ch * L::CE,
-           true);
-  }
+  for (int i = 0; i < 8; ++i) v[i] = (bf16)x[i];
+  *reinterpret_cast<bf16x8*>(p) = v;
+}
+__device__ inline void store4(float* p, f32x4 v) {
+  *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+}
+__device__ inline void store4(bf16* p, f32x4 v) {
+  bf16x4 b;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) b[i] = (bf16)v[i];
+  *reinterpret_cast<bf16x4*>(p) = b;
 }
 
-// A-operand fragment from a row-major LDS tile: row `row`, k-step kk.
+// This thread's share of a [64][D] tile held in registers between a global
+// load and an LDS store (the software pipeline of every kernel's main loop).
+// Chunks are 8 consecutive elements of one row; chunk index tid + i*NT maps
+// to (row, chunk) with the chunk fastest, so a wave reads whole rows.
+template <typename IO, int D, int NT = kThreads>
+struct TileRegs {
+  static constexpr int CPR = D / 8;                  // chunks per row
+  static constexpr int N = kTile * CPR / NT;         // chunks per thread
+  static constexpr int W = 8 * sizeof(IO) / 16;      // 16-byte words per chunk
+  static_assert(N * NT == kTile * CPR, "tile must split evenly");
+  uint4 w[N][W];
+
+  // Rows r >= nvalid are zero (past the end of the sequence).
+  __device__ inline void load(const IO* src, long gstride, int nvalid, int tid) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int idx = tid + i * NT;
+      const int r = idx / CPR, ch = idx % CPR;
+      const uint4* p = reinterpret_cast<const uint4*>(src + (long)r * gstride + ch * 8);
+#pragma unroll
+      for (int j = 0; j < W; ++j) w[i][j] = r < nvalid ? p[j] : make_uint4(0, 0, 0, 0);
+    }
+  }
+
+  // Writes the tile to a row-major LDS tile of element type T (converting).
+  template <typename T>
+  __device__ inline void store(T* lds, int tid) const {
+    constexpr int S = Lds<T, D>::STRIDE;
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int idx = tid + i * NT;
+      const int r = idx / CPR, ch = idx % CPR;
+      T* dst = lds + r * S + ch * 8;
+      if constexpr (sizeof(IO) == sizeof(T)) {
+#pragma unroll
+        for (int j = 0; j < W; ++j) reinterpret_cast<uint4*>(dst)[j] = w[i][j];
+      } else {
+        float x[8];
+        load8(reinterpret_cast<const IO*>(&w[i][0]), x);
+        store8(dst, x);
+      }
+    }
+  }
+};
+
+// A/B fragment from a row-major LDS tile: row `row`, k-step kk, lane group g.
 template <typename T, int D>
-__device__ inline typename Mfma<T>::Frag frag_rm(const T* lds, int row, int kk,
-                                                 int g) {
+__device__ inline typename Mfma<T>::Frag frag_rm(const T* lds, int row, int kk, int g) {
   using M = Mfma<T>;
-  const T* p = lds + row * Lds<T, D>::RM + kk * M::KSTEP + M::KPL * g;
+  const T* p = lds + row * Lds<T, D>::STRIDE + kk * M::KSTEP + M::KPL * g;
   if constexpr (sizeof(T) == 2) {
     return *reinterpret_cast<const bf16x8*>(p);
   } else {
@@ -131,15 +171,59 @@ __device__ inline typename Mfma<T>::Frag frag_rm(const T* lds, int row, int kk,
   }
 }
 
-// acc[db] (+)= sum over the 64 columns of the transposed tile `tt`
-// (rows d = 16*db + c) times the lane's own probabilities/gradients
-// v[b][r] (column 16b + 4g + r), i.e. Out^T += Tt * V^T with the permuted
-// k-slot map described at the top of this file.  Blocks b >= nb are zero
-// and skipped.
+// A/B fragment straight from a global row (token-major tensor), converted to
+// the compute dtype: elements kk*KSTEP + KPL*g .. of the row.
+template <typename T, typename IO>
+__device__ inline typename Mfma<T>::Frag frag_global(const IO* rowp, int kk, int g) {
+  using M = Mfma<T>;
+  const IO* p = rowp + kk * M::KSTEP + M::KPL * g;
+  if constexpr (sizeof(T) == 2) {
+    if constexpr (sizeof(IO) == 2) {
+      return *reinterpret_cast<const bf16x8*>(p);
+    } else {
+      float x[8];
+      load8(p, x);
+      bf16x8 f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) f[e] = (bf16)x[e];
+      return f;
+    }
+  } else {
+    return to_f32(*p);
+  }
+}
+
+template <typename T>
+__device__ inline typename Mfma<T>::Frag frag_zero() {
+  if constexpr (sizeof(T) == 2) {
+    bf16x8 z;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) z[i] = (bf16)0.0f;
+    return z;
+  } else {
+    return 0.0f;
+  }
+}
+
+// Transpose read: 4 consecutive rows R..R+3 of column c0 + (lane % 16) of a
+// row-major bf16 LDS tile, where R = row0 + 4 * (lane / 16).
+template <int STRIDE>
+__device__ inline bf16x4 read_tr(const bf16* tile, int row0, int c0, int lane) {
+  const int g = lane >> 4, i = lane & 15;
+  const bf16* p = tile + (row0 + 4 * g + (i >> 2)) * STRIDE + c0 + 4 * (i & 3);
+  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+      (bf16x4 GLACIER_LDS*)(const_cast<bf16*>(p)));
+}
+
+// acc[db] (+)= sum over the 64 rows of the row-major LDS tile `tile`, of
+// tile[row][16*db + i] * v[row-slot] -- i.e. Out^T[d][col] += Tile^T * V
+// with Out^T row d = 16*db + i (the MFMA A row) and the lane's own values
+// v[b][r] for row 16b + 4g + r as the B operand (permuted k-slots, see the
+// top of this file).  Row blocks b >= nb are zero and skipped.
 template <typename T, int D>
-__device__ inline void acc_tr(f32x4 (&acc)[D / 16], const T* tt,
-                              const float (&v)[4][4], int nb, int lane) {
-  using L = Lds<T, D>;
+__device__ inline void acc_rows(f32x4 (&acc)[D / 16], const T* tile,
+                                const float (&v)[4][4], int nb, int lane) {
+  constexpr int S = Lds<T, D>::STRIDE;
   const int g = lane >> 4, c = lane & 15;
   if constexpr (sizeof(T) == 2) {
 #pragma unroll
@@ -153,9 +237,8 @@ __device__ inline void acc_tr(f32x4 (&acc)[D / 16], const T* tt,
       }
 #pragma unroll
       for (int db = 0; db < D / 16; ++db) {
-        const T* row = tt + (16 * db + c) * L::TR + 32 * s + 4 * g;
-        bf16x4 lo = *reinterpret_cast<const bf16x4*>(row);
-        bf16x4 hi = *reinterpret_cast<const bf16x4*>(row + 16);
+        const bf16x4 lo = read_tr<S>(tile, 32 * s, 16 * db, lane);
+        const bf16x4 hi = read_tr<S>(tile, 32 * s + 16, 16 * db, lane);
         bf16x8 a;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -173,7 +256,7 @@ __device__ inline void acc_tr(f32x4 (&acc)[D / 16], const T* tt,
       for (int r = 0; r < 4; ++r) {
 #pragma unroll
         for (int db = 0; db < D / 16; ++db) {
-          float a = tt[(16 * db + c) * L::TR + 16 * b + 4 * g + r];
+          const float a = tile[(16 * b + 4 * g + r) * S + 16 * db + c];
           acc[db] = Mfma<float>::mma(a, v[b][r], acc[db]);
         }
       }
@@ -181,8 +264,8 @@ __device__ inline void acc_tr(f32x4 (&acc)[D / 16], const T* tt,
   }
 }
 
-// Sum over the 4 lanes that share a query/key column (xor 16, xor 32), in a
-// fixed order so every lane gets the same bits.
+// Sum over the 4 lanes that share a column (xor 16, xor 32), in a fixed
+// order so every lane gets the same bits.
 __device__ inline float col_sum(float x) {
   x = x + __shfl_xor(x, 16);
   return x + __shfl_xor(x, 32);

@@ -1,20 +1,19 @@
 // attn_kernels.hip -- gfx950 kernels of the causal GQA attention path.
 //
 // Forward  (GpuLoraEngine.Forward.cs:401-465 rope_batch + tune_attn_causal_gqa_fwd):
-//   kv_prep   K -> RoPE -> Kc (compute dtype, token-major) [+ k_rot out],
-//             V -> Vt (compute dtype, [Hkv][D][padded tokens]).
+//   rope_k    K -> RoPE -> k_rot (caller dtype) and/or a compute-dtype copy.
 //   attn_fwd  one workgroup = 64 queries of one head; 4 waves x 16 queries.
-//             Q is rotated in registers on load (q_rot written if asked),
-//             K and V^T tiles of 64 keys are staged in LDS and shared by the
-//             4 waves; online softmax in fp32 (exp2 domain); O and the row
+//             Q is rotated in registers on load (q_rot written if asked);
+//             rotated-K and V tiles of 64 keys are staged row-major in LDS
+//             (double-buffered, the next tile's global loads in flight while
+//             the current one is multiplied) and shared by the 4 waves;
+//             online softmax in fp32 (exp2 domain); O and the row
 //             log-sum-exp are written at the end.  No [S,S] matrix exists.
 // Backward (GpuLoraEngine.Backward.cs:354-412 dq_ds + dk_dv, :452 inverse rope):
-//   bwd_prep  D_i = dO_i . O_i, transposed copies Q^T, dO^T, K^T (and
-//             compute-dtype copies when the device tensors are fp32 and the
-//             matrix cores run bf16).
-//   attn_dq   one workgroup = 64 queries of one head: recomputes P from the
-//             saved lse, dS = P (dP - D), dQ = scale * dS K, inverse RoPE.
-//   attn_dkdv one workgroup = 64 keys of one (query head): dV_h = P^T dO,
+//   attn_dq   one workgroup = 64 queries of one head: D_i = dO_i . O_i
+//             (written for attn_dkdv), P recomputed from the saved lse,
+//             dS = P (dP - D), dQ = scale * dS K, inverse RoPE on the store.
+//   attn_dkdv one workgroup = 64 keys of one query head: dV_h = P^T dO,
 //             dK_h = scale * dS^T Q accumulated in registers over all query
 //             tiles, written as this head's partial (fp32).
 //   dkdv_reduce  dK/dV = sum of the partials over the heads of the KV group
@@ -25,6 +24,8 @@
 // recompute relies on that).
 #include "attn_common.hpp"
 #include "attn_launch.hpp"
+
+#include <type_traits>
 
 namespace glacier {
 
@@ -47,210 +48,165 @@ __device__ inline void rope_inv(float x0, float x1, float c, float s, float& y0,
   y1 = x1 * c - x0 * s;
 }
 
-__device__ inline void load8(const float* p, float (&x)[8]) {
-  float4 a = *reinterpret_cast<const float4*>(p);
-  float4 b = *reinterpret_cast<const float4*>(p + 4);
-  x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
-  x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
-}
-__device__ inline void load8(const bf16* p, float (&x)[8]) {
-  bf16x8 v = *reinterpret_cast<const bf16x8*>(p);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) x[i] = (float)v[i];
-}
-__device__ inline void store8(float* p, const float (&x)[8]) {
-  *reinterpret_cast<float4*>(p) = make_float4(x[0], x[1], x[2], x[3]);
-  *reinterpret_cast<float4*>(p + 4) = make_float4(x[4], x[5], x[6], x[7]);
-}
-__device__ inline void store8(bf16* p, const float (&x)[8]) {
-  bf16x8 v;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) v[i] = (bf16)x[i];
-  *reinterpret_cast<bf16x8*>(p) = v;
-}
-__device__ inline void store4(float* p, f32x4 v) {
-  *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
-}
-__device__ inline void store4(bf16* p, f32x4 v) {
-  bf16x4 b;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) b[i] = (bf16)v[i];
-  *reinterpret_cast<bf16x4*>(p) = b;
-}
-
-// Global (token-major) fragment of row `row` for k-step kk.
-template <typename T>
-__device__ inline typename Mfma<T>::Frag frag_global(const T* rowp, int kk, int g) {
-  using M = Mfma<T>;
-  const T* p = rowp + kk * M::KSTEP + M::KPL * g;
-  if constexpr (sizeof(T) == 2) {
-    return *reinterpret_cast<const bf16x8*>(p);
-  } else {
-    return *p;
-  }
-}
-
-template <typename T>
-__device__ inline typename Mfma<T>::Frag frag_zero() {
-  if constexpr (sizeof(T) == 2) {
-    bf16x8 z;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) z[i] = (bf16)0.0f;
-    return z;
-  } else {
-    return 0.0f;
-  }
-}
-
 // ---------------------------------------------------------------------------
-// Copy one [64 rows][D] block (rows r < nvalid of src, row stride gstride)
-// into a transposed destination dst[d * dstride + r] (64 columns, zeros for
-// r >= nvalid) and, if dst_rm is given, a row-major compute-dtype copy.
-// `lds` holds 64 * (D + 2) elements of T.
+// rope_k: one thread per (token, kv head, 8 rotation pairs).  Writes the
+// rotated K to k_rot (caller dtype) and/or kc (compute dtype), and, when vc
+// is given, a compute-dtype copy of V.
 // ---------------------------------------------------------------------------
 template <typename IO, typename T, int D>
-__device__ inline void transpose_block(const IO* src, long gstride, int nvalid,
-                                       T* dst_tr, long dstride, T* dst_rm,
-                                       long rm_stride, T* lds, int tid) {
-  constexpr int LS = D + 2;
-  // phase 1: rows -> LDS (8 consecutive elements per thread and step)
-  constexpr int CPR = D / 8;
-  for (int idx = tid; idx < kTile * CPR; idx += kThreads) {
-    int r = idx / CPR, ch = idx % CPR;
-    float x[8];
-    if (r < nvalid) {
-      load8(src + (long)r * gstride + ch * 8, x);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) x[e] = 0.0f;
-    }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) lds[r * LS + ch * 8 + e] = from_f32<T>(x[e]);
-    if (dst_rm != nullptr && r < nvalid) store8(dst_rm + (long)r * rm_stride + ch * 8, x);
-  }
-  __syncthreads();
-  // phase 2: LDS columns -> transposed rows (16-byte chunks)
-  constexpr int CE = 16 / sizeof(T);
-  constexpr int CPT = kTile / CE;
-  for (int idx = tid; idx < D * CPT; idx += kThreads) {
-    int d = idx / CPT, ch = idx % CPT;
-    union {
-      uint4 u;
-      T e[CE];
-    } pk;
-#pragma unroll
-    for (int e = 0; e < CE; ++e) pk.e[e] = lds[(ch * CE + e) * LS + d];
-    *reinterpret_cast<uint4*>(dst_tr + (long)d * dstride + ch * CE) = pk.u;
-  }
-}
-
-// ---------------------------------------------------------------------------
-// kv_prep: grid (Hkv, ntiles).
-// ---------------------------------------------------------------------------
-template <typename IO, typename T, int D>
-__global__ __launch_bounds__(kThreads) void kv_prep_kernel(
-    const IO* __restrict__ k, const IO* __restrict__ v, T* __restrict__ kc,
-    IO* __restrict__ k_rot, T* __restrict__ vt, const TileDesc* __restrict__ tiles,
-    int n_heads_kv, int ptot, const float* __restrict__ cos_t,
-    const float* __restrict__ sin_t) {
-  __shared__ T lds[kTile * (D + 2)];
-  const int j = blockIdx.x;
-  const TileDesc td = tiles[blockIdx.y];
-  const int tid = threadIdx.x;
-  const int row0 = kTile * td.tile;
-  const int nvalid = min(kTile, td.len - row0);
+__global__ __launch_bounds__(kThreads) void rope_k_kernel(
+    const IO* __restrict__ k, IO* __restrict__ k_rot, T* __restrict__ kc,
+    const IO* __restrict__ v, T* __restrict__ vc,
+    const int32_t* __restrict__ pos_of, int total_tokens, int n_heads_kv,
+    const float* __restrict__ cos_t, const float* __restrict__ sin_t) {
   constexpr int H = D / 2;
-  // K: rotate each pair (p, p + D/2) of each valid row.
-  for (int idx = tid; idx < kTile * H; idx += kThreads) {
-    int r = idx / H, p = idx % H;
-    if (r >= nvalid) continue;
-    int pos = row0 + r;
-    long base = ((long)(td.tok0 + pos) * n_heads_kv + j) * D;
-    float x0 = to_f32(k[base + p]), x1 = to_f32(k[base + p + H]);
-    float c = cos_t[(long)pos * H + p], s = sin_t[(long)pos * H + p];
-    float y0, y1;
-    rope_fwd(x0, x1, c, s, y0, y1);
-    kc[base + p] = from_f32<T>(y0);
-    kc[base + p + H] = from_f32<T>(y1);
-    if (k_rot != nullptr) {
-      k_rot[base + p] = from_f32<IO>(y0);
-      k_rot[base + p + H] = from_f32<IO>(y1);
-    }
+  constexpr int CH = H / 8;  // 8-pair chunks per head
+  const long idx = (long)blockIdx.x * kThreads + threadIdx.x;
+  if (idx >= (long)total_tokens * n_heads_kv * CH) return;
+  const int p0 = 8 * (int)(idx % CH);
+  const long th = idx / CH;  // token * Hkv + head
+  const long tok = th / n_heads_kv;
+  const long base = th * D + p0;
+  const long ti = (long)pos_of[tok] * H + p0;
+  float x0[8], x1[8], c[8], s[8], y0[8], y1[8];
+  load8(k + base, x0);
+  load8(k + base + H, x1);
+  load8(cos_t + ti, c);
+  load8(sin_t + ti, s);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) rope_fwd(x0[e], x1[e], c[e], s[e], y0[e], y1[e]);
+  if (k_rot != nullptr) {
+    store8(k_rot + base, y0);
+    store8(k_rot + base + H, y1);
   }
-  // V -> V^T (zero columns past the sequence end)
-  transpose_block<IO, T, D>(v + ((long)td.tok0 * n_heads_kv + j) * D + (long)row0 * n_heads_kv * D,
-                            (long)n_heads_kv * D, nvalid,
-                            vt + (long)j * D * ptot + td.ptok0 + row0, ptot,
-                            nullptr, 0, lds, tid);
+  if (kc != nullptr) {
+    store8(kc + base, y0);
+    store8(kc + base + H, y1);
+  }
+  if (vc != nullptr) {
+    load8(v + base, x0);
+    load8(v + base + H, x1);
+    store8(vc + base, x0);
+    store8(vc + base + H, x1);
+  }
 }
 
 // ---------------------------------------------------------------------------
-// attn_fwd: grid (Hq, ntiles), 256 threads, dynamic LDS = K tile + V^T tile.
+// attn_fwd: grid (Hq, ntiles), 256 * G threads.  G key groups split a query
+// tile's key tiles (group grp takes tiles grp, grp + G, ...): 2 in the bf16
+// mode, so two waves share each SIMD and one's softmax arithmetic overlaps
+// the other's matrix products; 1 in the fp32 mode (its tiles are twice as
+// large).  Each group double-buffers its own K and V tiles in LDS; the
+// groups' partial (max, sum, O) are merged through LDS at the end in a fixed
+// order.  kc: rotated K in the compute dtype T; v: V in the caller's dtype.
+// tiles == nullptr means one sequence of total_tokens tokens (the tile order
+// is then computed, longest first, instead of read).
 // ---------------------------------------------------------------------------
+template <typename T>
+constexpr int fwd_groups() {
+  return sizeof(T) == 2 ? 2 : 1;
+}
+
+// Lazy rescaling: the running max used for exp2 moves only when a tile's max
+// exceeds it by more than this (log2 units), so P stays <= 2^8 and O is
+// rescaled only a few times per row instead of once per tile.
+constexpr float kRescaleTau = 8.0f;
+
 template <typename IO, typename T, int D>
-__global__ __launch_bounds__(kThreads) void attn_fwd_kernel(
-    const IO* __restrict__ q, const T* __restrict__ kc, const T* __restrict__ vt,
+__global__ __launch_bounds__(kThreads * fwd_groups<T>()) void attn_fwd_kernel(
+    const IO* __restrict__ q, const T* __restrict__ kc, const IO* __restrict__ v,
     IO* __restrict__ out, float* __restrict__ lse, IO* __restrict__ q_rot,
-    const TileDesc* __restrict__ tiles, int n_heads_q, int n_heads_kv,
-    int total_tokens, int ptot, float scale_log2, const float* __restrict__ cos_t,
+    const TileDesc* __restrict__ tiles, int n_tiles, int n_heads_q, int n_heads_kv,
+    int total_tokens, float scale_log2, const float* __restrict__ cos_t,
     const float* __restrict__ sin_t) {
   using M = Mfma<T>;
   using L = Lds<T, D>;
+  constexpr int G = fwd_groups<T>();
   constexpr int NKD = D / M::KSTEP;
   constexpr int H = D / 2;
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  T* ks = reinterpret_cast<T*>(smem_raw);
-  T* vts = ks + L::RM_ELEMS;
+  T* const lds = reinterpret_cast<T*>(smem_raw);  // [G][2 buffers][K tile, V tile]
 
   const int h = blockIdx.x;
-  const TileDesc td = tiles[blockIdx.y];
+  const TileDesc td = tiles != nullptr
+                          ? tiles[blockIdx.y]
+                          : TileDesc{0, total_tokens, n_tiles - 1 - (int)blockIdx.y, 0};
   const int kvh = h / (n_heads_q / n_heads_kv);
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int grp = w >> 2, wq = w & 3, gtid = tid & (kThreads - 1);
   const int g = lane >> 4, c = lane & 15;
-  const int qrow = kTile * td.tile + 16 * w + c;
+  const int qrow = kTile * td.tile + 16 * wq + c;
   const bool qvalid = qrow < td.len;
   const long qbase = ((long)(td.tok0 + qrow) * n_heads_q + h) * D;
+  T* const glds = lds + grp * 4 * L::TILE;  // this group's two buffers
 
-  // Q fragments, rotated in fp32 then rounded to the compute dtype.
+  // Start this group's first K/V tile loads before the Q prologue.
+  const long kvstride = (long)n_heads_kv * D;
+  const T* kbase = kc + ((long)td.tok0 * n_heads_kv + kvh) * D;
+  const IO* vbase = v + ((long)td.tok0 * n_heads_kv + kvh) * D;
+  TileRegs<T, D> kreg;
+  TileRegs<IO, D> vreg;
+  if (grp <= td.tile) {
+    const long roff = (long)kTile * grp * kvstride;
+    kreg.load(kbase + roff, kvstride, td.len - kTile * grp, gtid);
+    vreg.load(vbase + roff, kvstride, td.len - kTile * grp, gtid);
+  }
+
+  // Q fragments, rotated in fp32 then rounded to the compute dtype.  Group 0
+  // rotates (and writes q_rot); with two groups it hands the fragments to
+  // group 1 through LDS, lane for lane, so Q and the cos/sin rows are read
+  // from memory once per workgroup.
   typename M::Frag qf[NKD];
+  if (grp == 0) {
 #pragma unroll
-  for (int kk = 0; kk < NKD / 2; ++kk) {
-    if constexpr (sizeof(T) == 2) {
-      const int d0 = kk * M::KSTEP + 8 * g;
-      float x0[8], x1[8], y0[8], y1[8];
-      if (qvalid) {
-        load8(q + qbase + d0, x0);
-        load8(q + qbase + d0 + H, x1);
+    for (int kk = 0; kk < NKD / 2; ++kk) {
+      if constexpr (sizeof(T) == 2) {
+        const int d0 = kk * M::KSTEP + 8 * g;
+        float x0[8], x1[8], y0[8], y1[8], cs[8], sn[8];
+        if (qvalid) {
+          load8(q + qbase + d0, x0);
+          load8(q + qbase + d0 + H, x1);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) x0[e] = x1[e] = 0.0f;
+        }
+        const long ti = (long)(qvalid ? qrow : 0) * H + d0;
+        load8(cos_t + ti, cs);
+        load8(sin_t + ti, sn);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          rope_fwd(x0[e], x1[e], cs[e], sn[e], y0[e], y1[e]);
+          qf[kk][e] = (bf16)y0[e];
+          qf[kk + NKD / 2][e] = (bf16)y1[e];
+        }
+        if (q_rot != nullptr && qvalid) {
+          store8(q_rot + qbase + d0, y0);
+          store8(q_rot + qbase + d0 + H, y1);
+        }
       } else {
+        const int d0 = kk * M::KSTEP + g;
+        float x0 = 0.0f, x1 = 0.0f, y0, y1;
+        if (qvalid) {
+          x0 = to_f32(q[qbase + d0]);
+          x1 = to_f32(q[qbase + d0 + H]);
+        }
+        const long ti = (long)(qvalid ? qrow : 0) * H + d0;
+        rope_fwd(x0, x1, cos_t[ti], sin_t[ti], y0, y1);
+        qf[kk] = y0;
+        qf[kk + NKD / 2] = y1;
+        if (q_rot != nullptr && qvalid) {
+          q_rot[qbase + d0] = from_f32<IO>(y0);
+          q_rot[qbase + d0 + H] = from_f32<IO>(y1);
+        }
+      }
+    }
+  }
+  typename M::Frag* const qlds =
+      reinterpret_cast<typename M::Frag*>(lds + 4 * G * L::TILE) + wq * NKD * 64 + lane;
+  if constexpr (G == 2) {
+    if (grp == 0) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) x0[e] = x1[e] = 0.0f;
-      }
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const long ti = (long)(qvalid ? qrow : 0) * H + d0 + e;
-        rope_fwd(x0[e], x1[e], cos_t[ti], sin_t[ti], y0[e], y1[e]);
-        qf[kk][e] = (bf16)y0[e];
-        qf[kk + NKD / 2][e] = (bf16)y1[e];
-      }
-      if (q_rot != nullptr && qvalid) {
-        store8(q_rot + qbase + d0, y0);
-        store8(q_rot + qbase + d0 + H, y1);
-      }
-    } else {
-      const int d0 = kk * M::KSTEP + g;
-      float x0 = 0.0f, x1 = 0.0f, y0, y1;
-      if (qvalid) {
-        x0 = to_f32(q[qbase + d0]);
-        x1 = to_f32(q[qbase + d0 + H]);
-      }
-      const long ti = (long)(qvalid ? qrow : 0) * H + d0;
-      rope_fwd(x0, x1, cos_t[ti], sin_t[ti], y0, y1);
-      qf[kk] = y0;
-      qf[kk + NKD / 2] = y1;
-      if (q_rot != nullptr && qvalid) {
-        q_rot[qbase + d0] = from_f32<IO>(y0);
-        q_rot[qbase + d0 + H] = from_f32<IO>(y1);
-      }
+      for (int kk = 0; kk < NKD; ++kk) qlds[kk * 64] = qf[kk];
     }
   }
 
@@ -259,17 +215,12 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(
   for (int db = 0; db < D / 16; ++db) o[db] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   float m_run = kNegBig, l_lane = 0.0f;
 
-  const T* kbase = kc + ((long)td.tok0 * n_heads_kv + kvh) * D;
-  const T* vtbase = vt + (long)kvh * D * ptot + td.ptok0;
-  for (int kt = 0; kt <= td.tile; ++kt) {
-    __syncthreads();
-    stage_rm<T, D>(ks, kbase + (long)kTile * kt * n_heads_kv * D,
-                   (long)n_heads_kv * D, td.len - kTile * kt, tid);
-    stage_tr<T, D>(vts, vtbase + kTile * kt, ptot, tid);
-    __syncthreads();
-
-    const int nb = (kt == td.tile) ? (w + 1) : 4;
-    float p[4][4];
+  // One key tile: scores, online softmax, O^T += V^T P^T.  DIAG: the tile
+  // that holds the queries themselves (causal mask inside it).
+  auto step = [&](const T* ks, const T* vs, auto diag) {
+    constexpr bool DIAG = decltype(diag)::value;
+    const int nb = DIAG ? (wq + 1) : 4;
+    float sc[4][4];
     float mloc = -INFINITY;
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
@@ -281,28 +232,94 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int key = kTile * kt + 16 * b + 4 * g + r;
-        const float t = (b < nb && key <= qrow) ? acc[r] * scale_log2 : -INFINITY;
-        p[b][r] = t;
-        mloc = fmaxf(mloc, t);
+        float x = acc[r];
+        if (DIAG) x = (b < nb && 16 * b + 4 * g + r <= 16 * wq + c) ? x : -INFINITY;
+        sc[b][r] = x;
+        mloc = fmaxf(mloc, x);
       }
     }
-    mloc = col_max(mloc);
-    const float m_new = fmaxf(m_run, mloc);
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+    const float m_tile = col_max(mloc) * scale_log2;
+    if (__builtin_amdgcn_ballot_w64(m_tile > m_run + kRescaleTau) != 0) {
+      const float m_new = fmaxf(m_run, m_tile);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      l_lane *= alpha;
+#pragma unroll
+      for (int db = 0; db < D / 16; ++db) o[db] *= alpha;
+      m_run = m_new;
+    }
+    float p[4][4];
     float psum = 0.0f;
 #pragma unroll
     for (int b = 0; b < 4; ++b)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        p[b][r] = __builtin_amdgcn_exp2f(p[b][r] - m_new);
+        p[b][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[b][r], scale_log2, -m_run));
         psum += p[b][r];
       }
-    l_lane = l_lane * alpha + psum;
-    m_run = m_new;
+    l_lane += psum;
+    acc_rows<T, D>(o, vs, p, nb, lane);
+  };
+
+  if (grp <= td.tile) {
+    kreg.store(glds, gtid);
+    vreg.store(glds + L::TILE, gtid);
+  }
+  __syncthreads();
+  if constexpr (G == 2) {
+    if (grp == 1) {
 #pragma unroll
-    for (int db = 0; db < D / 16; ++db) o[db] *= alpha;
-    acc_tr<T, D>(o, vts, p, nb, lane);
+      for (int kk = 0; kk < NKD; ++kk) qf[kk] = qlds[kk * 64];
+    }
+  }
+
+  const int nit = (td.tile + G) / G;  // iterations of group 0 (the most)
+  for (int it = 0; it < nit; ++it) {
+    const int kt = grp + G * it;
+    const T* ks = glds + (it & 1) * 2 * L::TILE;
+    const bool more = kt + G <= td.tile;
+    if (more) {  // prefetch this group's next tile into registers
+      const long roff = (long)kTile * (kt + G) * kvstride;
+      const int nv = td.len - kTile * (kt + G);
+      kreg.load(kbase + roff, kvstride, nv, gtid);
+      vreg.load(vbase + roff, kvstride, nv, gtid);
+    }
+    if (kt < td.tile)
+      step(ks, ks + L::TILE, std::false_type{});
+    else if (kt == td.tile)
+      step(ks, ks + L::TILE, std::true_type{});
+    if (more) {
+      T* nxt = glds + ((it + 1) & 1) * 2 * L::TILE;
+      kreg.store(nxt, gtid);
+      vreg.store(nxt + L::TILE, gtid);
+    }
+    __syncthreads();
+  }
+
+  if constexpr (G == 2) {
+    // Merge group 1's partial row state into group 0 (lane for lane: waves
+    // wq and wq + 4 own the same queries with the same lane layout).
+    constexpr int NF = D / 4 + 2;  // floats per lane: O, max, sum
+    float* cmb = reinterpret_cast<float*>(lds + 4 * L::TILE) + wq * NF * 64 + lane;
+    if (grp == 1) {
+      cmb[0] = m_run;
+      cmb[64] = l_lane;
+#pragma unroll
+      for (int db = 0; db < D / 16; ++db)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) cmb[(2 + 4 * db + r) * 64] = o[db][r];
+    }
+    __syncthreads();
+    if (grp == 1) return;
+    const float m1 = cmb[0], l1 = cmb[64];
+    const float m_new = fmaxf(m_run, m1);
+    const float a0 = __builtin_amdgcn_exp2f(m_run - m_new);
+    const float a1 = __builtin_amdgcn_exp2f(m1 - m_new);
+    l_lane = l_lane * a0 + l1 * a1;
+#pragma unroll
+    for (int db = 0; db < D / 16; ++db)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o[db][r] = o[db][r] * a0 + cmb[(2 + 4 * db + r) * 64] * a1;
+    m_run = m_new;
   }
 
   const float l_tot = col_sum(l_lane);
@@ -317,150 +334,429 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// bwd_prep: grid (Hq + Hkv, ntiles).
+// attn_fwd, bf16 matrix cores: grid (Hq, ntiles), 512 threads = 4 key groups
+// x 2 waves.  Each wave owns 32 queries (two 16-query MFMA column blocks), so
+// every K and V fragment read from LDS feeds two MFMAs; group grp takes the
+// key tiles grp, grp + 4, ... of the query tile into its own single LDS
+// buffer (the next tile's global loads are in registers while the current
+// one is multiplied).  Group 0 rotates Q and hands the fragments to the other
+// groups through LDS; the four partial (max, sum, O) are merged in group
+// order at the end.
 // ---------------------------------------------------------------------------
-template <typename IO, typename T, int D>
-__global__ __launch_bounds__(kThreads) void bwd_prep_kernel(
-    const IO* __restrict__ d_out, const IO* __restrict__ out,
-    const IO* __restrict__ q_rot, const IO* __restrict__ k_rot,
-    const IO* __restrict__ v, float* __restrict__ dvec, T* __restrict__ dot_t,
-    T* __restrict__ qt, T* __restrict__ kt, T* __restrict__ doc,
-    T* __restrict__ qc, T* __restrict__ kc, T* __restrict__ vc,
-    const TileDesc* __restrict__ tiles, int n_heads_q, int n_heads_kv,
-    int total_tokens, int ptot) {
-  __shared__ T lds[kTile * (D + 2)];
-  const int y = blockIdx.x;
-  const TileDesc td = tiles[blockIdx.y];
-  const int tid = threadIdx.x;
-  const int row0 = kTile * td.tile;
-  const int nvalid = min(kTile, td.len - row0);
-  if (y < n_heads_q) {
-    const int h = y;
-    const long off = ((long)(td.tok0 + row0) * n_heads_q + h) * D;
-    const long gs = (long)n_heads_q * D;
-    // D_i = sum_d dO_i[d] * O_i[d]: 4 threads per row, fixed combine order.
-    {
-      const int r = tid >> 2, part = tid & 3;
-      float acc = 0.0f;
-      if (r < nvalid) {
-        const IO* a = d_out + off + (long)r * gs + part * (D / 4);
-        const IO* b = out + off + (long)r * gs + part * (D / 4);
-        for (int d = 0; d < D / 4; d += 8) {
-          float xa[8], xb[8];
-          load8(a + d, xa);
-          load8(b + d, xb);
+constexpr int kFwdGroups = 4;
+constexpr int kFwdThreads = 512;
+
+template <int D>
+constexpr size_t fwd_bf16_lds() {
+  // one K + V tile per group, then group 0's Q fragments (64 queries x D)
+  return sizeof(bf16) * (2 * kFwdGroups * Lds<bf16, D>::TILE + kTile * D);
+}
+
+template <typename IO, int D>
+__global__ __launch_bounds__(kFwdThreads) void attn_fwd_bf16_kernel(
+    const IO* __restrict__ q, const bf16* __restrict__ kc, const bf16* __restrict__ v,
+    IO* __restrict__ out, float* __restrict__ lse, IO* __restrict__ q_rot,
+    const TileDesc* __restrict__ tiles, int n_tiles, int n_heads_q, int n_heads_kv,
+    int total_tokens, float scale_log2, const float* __restrict__ cos_t,
+    const float* __restrict__ sin_t) {
+  using M = Mfma<bf16>;
+  using L = Lds<bf16, D>;
+  using Frag = M::Frag;
+  constexpr int G = kFwdGroups;
+  constexpr int GT = kFwdThreads / G;  // threads per group (2 waves)
+  constexpr int QB = 2;                // 16-query blocks per wave
+  constexpr int NKD = D / M::KSTEP;
+  constexpr int H = D / 2;
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  bf16* const lds = reinterpret_cast<bf16*>(smem_raw);  // [G][K tile, V tile], Q frags
+
+  const int h = blockIdx.x;
+  const TileDesc td = tiles != nullptr
+                          ? tiles[blockIdx.y]
+                          : TileDesc{0, total_tokens, n_tiles - 1 - (int)blockIdx.y, 0};
+  const int kvh = h / (n_heads_q / n_heads_kv);
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int grp = w >> 1, qh = w & 1, gtid = tid & (GT - 1);
+  const int g = lane >> 4, c = lane & 15;
+  bf16* const glds = lds + grp * 2 * L::TILE;
+
+  // Start this group's first K/V tile loads before the Q prologue.
+  const long kvstride = (long)n_heads_kv * D;
+  const bf16* kbase = kc + ((long)td.tok0 * n_heads_kv + kvh) * D;
+  const bf16* vbase = v + ((long)td.tok0 * n_heads_kv + kvh) * D;
+  TileRegs<bf16, D, GT> kreg, vreg;
+  if (grp <= td.tile) {
+    const long roff = (long)kTile * grp * kvstride;
+    kreg.load(kbase + roff, kvstride, td.len - kTile * grp, gtid);
+    vreg.load(vbase + roff, kvstride, td.len - kTile * grp, gtid);
+  }
+
+  // Q fragments of the wave's two query blocks, rotated in fp32 (group 0).
+  Frag qf[QB][NKD];
+  Frag* const qlds = reinterpret_cast<Frag*>(lds + 2 * G * L::TILE) + qh * QB * NKD * 64 + lane;
+  if (grp == 0) {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) acc += xa[e] * xb[e];
+    for (int qb = 0; qb < QB; ++qb) {
+      const int qrow = kTile * td.tile + 32 * qh + 16 * qb + c;
+      const bool qvalid = qrow < td.len;
+      const long qbase = ((long)(td.tok0 + qrow) * n_heads_q + h) * D;
+#pragma unroll
+      for (int kk = 0; kk < NKD / 2; ++kk) {
+        const int d0 = kk * M::KSTEP + 8 * g;
+        float x0[8], x1[8], y0[8], y1[8], cs[8], sn[8];
+        if (qvalid) {
+          load8(q + qbase + d0, x0);
+          load8(q + qbase + d0 + H, x1);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) x0[e] = x1[e] = 0.0f;
+        }
+        const long ti = (long)(qvalid ? qrow : 0) * H + d0;
+        load8(cos_t + ti, cs);
+        load8(sin_t + ti, sn);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          rope_fwd(x0[e], x1[e], cs[e], sn[e], y0[e], y1[e]);
+          qf[qb][kk][e] = (bf16)y0[e];
+          qf[qb][kk + NKD / 2][e] = (bf16)y1[e];
+        }
+        if (q_rot != nullptr && qvalid) {
+          store8(q_rot + qbase + d0, y0);
+          store8(q_rot + qbase + d0 + H, y1);
         }
       }
-      acc += __shfl_xor(acc, 1);
-      acc += __shfl_xor(acc, 2);
-      if (r < nvalid && part == 0)
-        dvec[(long)h * total_tokens + td.tok0 + row0 + r] = acc;
+#pragma unroll
+      for (int kk = 0; kk < NKD; ++kk) qlds[(qb * NKD + kk) * 64] = qf[qb][kk];
     }
-    transpose_block<IO, T, D>(d_out + off, gs, nvalid,
-                              dot_t + (long)h * D * ptot + td.ptok0 + row0, ptot,
-                              doc != nullptr ? doc + off : nullptr, gs, lds, tid);
-    __syncthreads();
-    transpose_block<IO, T, D>(q_rot + off, gs, nvalid,
-                              qt + (long)h * D * ptot + td.ptok0 + row0, ptot,
-                              qc != nullptr ? qc + off : nullptr, gs, lds, tid);
-  } else {
-    const int j = y - n_heads_q;
-    const long off = ((long)(td.tok0 + row0) * n_heads_kv + j) * D;
-    const long gs = (long)n_heads_kv * D;
-    transpose_block<IO, T, D>(k_rot + off, gs, nvalid,
-                              kt + (long)j * D * ptot + td.ptok0 + row0, ptot,
-                              kc != nullptr ? kc + off : nullptr, gs, lds, tid);
-    if (vc != nullptr) {
-      constexpr int CPR = D / 8;
-      for (int idx = tid; idx < kTile * CPR; idx += kThreads) {
-        int r = idx / CPR, ch = idx % CPR;
-        if (r >= nvalid) continue;
-        float x[8];
-        load8(v + off + (long)r * gs + ch * 8, x);
-        store8(vc + off + (long)r * gs + ch * 8, x);
+  }
+
+  f32x4 o[QB][D / 16];
+  float m_run[QB], l_lane[QB];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+#pragma unroll
+    for (int db = 0; db < D / 16; ++db) o[qb][db] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    m_run[qb] = kNegBig;
+    l_lane[qb] = 0.0f;
+  }
+
+  // One key tile.  DIAG: the tile holding the queries (causal mask inside);
+  // there the wave needs key blocks b <= 2*qh + 1 only.
+  auto step = [&](const bf16* ks, const bf16* vs, auto diag) {
+    constexpr bool DIAG = decltype(diag)::value;
+    float sc[QB][4][4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      f32x4 acc[QB];
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) acc[qb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      if (!DIAG || b <= 2 * qh + 1) {
+#pragma unroll
+        for (int kk = 0; kk < NKD; ++kk) {
+          const Frag kf = frag_rm<bf16, D>(ks, 16 * b + c, kk, g);
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb) acc[qb] = M::mma(kf, qf[qb][kk], acc[qb]);
+        }
       }
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float x = acc[qb][r];
+          if (DIAG) x = (16 * b + 4 * g + r <= 32 * qh + 16 * qb + c) ? x : -INFINITY;
+          sc[qb][b][r] = x;
+        }
+    }
+    float p[QB][4][4];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      float mloc = -INFINITY;
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) mloc = fmaxf(mloc, sc[qb][b][r]);
+      const float m_tile = col_max(mloc) * scale_log2;
+      if (__builtin_amdgcn_ballot_w64(m_tile > m_run[qb] + kRescaleTau) != 0) {
+        const float m_new = fmaxf(m_run[qb], m_tile);
+        const float alpha = __builtin_amdgcn_exp2f(m_run[qb] - m_new);
+        l_lane[qb] *= alpha;
+#pragma unroll
+        for (int db = 0; db < D / 16; ++db) o[qb][db] *= alpha;
+        m_run[qb] = m_new;
+      }
+      float psum = 0.0f;
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          p[qb][b][r] =
+              __builtin_amdgcn_exp2f(__builtin_fmaf(sc[qb][b][r], scale_log2, -m_run[qb]));
+          psum += p[qb][b][r];
+        }
+      l_lane[qb] += psum;
+    }
+    // O^T += V^T P^T: each V^T fragment (transpose read) feeds both blocks.
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) {
+      if (DIAG && s2 > qh) break;
+      Frag pf[QB];
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          pf[qb][r] = (bf16)p[qb][2 * s2][r];
+          pf[qb][4 + r] = (bf16)p[qb][2 * s2 + 1][r];
+        }
+#pragma unroll
+      for (int db = 0; db < D / 16; ++db) {
+        const bf16x4 lo = read_tr<L::STRIDE>(vs, 32 * s2, 16 * db, lane);
+        const bf16x4 hi = read_tr<L::STRIDE>(vs, 32 * s2 + 16, 16 * db, lane);
+        Frag a;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          a[r] = lo[r];
+          a[4 + r] = hi[r];
+        }
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) o[qb][db] = M::mma(a, pf[qb], o[qb][db]);
+      }
+    }
+  };
+
+  if (grp <= td.tile) {
+    kreg.store(glds, gtid);
+    vreg.store(glds + L::TILE, gtid);
+  }
+  __syncthreads();
+  if (grp != 0) {
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+      for (int kk = 0; kk < NKD; ++kk) qf[qb][kk] = qlds[(qb * NKD + kk) * 64];
+  }
+
+  const int nit = (td.tile + G) / G;  // iterations of group 0 (the most)
+  for (int it = 0; it < nit; ++it) {
+    const int kt = grp + G * it;
+    const bool more = kt + G <= td.tile;
+    if (more) {  // prefetch this group's next tile into registers
+      const long roff = (long)kTile * (kt + G) * kvstride;
+      const int nv = td.len - kTile * (kt + G);
+      kreg.load(kbase + roff, kvstride, nv, gtid);
+      vreg.load(vbase + roff, kvstride, nv, gtid);
+    }
+    if (kt < td.tile)
+      step(glds, glds + L::TILE, std::false_type{});
+    else if (kt == td.tile)
+      step(glds, glds + L::TILE, std::true_type{});
+    if (it + 1 < nit) {
+      __syncthreads();
+      if (more) {
+        kreg.store(glds, gtid);
+        vreg.store(glds + L::TILE, gtid);
+      }
+      __syncthreads();
+    }
+  }
+
+  // Merge groups 1..3 into group 0, in group order, lane for lane (waves
+  // (grp, qh) all own the same queries with the same lane layout).
+  constexpr int NF = QB * (D / 4 + 2);  // floats per lane: per block O, max, sum
+  __syncthreads();
+  float* const cmb = reinterpret_cast<float*>(smem_raw) + qh * NF * 64 + lane;
+  constexpr int GSTRIDE = 2 * NF * 64;  // floats per group
+  if (grp != 0) {
+    float* dst = cmb + (grp - 1) * GSTRIDE;
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      float* d = dst + qb * (D / 4 + 2) * 64;
+      d[0] = m_run[qb];
+      d[64] = l_lane[qb];
+#pragma unroll
+      for (int db = 0; db < D / 16; ++db)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) d[(2 + 4 * db + r) * 64] = o[qb][db][r];
+    }
+  }
+  __syncthreads();
+  if (grp != 0) return;
+#pragma unroll
+  for (int src = 0; src < G - 1; ++src) {
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      const float* d = cmb + src * GSTRIDE + qb * (D / 4 + 2) * 64;
+      const float m1 = d[0], l1 = d[64];
+      const float m_new = fmaxf(m_run[qb], m1);
+      const float a0 = __builtin_amdgcn_exp2f(m_run[qb] - m_new);
+      const float a1 = __builtin_amdgcn_exp2f(m1 - m_new);
+      l_lane[qb] = l_lane[qb] * a0 + l1 * a1;
+#pragma unroll
+      for (int db = 0; db < D / 16; ++db)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          o[qb][db][r] = o[qb][db][r] * a0 + d[(2 + 4 * db + r) * 64] * a1;
+      m_run[qb] = m_new;
+    }
+  }
+
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    const int qrow = kTile * td.tile + 32 * qh + 16 * qb + c;
+    const long qbase = ((long)(td.tok0 + qrow) * n_heads_q + h) * D;
+    const float l_tot = col_sum(l_lane[qb]);
+    const float inv = 1.0f / l_tot;
+    if (qrow < td.len) {
+#pragma unroll
+      for (int db = 0; db < D / 16; ++db)
+        store4(out + qbase + 16 * db + 4 * g, o[qb][db] * inv);
+      if (lse != nullptr && g == 0)
+        lse[(long)h * total_tokens + td.tok0 + qrow] = (m_run[qb] + log2f(l_tot)) * kLn2;
     }
   }
 }
 
 // ---------------------------------------------------------------------------
-// attn_dq: grid (Hq, ntiles), dynamic LDS = K tile + V tile + K^T tile.
+// attn_dq: grid (Hq, ntiles), 256 * G threads; G key groups split the query
+// tile's key tiles like attn_fwd and their dQ partials are summed in a fixed
+// order (group 0 + group 1).  Also writes dvec = D_i = dO_i . O_i for
+// attn_dkdv.  tiles == nullptr: one sequence, longest tiles first.
 // ---------------------------------------------------------------------------
+template <typename T>
+constexpr int bwd_groups() {
+  return sizeof(T) == 2 ? 2 : 1;
+}
+
 template <typename IO, typename T, int D>
-__global__ __launch_bounds__(kThreads) void attn_dq_kernel(
-    const T* __restrict__ qsrc, const T* __restrict__ dosrc,
-    const T* __restrict__ ksrc, const T* __restrict__ vsrc,
-    const T* __restrict__ kt_g, const float* __restrict__ lse,
-    const float* __restrict__ dvec, IO* __restrict__ dq,
-    const TileDesc* __restrict__ tiles, int n_heads_q, int n_heads_kv,
-    int total_tokens, int ptot, float scale_log2, float scale,
+__global__ __launch_bounds__(kThreads * bwd_groups<T>()) void attn_dq_kernel(
+    const IO* __restrict__ q_rot, const IO* __restrict__ d_out,
+    const IO* __restrict__ out, const IO* __restrict__ k_rot,
+    const IO* __restrict__ v, const float* __restrict__ lse,
+    float* __restrict__ dvec, IO* __restrict__ dq,
+    const TileDesc* __restrict__ tiles, int n_tiles, int n_heads_q, int n_heads_kv,
+    int total_tokens, float scale_log2, float scale,
     const float* __restrict__ cos_t, const float* __restrict__ sin_t) {
   using M = Mfma<T>;
   using L = Lds<T, D>;
+  constexpr int G = bwd_groups<T>();
   constexpr int NKD = D / M::KSTEP;
   constexpr int H = D / 2;
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  T* ks = reinterpret_cast<T*>(smem_raw);
-  T* vs = ks + L::RM_ELEMS;
-  T* kts = vs + L::RM_ELEMS;
+  T* const lds = reinterpret_cast<T*>(smem_raw);  // [G][2 buffers][K tile, V tile]
 
   const int h = blockIdx.x;
-  const TileDesc td = tiles[blockIdx.y];
+  const TileDesc td = tiles != nullptr
+                          ? tiles[blockIdx.y]
+                          : TileDesc{0, total_tokens, n_tiles - 1 - (int)blockIdx.y, 0};
   const int kvh = h / (n_heads_q / n_heads_kv);
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int grp = w >> 2, wq = w & 3, gtid = tid & (kThreads - 1);
   const int g = lane >> 4, c = lane & 15;
-  const int qrow = kTile * td.tile + 16 * w + c;
+  const int qrow = kTile * td.tile + 16 * wq + c;
   const bool qvalid = qrow < td.len;
   const long qbase = ((long)(td.tok0 + qrow) * n_heads_q + h) * D;
+  T* const glds = lds + grp * 4 * L::TILE;
+
+  const long kvstride = (long)n_heads_kv * D;
+  const IO* kbase = k_rot + ((long)td.tok0 * n_heads_kv + kvh) * D;
+  const IO* vbase = v + ((long)td.tok0 * n_heads_kv + kvh) * D;
+  TileRegs<IO, D> kreg, vreg;
+  if (grp <= td.tile) {
+    const long roff = (long)kTile * grp * kvstride;
+    kreg.load(kbase + roff, kvstride, td.len - kTile * grp, gtid);
+    vreg.load(vbase + roff, kvstride, td.len - kTile * grp, gtid);
+  }
 
   typename M::Frag qf[NKD], df[NKD];
+  float dot = 0.0f;
 #pragma unroll
   for (int kk = 0; kk < NKD; ++kk) {
-    qf[kk] = qvalid ? frag_global<T>(qsrc + qbase, kk, g) : frag_zero<T>();
-    df[kk] = qvalid ? frag_global<T>(dosrc + qbase, kk, g) : frag_zero<T>();
+    qf[kk] = qvalid ? frag_global<T>(q_rot + qbase, kk, g) : frag_zero<T>();
+    df[kk] = qvalid ? frag_global<T>(d_out + qbase, kk, g) : frag_zero<T>();
+    if (qvalid) {  // D_i partial over this lane's columns, in the caller's precision
+      const IO* po = out + qbase + kk * M::KSTEP + M::KPL * g;
+      const IO* pd = d_out + qbase + kk * M::KSTEP + M::KPL * g;
+#pragma unroll
+      for (int e = 0; e < M::KPL; ++e) dot += to_f32(pd[e]) * to_f32(po[e]);
+    }
   }
+  const float drow = col_sum(dot);
   const long si = (long)h * total_tokens + td.tok0 + qrow;
-  const float lse2 = qvalid ? lse[si] * kLog2e : 0.0f;
-  const float drow = qvalid ? dvec[si] : 0.0f;
+  if (grp == 0 && qvalid && g == 0) dvec[si] = drow;
+  const float nlse2 = qvalid ? -lse[si] * kLog2e : 0.0f;
 
   f32x4 acc_dq[D / 16];
 #pragma unroll
   for (int db = 0; db < D / 16; ++db) acc_dq[db] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  const T* kb = ksrc + ((long)td.tok0 * n_heads_kv + kvh) * D;
-  const T* vb = vsrc + ((long)td.tok0 * n_heads_kv + kvh) * D;
-  const T* ktb = kt_g + (long)kvh * D * ptot + td.ptok0;
-  for (int kt = 0; kt <= td.tile; ++kt) {
-    __syncthreads();
-    const long roff = (long)kTile * kt * n_heads_kv * D;
-    stage_rm<T, D>(ks, kb + roff, (long)n_heads_kv * D, td.len - kTile * kt, tid);
-    stage_rm<T, D>(vs, vb + roff, (long)n_heads_kv * D, td.len - kTile * kt, tid);
-    stage_tr<T, D>(kts, ktb + kTile * kt, ptot, tid);
-    __syncthreads();
-
-    const int nb = (kt == td.tile) ? (w + 1) : 4;
+  // One key tile: S, dP, P from lse, dS = P (dP - D), dQ^T += K^T dS^T.
+  auto step = [&](const T* ks, const T* vs, auto diag) {
+    constexpr bool DIAG = decltype(diag)::value;
+    const int nb = DIAG ? (wq + 1) : 4;
     float ds[4][4];
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
-      f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f}, dp = {0.0f, 0.0f, 0.0f, 0.0f};
+      f32x4 sv = {0.0f, 0.0f, 0.0f, 0.0f}, dp = {0.0f, 0.0f, 0.0f, 0.0f};
       if (b < nb) {
 #pragma unroll
         for (int kk = 0; kk < NKD; ++kk) {
-          s = M::mma(frag_rm<T, D>(ks, 16 * b + c, kk, g), qf[kk], s);
+          sv = M::mma(frag_rm<T, D>(ks, 16 * b + c, kk, g), qf[kk], sv);
           dp = M::mma(frag_rm<T, D>(vs, 16 * b + c, kk, g), df[kk], dp);
         }
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int key = kTile * kt + 16 * b + 4 * g + r;
-        const bool ok = b < nb && key <= qrow;
-        const float pv = ok ? __builtin_amdgcn_exp2f(s[r] * scale_log2 - lse2) : 0.0f;
-        ds[b][r] = ok ? pv * (dp[r] - drow) : 0.0f;
+        const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[r], scale_log2, nlse2));
+        float x = pv * (dp[r] - drow);
+        if (DIAG) x = (b < nb && 16 * b + 4 * g + r <= 16 * wq + c) ? x : 0.0f;
+        ds[b][r] = x;
       }
     }
-    acc_tr<T, D>(acc_dq, kts, ds, nb, lane);
+    acc_rows<T, D>(acc_dq, ks, ds, nb, lane);
+  };
+
+  if (grp <= td.tile) {
+    kreg.store(glds, gtid);
+    vreg.store(glds + L::TILE, gtid);
+  }
+  __syncthreads();
+
+  const int nit = (td.tile + G) / G;
+  for (int it = 0; it < nit; ++it) {
+    const int kt = grp + G * it;
+    const T* ks = glds + (it & 1) * 2 * L::TILE;
+    const bool more = kt + G <= td.tile;
+    if (more) {
+      const long roff = (long)kTile * (kt + G) * kvstride;
+      const int nv = td.len - kTile * (kt + G);
+      kreg.load(kbase + roff, kvstride, nv, gtid);
+      vreg.load(vbase + roff, kvstride, nv, gtid);
+    }
+    if (kt < td.tile)
+      step(ks, ks + L::TILE, std::false_type{});
+    else if (kt == td.tile)
+      step(ks, ks + L::TILE, std::true_type{});
+    if (more) {
+      T* nxt = glds + ((it + 1) & 1) * 2 * L::TILE;
+      kreg.store(nxt, gtid);
+      vreg.store(nxt + L::TILE, gtid);
+    }
+    __syncthreads();
+  }
+
+  if constexpr (G == 2) {
+    float* cmb = reinterpret_cast<float*>(lds + 4 * L::TILE) + wq * (D / 4) * 64 + lane;
+    if (grp == 1) {
+#pragma unroll
+      for (int db = 0; db < D / 16; ++db)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) cmb[(4 * db + r) * 64] = acc_dq[db][r];
+    }
+    __syncthreads();
+    if (grp == 1) return;
+#pragma unroll
+    for (int db = 0; db < D / 16; ++db)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc_dq[db][r] += cmb[(4 * db + r) * 64];
   }
 
   if (qvalid) {
@@ -484,43 +780,79 @@ __global__ __launch_bounds__(kThreads) void attn_dq_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// attn_dkdv: grid (Hq, ntiles in key order); dynamic LDS = Q, dO tiles,
-// Q^T, dO^T tiles, 64 lse and 64 D values.
+// attn_dkdv: grid (Hq, ntiles in key order), 256 * G threads; G query groups
+// split the key tile's query tiles (group grp takes td.tile + grp, + G, ...),
+// each double-buffering its own Q tile, dO tile and 64 lse / 64 D values in
+// LDS; the partial dK/dV are summed in a fixed order at the end.
+// tiles == nullptr: one sequence, key tile 0 (the most query tiles) first.
 // ---------------------------------------------------------------------------
-template <typename T, int D>
-__global__ __launch_bounds__(kThreads) void attn_dkdv_kernel(
-    const T* __restrict__ qsrc, const T* __restrict__ dosrc,
-    const T* __restrict__ ksrc, const T* __restrict__ vsrc,
-    const T* __restrict__ qt_g, const T* __restrict__ dot_g,
+template <typename IO, typename T, int D>
+__global__ __launch_bounds__(kThreads * bwd_groups<T>()) void attn_dkdv_kernel(
+    const IO* __restrict__ q_rot, const IO* __restrict__ d_out,
+    const IO* __restrict__ k_rot, const IO* __restrict__ v,
     const float* __restrict__ lse, const float* __restrict__ dvec,
     float* __restrict__ wk, float* __restrict__ wv,
-    const TileDesc* __restrict__ tiles, int n_heads_q, int n_heads_kv,
-    int total_tokens, int ptot, float scale_log2, float scale) {
+    const TileDesc* __restrict__ tiles, int n_tiles, int n_heads_q, int n_heads_kv,
+    int total_tokens, float scale_log2, float scale) {
   using M = Mfma<T>;
   using L = Lds<T, D>;
+  constexpr int G = bwd_groups<T>();
   constexpr int NKD = D / M::KSTEP;
+  constexpr int BUF = 2 * L::TILE * sizeof(T) + 2 * kTile * sizeof(float);  // bytes
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  T* qs = reinterpret_cast<T*>(smem_raw);
-  T* dos = qs + L::RM_ELEMS;
-  T* qts = dos + L::RM_ELEMS;
-  T* dots = qts + L::TR_ELEMS;
-  float* lse_s = reinterpret_cast<float*>(dots + L::TR_ELEMS);
-  float* d_s = lse_s + kTile;
 
   const int h = blockIdx.x;
-  const TileDesc td = tiles[blockIdx.y];
+  const TileDesc td = tiles != nullptr ? tiles[blockIdx.y]
+                                       : TileDesc{0, total_tokens, (int)blockIdx.y, 0};
   const int kvh = h / (n_heads_q / n_heads_kv);
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int grp = w >> 2, wq = w & 3, gtid = tid & (kThreads - 1);
   const int g = lane >> 4, c = lane & 15;
-  const int krow = kTile * td.tile + 16 * w + c;
+  const int krow = kTile * td.tile + 16 * wq + c;
   const bool kvalid = krow < td.len;
   const long kbase = ((long)(td.tok0 + krow) * n_heads_kv + kvh) * D;
+  unsigned char* const gsm = smem_raw + grp * 2 * BUF;
+
+  const int ntq = (td.len + kTile - 1) / kTile;
+  const long qstride = (long)n_heads_q * D;
+  const IO* qb = q_rot + ((long)td.tok0 * n_heads_q + h) * D;
+  const IO* dob = d_out + ((long)td.tok0 * n_heads_q + h) * D;
+  const float* lseb = lse + (long)h * total_tokens + td.tok0;
+  const float* dvb = dvec + (long)h * total_tokens + td.tok0;
+
+  // Stage one query tile: Q, dO rows into registers, -lse*log2(e) or D into
+  // one float (rows past the sequence get -inf / 0, so their P and dS are 0).
+  TileRegs<IO, D> qreg, dreg;
+  float vecv = 0.0f;
+  auto load_tile = [&](int qt) {
+    const long roff = (long)kTile * qt * qstride;
+    const int nv = td.len - kTile * qt;
+    qreg.load(qb + roff, qstride, nv, gtid);
+    dreg.load(dob + roff, qstride, nv, gtid);
+    if (gtid < 2 * kTile) {
+      const int r = gtid & (kTile - 1);
+      if (gtid < kTile)
+        vecv = r < nv ? -lseb[kTile * qt + r] * kLog2e : -INFINITY;
+      else
+        vecv = r < nv ? dvb[kTile * qt + r] : 0.0f;
+    }
+  };
+  auto store_tile = [&](int buf) {
+    unsigned char* base = gsm + buf * BUF;
+    qreg.store(reinterpret_cast<T*>(base), gtid);
+    dreg.store(reinterpret_cast<T*>(base) + L::TILE, gtid);
+    if (gtid < 2 * kTile)
+      reinterpret_cast<float*>(base + 2 * L::TILE * sizeof(T))[gtid] = vecv;
+  };
+
+  const int first = td.tile + grp;
+  if (first < ntq) load_tile(first);
 
   typename M::Frag kf[NKD], vf[NKD];
 #pragma unroll
   for (int kk = 0; kk < NKD; ++kk) {
-    kf[kk] = kvalid ? frag_global<T>(ksrc + kbase, kk, g) : frag_zero<T>();
-    vf[kk] = kvalid ? frag_global<T>(vsrc + kbase, kk, g) : frag_zero<T>();
+    kf[kk] = kvalid ? frag_global<T>(k_rot + kbase, kk, g) : frag_zero<T>();
+    vf[kk] = kvalid ? frag_global<T>(v + kbase, kk, g) : frag_zero<T>();
   }
 
   f32x4 acc_dk[D / 16], acc_dv[D / 16];
@@ -530,52 +862,76 @@ __global__ __launch_bounds__(kThreads) void attn_dkdv_kernel(
     acc_dv[db] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   }
 
-  const int ntq = (td.len + kTile - 1) / kTile;
-  const T* qb = qsrc + ((long)td.tok0 * n_heads_q + h) * D;
-  const T* dob = dosrc + ((long)td.tok0 * n_heads_q + h) * D;
-  const T* qtb = qt_g + (long)h * D * ptot + td.ptok0;
-  const T* dotb = dot_g + (long)h * D * ptot + td.ptok0;
-  const float* lseb = lse + (long)h * total_tokens + td.tok0;
-  const float* db_ = dvec + (long)h * total_tokens + td.tok0;
-  for (int qt = td.tile; qt < ntq; ++qt) {
-    __syncthreads();
-    const long roff = (long)kTile * qt * n_heads_q * D;
-    const int nv = td.len - kTile * qt;
-    stage_rm<T, D>(qs, qb + roff, (long)n_heads_q * D, nv, tid);
-    stage_rm<T, D>(dos, dob + roff, (long)n_heads_q * D, nv, tid);
-    stage_tr<T, D>(qts, qtb + kTile * qt, ptot, tid);
-    stage_tr<T, D>(dots, dotb + kTile * qt, ptot, tid);
-    if (tid < kTile) {
-      const bool ok = tid < nv;
-      lse_s[tid] = ok ? lseb[kTile * qt + tid] * kLog2e : 0.0f;
-      d_s[tid] = ok ? db_[kTile * qt + tid] : 0.0f;
-    }
-    __syncthreads();
-
-    const int b0 = (qt == td.tile) ? w : 0;  // query blocks below b0 are masked
+  // One query tile: S, dP (keys as columns), P, dS; dV^T += dO^T P,
+  // dK^T += Q^T dS.  DIAG: the query tile that holds the keys themselves.
+  auto step = [&](const unsigned char* base, auto diag) {
+    constexpr bool DIAG = decltype(diag)::value;
+    const T* qs = reinterpret_cast<const T*>(base);
+    const T* dos = qs + L::TILE;
+    const float* nlse_s = reinterpret_cast<const float*>(base + 2 * L::TILE * sizeof(T));
+    const float* d_s = nlse_s + kTile;
+    const int b0 = DIAG ? wq : 0;  // query blocks below b0 are masked
     float p[4][4], ds[4][4];
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
-      f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f}, dp = {0.0f, 0.0f, 0.0f, 0.0f};
+      f32x4 sv = {0.0f, 0.0f, 0.0f, 0.0f}, dp = {0.0f, 0.0f, 0.0f, 0.0f};
       if (b >= b0) {
 #pragma unroll
         for (int kk = 0; kk < NKD; ++kk) {
-          s = M::mma(frag_rm<T, D>(qs, 16 * b + c, kk, g), kf[kk], s);
+          sv = M::mma(frag_rm<T, D>(qs, 16 * b + c, kk, g), kf[kk], sv);
           dp = M::mma(frag_rm<T, D>(dos, 16 * b + c, kk, g), vf[kk], dp);
         }
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int qi = 16 * b + 4 * g + r;
-        const int qrow = kTile * qt + qi;
-        const bool ok = b >= b0 && krow <= qrow && qrow < td.len;
-        const float pv = ok ? __builtin_amdgcn_exp2f(s[r] * scale_log2 - lse_s[qi]) : 0.0f;
+        float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[r], scale_log2, nlse_s[qi]));
+        if (DIAG) pv = (b >= b0 && 16 * wq + c <= qi) ? pv : 0.0f;
         p[b][r] = pv;
-        ds[b][r] = ok ? pv * (dp[r] - d_s[qi]) : 0.0f;
+        ds[b][r] = pv * (dp[r] - d_s[qi]);
       }
     }
-    acc_tr<T, D>(acc_dv, dots, p, 4, lane);
-    acc_tr<T, D>(acc_dk, qts, ds, 4, lane);
+    acc_rows<T, D>(acc_dv, dos, p, 4, lane);
+    acc_rows<T, D>(acc_dk, qs, ds, 4, lane);
+  };
+
+  if (first < ntq) store_tile(0);
+  __syncthreads();
+
+  const int nit = (ntq - td.tile + G - 1) / G;  // iterations of group 0 (the most)
+  for (int it = 0; it < nit; ++it) {
+    const int qt = first + G * it;
+    const unsigned char* base = gsm + (it & 1) * BUF;
+    const bool more = qt + G < ntq;
+    if (more) load_tile(qt + G);
+    if (qt == td.tile)
+      step(base, std::true_type{});
+    else if (qt < ntq)
+      step(base, std::false_type{});
+    if (more) store_tile((it + 1) & 1);
+    __syncthreads();
+  }
+
+  if constexpr (G == 2) {
+    float* cmb = reinterpret_cast<float*>(smem_raw + 2 * BUF) + wq * (D / 2) * 64 + lane;
+    if (grp == 1) {
+#pragma unroll
+      for (int db = 0; db < D / 16; ++db)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          cmb[(4 * db + r) * 64] = acc_dk[db][r];
+          cmb[(D / 4 + 4 * db + r) * 64] = acc_dv[db][r];
+        }
+    }
+    __syncthreads();
+    if (grp == 1) return;
+#pragma unroll
+    for (int db = 0; db < D / 16; ++db)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        acc_dk[db][r] += cmb[(4 * db + r) * 64];
+        acc_dv[db][r] += cmb[(D / 4 + 4 * db + r) * 64];
+      }
   }
 
   if (kvalid) {
@@ -630,16 +986,17 @@ namespace {
 
 template <typename T, int D>
 constexpr size_t fwd_lds() {
-  return sizeof(T) * (Lds<T, D>::RM_ELEMS + Lds<T, D>::TR_ELEMS);
+  // K/V double buffers per group, plus group 0's Q fragments for group 1
+  return sizeof(T) * 4 * Lds<T, D>::TILE * fwd_groups<T>() +
+         (fwd_groups<T>() == 2 ? sizeof(T) * kTile * D : 0);
 }
 template <typename T, int D>
 constexpr size_t dq_lds() {
-  return sizeof(T) * (2 * Lds<T, D>::RM_ELEMS + Lds<T, D>::TR_ELEMS);
+  return sizeof(T) * 4 * Lds<T, D>::TILE * bwd_groups<T>();
 }
 template <typename T, int D>
 constexpr size_t dkdv_lds() {
-  return sizeof(T) * (2 * Lds<T, D>::RM_ELEMS + 2 * Lds<T, D>::TR_ELEMS) +
-         2 * kTile * sizeof(float);
+  return 2 * (sizeof(T) * 2 * Lds<T, D>::TILE + 2 * kTile * sizeof(float)) * bwd_groups<T>();
 }
 
 template <typename F>
@@ -659,25 +1016,42 @@ hipError_t allow_lds(F* fn, size_t bytes) {
 template <typename IO, typename T, int D>
 hipError_t forward_impl(const FwdLaunch& a, hipStream_t st, KernelTimer* tm) {
   const dim3 blk(kThreads);
+  T* kc = static_cast<T*>(a.kc);
   {
-    ScopedTiming t(tm, kKernKvPrep, st);
-    hipLaunchKernelGGL((kv_prep_kernel<IO, T, D>), dim3(a.n_heads_kv, a.n_tiles), blk, 0, st,
-                       static_cast<const IO*>(a.k), static_cast<const IO*>(a.v),
-                       static_cast<T*>(a.kc), static_cast<IO*>(a.k_rot),
-                       static_cast<T*>(a.vt), a.tiles_any, a.n_heads_kv, a.ptot,
-                       a.cos_t, a.sin_t);
+    const long n = (long)a.total_tokens * a.n_heads_kv * (D / 16);
+    const unsigned grid = static_cast<unsigned>((n + kThreads - 1) / kThreads);
+    IO* k_rot = static_cast<IO*>(a.k_rot);
+    ScopedTiming t(tm, kKernRopeK, st);
+    hipLaunchKernelGGL((rope_k_kernel<IO, T, D>), dim3(grid), blk, 0, st,
+                       static_cast<const IO*>(a.k), k_rot,
+                       (static_cast<void*>(kc) == static_cast<void*>(k_rot)) ? nullptr : kc,
+                       static_cast<const IO*>(a.v), static_cast<T*>(a.vc), a.pos_of,
+                       a.total_tokens, a.n_heads_kv, a.cos_t, a.sin_t);
     GL_CHECK(hipGetLastError());
   }
-  {
+  if constexpr (sizeof(T) == 2) {
+    auto fn = attn_fwd_bf16_kernel<IO, D>;
+    constexpr size_t lds = fwd_bf16_lds<D>();
+    GL_CHECK(allow_lds(fn, lds));
+    ScopedTiming t(tm, kKernFwd, st);
+    hipLaunchKernelGGL(fn, dim3(a.n_heads_q, a.n_tiles), dim3(kFwdThreads), lds, st,
+                       static_cast<const IO*>(a.q), static_cast<const bf16*>(a.kc),
+                       static_cast<const bf16*>(a.vc != nullptr ? a.vc : a.v),
+                       static_cast<IO*>(a.out), a.lse,
+                       static_cast<IO*>(a.q_rot), a.single_seq ? nullptr : a.tiles_fwd,
+                       a.n_tiles, a.n_heads_q, a.n_heads_kv, a.total_tokens, a.scale_log2,
+                       a.cos_t, a.sin_t);
+    GL_CHECK(hipGetLastError());
+  } else {
     auto fn = attn_fwd_kernel<IO, T, D>;
     constexpr size_t lds = fwd_lds<T, D>();
     GL_CHECK(allow_lds(fn, lds));
     ScopedTiming t(tm, kKernFwd, st);
-    hipLaunchKernelGGL(fn, dim3(a.n_heads_q, a.n_tiles), blk, lds, st,
-                       static_cast<const IO*>(a.q), static_cast<const T*>(a.kc),
-                       static_cast<const T*>(a.vt), static_cast<IO*>(a.out), a.lse,
-                       static_cast<IO*>(a.q_rot), a.tiles_fwd, a.n_heads_q,
-                       a.n_heads_kv, a.total_tokens, a.ptot, a.scale_log2,
+    hipLaunchKernelGGL(fn, dim3(a.n_heads_q, a.n_tiles), dim3(kThreads * fwd_groups<T>()), lds,
+                       st, static_cast<const IO*>(a.q), static_cast<const T*>(kc),
+                       static_cast<const IO*>(a.v), static_cast<IO*>(a.out), a.lse,
+                       static_cast<IO*>(a.q_rot), a.single_seq ? nullptr : a.tiles_fwd,
+                       a.n_tiles, a.n_heads_q, a.n_heads_kv, a.total_tokens, a.scale_log2,
                        a.cos_t, a.sin_t);
     GL_CHECK(hipGetLastError());
   }
@@ -687,48 +1061,31 @@ hipError_t forward_impl(const FwdLaunch& a, hipStream_t st, KernelTimer* tm) {
 template <typename IO, typename T, int D>
 hipError_t backward_impl(const BwdLaunch& a, hipStream_t st, KernelTimer* tm) {
   const dim3 blk(kThreads);
-  const bool same = std::is_same<IO, T>::value;
-  {
-    ScopedTiming t(tm, kKernBwdPrep, st);
-    hipLaunchKernelGGL((bwd_prep_kernel<IO, T, D>),
-                       dim3(a.n_heads_q + a.n_heads_kv, a.n_tiles), blk, 0, st,
-                       static_cast<const IO*>(a.d_out), static_cast<const IO*>(a.out),
-                       static_cast<const IO*>(a.q_rot), static_cast<const IO*>(a.k_rot),
-                       static_cast<const IO*>(a.v), a.dvec, static_cast<T*>(a.dot_t),
-                       static_cast<T*>(a.qt), static_cast<T*>(a.kt),
-                       same ? nullptr : static_cast<T*>(a.doc),
-                       same ? nullptr : static_cast<T*>(a.qc),
-                       same ? nullptr : static_cast<T*>(a.kc),
-                       same ? nullptr : static_cast<T*>(a.vc), a.tiles_any,
-                       a.n_heads_q, a.n_heads_kv, a.total_tokens, a.ptot);
-    GL_CHECK(hipGetLastError());
-  }
-  const T* qsrc = static_cast<const T*>(same ? a.q_rot : a.qc);
-  const T* dosrc = static_cast<const T*>(same ? a.d_out : a.doc);
-  const T* ksrc = static_cast<const T*>(same ? a.k_rot : a.kc);
-  const T* vsrc = static_cast<const T*>(same ? a.v : a.vc);
+  const IO* q_rot = static_cast<const IO*>(a.q_rot);
+  const IO* k_rot = static_cast<const IO*>(a.k_rot);
+  const IO* v = static_cast<const IO*>(a.v);
+  const IO* d_out = static_cast<const IO*>(a.d_out);
   {
     auto fn = attn_dq_kernel<IO, T, D>;
     constexpr size_t lds = dq_lds<T, D>();
     GL_CHECK(allow_lds(fn, lds));
     ScopedTiming t(tm, kKernDq, st);
-    hipLaunchKernelGGL(fn, dim3(a.n_heads_q, a.n_tiles), blk, lds, st, qsrc, dosrc,
-                       ksrc, vsrc, static_cast<const T*>(a.kt), a.lse, a.dvec,
-                       static_cast<IO*>(a.dq), a.tiles_fwd, a.n_heads_q,
-                       a.n_heads_kv, a.total_tokens, a.ptot, a.scale_log2,
+    hipLaunchKernelGGL(fn, dim3(a.n_heads_q, a.n_tiles), dim3(kThreads * bwd_groups<T>()), lds,
+                       st, q_rot, d_out, static_cast<const IO*>(a.out), k_rot, v, a.lse,
+                       a.dvec, static_cast<IO*>(a.dq), a.single_seq ? nullptr : a.tiles_fwd,
+                       a.n_tiles, a.n_heads_q, a.n_heads_kv, a.total_tokens, a.scale_log2,
                        a.scale, a.cos_t, a.sin_t);
     GL_CHECK(hipGetLastError());
   }
   {
-    auto fn = attn_dkdv_kernel<T, D>;
+    auto fn = attn_dkdv_kernel<IO, T, D>;
     constexpr size_t lds = dkdv_lds<T, D>();
     GL_CHECK(allow_lds(fn, lds));
     ScopedTiming t(tm, kKernDkdv, st);
-    hipLaunchKernelGGL(fn, dim3(a.n_heads_q, a.n_tiles), blk, lds, st, qsrc, dosrc,
-                       ksrc, vsrc, static_cast<const T*>(a.qt),
-                       static_cast<const T*>(a.dot_t), a.lse, a.dvec, a.wk, a.wv,
-                       a.tiles_kv, a.n_heads_q, a.n_heads_kv, a.total_tokens,
-                       a.ptot, a.scale_log2, a.scale);
+    hipLaunchKernelGGL(fn, dim3(a.n_heads_q, a.n_tiles), dim3(kThreads * bwd_groups<T>()), lds,
+                       st, q_rot, d_out, k_rot, v, a.lse, a.dvec, a.wk, a.wv,
+                       a.single_seq ? nullptr : a.tiles_kv, a.n_tiles, a.n_heads_q,
+                       a.n_heads_kv, a.total_tokens, a.scale_log2, a.scale);
     GL_CHECK(hipGetLastError());
   }
   {

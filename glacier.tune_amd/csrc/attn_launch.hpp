@@ -23,7 +23,7 @@ struct TileDesc {
   int32_t tok0;   // first token of the sequence in the [T][H][D] tensors
   int32_t len;    // tokens in the sequence
   int32_t tile;   // tile index inside the sequence (rows 64*tile ..)
-  int32_t ptok0;  // first column of the sequence in the padded transposed scratch
+  int32_t pad;
 };
 
 constexpr int kPrecFp32 = 0;
@@ -31,13 +31,12 @@ constexpr int kPrecBf16 = 1;
 
 // Kernel kinds, in launch order.
 enum KernelId : int {
-  kKernKvPrep = 0,
+  kKernRopeK = 0,
   kKernFwd = 1,
-  kKernBwdPrep = 2,
-  kKernDq = 3,
-  kKernDkdv = 4,
-  kKernReduce = 5,
-  kKernCount = 6,
+  kKernDq = 2,
+  kKernDkdv = 3,
+  kKernReduce = 4,
+  kKernCount = 5,
 };
 
 // Optional per-kernel hipEvent timing on the launch stream.
@@ -107,35 +106,35 @@ class ScopedTiming {
 struct FwdLaunch {
   int precision;
   bool io_bf16;
+  bool single_seq;               // one sequence: tile order is computed in-kernel
   int head_dim, n_heads_q, n_heads_kv, total_tokens;
-  int n_tiles, ptot;
+  int n_tiles;
   float scale_log2;
   const void *q, *k, *v;
   void *out, *q_rot, *k_rot;
   float* lse;
-  void *kc, *vt;                 // scratch: rotated K (token-major), V^T
+  void* kc;                      // rotated K in the compute dtype (may be k_rot)
+  void* vc;                      // V in the compute dtype when it differs from v's, else null
   const TileDesc* tiles_fwd;     // longest query tiles first
-  const TileDesc* tiles_any;
+  const int32_t* pos_of;         // position of each token inside its sequence
   const float *cos_t, *sin_t;    // [max len][D/2]
 };
 
 struct BwdLaunch {
   int precision;
   bool io_bf16;
+  bool single_seq;               // one sequence: tile order is computed in-kernel
   int head_dim, n_heads_q, n_heads_kv, total_tokens;
-  int n_tiles, ptot;
+  int n_tiles;
   float scale_log2, scale;
   const void *d_out, *q_rot, *k_rot, *v, *out;
   const float* lse;
   void *dq, *dk, *dv;
   float* dvec;                   // [Hq][T] row terms dO.O
-  void *dot_t, *qt, *kt;         // transposed scratch
-  void *doc, *qc, *kc, *vc;      // compute-dtype copies (fp32 tensors, bf16 math)
   float *wk, *wv;                // per-query-head dK/dV partials [T][Hq][D]
   const TileDesc* tiles_fwd;
   const TileDesc* tiles_kv;      // key tiles with the most query tiles first
-  const TileDesc* tiles_any;
-  const int32_t* pos_of;         // position of each token inside its sequence
+  const int32_t* pos_of;
   const float *cos_t, *sin_t;
 };
 

@@ -86,8 +86,8 @@ struct Shape {
 
 // Tile lists of one sequence layout, resident on the device.
 struct TileSet {
-  int n_tiles = 0, ptot = 0, max_len = 0;
-  DeviceBuffer tiles;  // [3][n_tiles] TileDesc: fwd order, kv order, natural
+  int n_tiles = 0, max_len = 0;
+  DeviceBuffer tiles;  // [2][n_tiles] TileDesc: fwd order, kv order
   DeviceBuffer pos;    // [T] int32
 };
 
@@ -141,23 +141,31 @@ class GpuAttentionEngine {
     const TileSet& ts = tiles_for(s);
     EnsureRopeTable(ts.max_len, s.head_dim, s.rope_freq_base);
     const size_t esz = compute_elem_size(s.precision, s.io_bf16);
+    const size_t io_esz = s.io_bf16 ? 2 : 4;
     FwdLaunch a{};
     a.precision = s.precision;
     a.io_bf16 = s.io_bf16;
+    a.single_seq = s.cu.size() == 2;
     a.head_dim = s.head_dim;
     a.n_heads_q = s.n_heads_q;
     a.n_heads_kv = s.n_heads_kv;
     a.total_tokens = s.total_tokens;
     a.n_tiles = ts.n_tiles;
-    a.ptot = ts.ptot;
     a.scale_log2 = kLog2e / std::sqrt(static_cast<float>(s.head_dim));
     a.q = q; a.k = k; a.v = v;
     a.out = out; a.lse = lse; a.q_rot = q_rot; a.k_rot = k_rot;
-    a.kc = kc_.ensure((size_t)s.total_tokens * s.n_heads_kv * s.head_dim * esz, "K scratch");
-    a.vt = vt_.ensure((size_t)s.n_heads_kv * s.head_dim * ts.ptot * esz, "V^T scratch");
+    // The attention kernel reads rotated K in the compute dtype: the caller's
+    // k_rot when it is that dtype, else library scratch.
+    if (k_rot != nullptr && esz == io_esz)
+      a.kc = k_rot;
+    else
+      a.kc = kc_.ensure((size_t)s.total_tokens * s.n_heads_kv * s.head_dim * esz, "K scratch");
+    // bf16 matrix cores on fp32 tensors: rope_k also writes a bf16 copy of V.
+    if (esz != io_esz)
+      a.vc = vc_.ensure((size_t)s.total_tokens * s.n_heads_kv * s.head_dim * esz, "V scratch");
     const TileDesc* t = static_cast<const TileDesc*>(ts.tiles.ptr);
     a.tiles_fwd = t;
-    a.tiles_any = t + 2 * ts.n_tiles;
+    a.pos_of = static_cast<const int32_t*>(ts.pos.ptr);
     a.cos_t = static_cast<const float*>(rope_cos_.ptr);
     a.sin_t = static_cast<const float*>(rope_sin_.ptr);
     check_hip(launch_forward(a, stream(), &timer_), "attention forward launch");
@@ -170,38 +178,26 @@ class GpuAttentionEngine {
     if (s.total_tokens == 0) return;
     const TileSet& ts = tiles_for(s);
     EnsureRopeTable(ts.max_len, s.head_dim, s.rope_freq_base);
-    const size_t esz = compute_elem_size(s.precision, s.io_bf16);
-    const size_t T = s.total_tokens, Hq = s.n_heads_q, Hkv = s.n_heads_kv, D = s.head_dim;
-    const bool copies = !s.io_bf16 && s.precision == kPrecBf16;
+    const size_t T = s.total_tokens, Hq = s.n_heads_q, D = s.head_dim;
     BwdLaunch a{};
     a.precision = s.precision;
     a.io_bf16 = s.io_bf16;
+    a.single_seq = s.cu.size() == 2;
     a.head_dim = s.head_dim;
     a.n_heads_q = s.n_heads_q;
     a.n_heads_kv = s.n_heads_kv;
     a.total_tokens = s.total_tokens;
     a.n_tiles = ts.n_tiles;
-    a.ptot = ts.ptot;
     a.scale = 1.0f / std::sqrt(static_cast<float>(s.head_dim));
     a.scale_log2 = kLog2e * a.scale;
     a.d_out = d_out; a.q_rot = q_rot; a.k_rot = k_rot; a.v = v; a.out = out;
     a.lse = lse; a.dq = dq; a.dk = dk; a.dv = dv;
     a.dvec = static_cast<float*>(dvec_.ensure(Hq * T * sizeof(float), "dO.O scratch"));
-    a.dot_t = dot_t_.ensure(Hq * D * ts.ptot * esz, "dO^T scratch");
-    a.qt = qt_.ensure(Hq * D * ts.ptot * esz, "Q^T scratch");
-    a.kt = kt_.ensure(Hkv * D * ts.ptot * esz, "K^T scratch");
-    if (copies) {
-      a.doc = doc_.ensure(T * Hq * D * esz, "dO scratch");
-      a.qc = qc_.ensure(T * Hq * D * esz, "Q scratch");
-      a.kc = kc_.ensure(T * Hkv * D * esz, "K scratch");
-      a.vc = vc_.ensure(T * Hkv * D * esz, "V scratch");
-    }
     a.wk = static_cast<float*>(wk_.ensure(T * Hq * D * sizeof(float), "dK partials"));
     a.wv = static_cast<float*>(wv_.ensure(T * Hq * D * sizeof(float), "dV partials"));
     const TileDesc* t = static_cast<const TileDesc*>(ts.tiles.ptr);
     a.tiles_fwd = t;
     a.tiles_kv = t + ts.n_tiles;
-    a.tiles_any = t + 2 * ts.n_tiles;
     a.pos_of = static_cast<const int32_t*>(ts.pos.ptr);
     a.cos_t = static_cast<const float*>(rope_cos_.ptr);
     a.sin_t = static_cast<const float*>(rope_sin_.ptr);
@@ -306,19 +302,16 @@ class GpuAttentionEngine {
     auto ts = std::make_unique<TileSet>();
     std::vector<TileDesc> nat;
     std::vector<int32_t> pos(s.total_tokens);
-    int ptok = 0;
     const int n = static_cast<int>(s.cu.size()) - 1;
     for (int b = 0; b < n; ++b) {
       const int tok0 = s.cu[b], len = s.cu[b + 1] - s.cu[b];
       if (len <= 0) continue;
       const int nt = (len + kTile - 1) / kTile;
-      for (int t = 0; t < nt; ++t) nat.push_back(TileDesc{tok0, len, t, ptok});
+      for (int t = 0; t < nt; ++t) nat.push_back(TileDesc{tok0, len, t, 0});
       for (int i = 0; i < len; ++i) pos[tok0 + i] = i;
-      ptok += nt * kTile;
       ts->max_len = std::max(ts->max_len, len);
     }
     ts->n_tiles = static_cast<int>(nat.size());
-    ts->ptot = ptok;
     if (ts->n_tiles > 65535)
       fail(GLACIER_ATTN_ERR_UNSUPPORTED, "more than 65535 tiles of 64 tokens in one call");
     // Longest query tiles first (they see the most keys), and key tiles with
@@ -333,7 +326,6 @@ class GpuAttentionEngine {
     std::vector<TileDesc> all;
     all.insert(all.end(), fwd.begin(), fwd.end());
     all.insert(all.end(), kv.begin(), kv.end());
-    all.insert(all.end(), nat.begin(), nat.end());
     ts->tiles.ensure(all.size() * sizeof(TileDesc), "tile table");
     ts->pos.ensure(pos.size() * sizeof(int32_t), "position table");
     check_hip(hipStreamSynchronize(stream()), "tile table");
@@ -359,7 +351,7 @@ class GpuAttentionEngine {
   int rope_len_ = 0, rope_dim_ = 0;
   float rope_base_ = 0.0f;
   // device-path scratch
-  DeviceBuffer kc_, vt_, dvec_, dot_t_, qt_, kt_, doc_, qc_, vc_, wk_, wv_;
+  DeviceBuffer kc_, vc_, dvec_, wk_, wv_;
   // host-path device copies
   DeviceBuffer h_q_, h_k_, h_v_, h_out_, h_lse_, h_qr_, h_kr_, h_dout_, h_dq_, h_dk_, h_dv_;
 };
@@ -455,7 +447,7 @@ int guarded(F&& f) {
 }
 
 const char* const kKernelNames[kKernCount] = {
-    "kv_prep", "attn_fwd", "bwd_prep", "attn_bwd_dq", "attn_bwd_dkdv", "dkdv_reduce",
+    "rope_k", "attn_fwd", "attn_bwd_dq", "attn_bwd_dkdv", "dkdv_reduce",
 };
 
 }  // namespace
