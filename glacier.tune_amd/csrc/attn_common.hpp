@@ -126,8 +126,20 @@ struct TileRegs {
   static_assert(N * NT == kTile * CPR, "tile must split evenly");
   uint4 w[N][W];
 
-  // Rows r >= nvalid are zero (past the end of the sequence).
+  // Rows r >= nvalid are zero (past the end of the sequence).  nvalid is
+  // uniform, so a full tile takes the branch-free path.
   __device__ inline void load(const IO* src, long gstride, int nvalid, int tid) {
+    if (nvalid >= kTile) {
+#pragma unroll
+      for (int i = 0; i < N; ++i) {
+        const int idx = tid + i * NT;
+        const int r = idx / CPR, ch = idx % CPR;
+        const uint4* p = reinterpret_cast<const uint4*>(src + (long)r * gstride + ch * 8);
+#pragma unroll
+        for (int j = 0; j < W; ++j) w[i][j] = p[j];
+      }
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < N; ++i) {
       const int idx = tid + i * NT;

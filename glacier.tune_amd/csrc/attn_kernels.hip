@@ -334,307 +334,330 @@ __global__ __launch_bounds__(kThreads * fwd_groups<T>()) void attn_fwd_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// attn_fwd, bf16 matrix cores: grid (Hq, ntiles), 512 threads = 4 key groups
-// x 2 waves.  Each wave owns 32 queries (two 16-query MFMA column blocks), so
-// every K and V fragment read from LDS feeds two MFMAs; group grp takes the
-// key tiles grp, grp + 4, ... of the query tile into its own single LDS
-// buffer (the next tile's global loads are in registers while the current
-// one is multiplied).  Group 0 rotates Q and hands the fragments to the other
-// groups through LDS; the four partial (max, sum, O) are merged in group
-// order at the end.
+// attn_fwd, bf16 matrix cores: grid (Hq/Hkv, Hkv, ntiles), 512 threads = 2
+// key groups x 4 waves x 16 queries.  Group grp takes the key tiles grp,
+// grp + 2, ... of the query tile and keeps two of them resident in LDS, so
+// the scores of its next tile are multiplied on the matrix cores while the
+// softmax of the current one runs on the vector ALUs (the next-next tile's
+// global loads are in registers meanwhile).  Group 0 rotates Q and hands the
+// fragments to group 1 through LDS; the two partial (max, sum, O) are merged
+// in group order at the end.
 // ---------------------------------------------------------------------------
-constexpr int kFwdGroups = 4;
+constexpr int kFwdGroups = 2;
 constexpr int kFwdThreads = 512;
 
 template <int D>
 constexpr size_t fwd_bf16_lds() {
-  // one K + V tile per group, then group 0's Q fragments (64 queries x D)
-  return sizeof(bf16) * (2 * kFwdGroups * Lds<bf16, D>::TILE + kTile * D);
+  // two K + V tiles per group, then group 0's Q fragments (64 queries x D)
+  return sizeof(bf16) * (4 * kFwdGroups * Lds<bf16, D>::TILE + kTile * D);
 }
 
-template <typename IO, int D>
+template <typename IO, int D, bool VARLEN>
 __global__ __launch_bounds__(kFwdThreads) void attn_fwd_bf16_kernel(
     const IO* __restrict__ q, const bf16* __restrict__ kc, const bf16* __restrict__ v,
     IO* __restrict__ out, float* __restrict__ lse, IO* __restrict__ q_rot,
-    const TileDesc* __restrict__ tiles, int n_tiles, int n_heads_q, int n_heads_kv,
-    int total_tokens, float scale_log2, const float* __restrict__ cos_t,
-    const float* __restrict__ sin_t) {
+    const TileDesc* __restrict__ tiles, int n_tiles, int total_tokens,
+    float scale_log2, const float* __restrict__ cos_t, const float* __restrict__ sin_t) {
   using M = Mfma<bf16>;
   using L = Lds<bf16, D>;
   using Frag = M::Frag;
   constexpr int G = kFwdGroups;
-  constexpr int GT = kFwdThreads / G;  // threads per group (2 waves)
-  constexpr int QB = 2;                // 16-query blocks per wave
+  constexpr int GT = kFwdThreads / G;  // threads per group (4 waves)
   constexpr int NKD = D / M::KSTEP;
   constexpr int H = D / 2;
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  bf16* const lds = reinterpret_cast<bf16*>(smem_raw);  // [G][K tile, V tile], Q frags
+  bf16* const lds = reinterpret_cast<bf16*>(smem_raw);  // [G][2][K tile, V tile], Q frags
 
-  const int h = blockIdx.x;
-  const TileDesc td = tiles != nullptr
-                          ? tiles[blockIdx.y]
-                          : TileDesc{0, total_tokens, n_tiles - 1 - (int)blockIdx.y, 0};
-  const int kvh = h / (n_heads_q / n_heads_kv);
+  // grid (query heads per KV head, KV heads, tiles): no integer division
+  const int n_heads_kv = gridDim.y, n_heads_q = gridDim.x * gridDim.y;
+  const int kvh = blockIdx.y, h = kvh * gridDim.x + blockIdx.x;
+  const TileDesc td = VARLEN ? tiles[blockIdx.z]
+                             : TileDesc{0, total_tokens, n_tiles - 1 - (int)blockIdx.z, 0};
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
-  const int grp = w >> 1, qh = w & 1, gtid = tid & (GT - 1);
+  const int grp = w >> 2, wq = w & 3, gtid = tid & (GT - 1);
   const int g = lane >> 4, c = lane & 15;
-  bf16* const glds = lds + grp * 2 * L::TILE;
+  const int qrow = kTile * td.tile + 16 * wq + c;
+  const bool qvalid = qrow < td.len;
+  const long qbase = ((long)(td.tok0 + qrow) * n_heads_q + h) * D;
+  bf16* const glds = lds + grp * 4 * L::TILE;  // buffer b: glds + b * 2 * TILE
 
-  // Start this group's first K/V tile loads before the Q prologue.
   const long kvstride = (long)n_heads_kv * D;
   const bf16* kbase = kc + ((long)td.tok0 * n_heads_kv + kvh) * D;
   const bf16* vbase = v + ((long)td.tok0 * n_heads_kv + kvh) * D;
   TileRegs<bf16, D, GT> kreg, vreg;
-  if (grp <= td.tile) {
-    const long roff = (long)kTile * grp * kvstride;
-    kreg.load(kbase + roff, kvstride, td.len - kTile * grp, gtid);
-    vreg.load(vbase + roff, kvstride, td.len - kTile * grp, gtid);
-  }
+  auto load_tile = [&](int kt) {
+    const long roff = (long)kTile * kt * kvstride;
+    kreg.load(kbase + roff, kvstride, td.len - kTile * kt, gtid);
+    vreg.load(vbase + roff, kvstride, td.len - kTile * kt, gtid);
+  };
+  auto store_tile = [&](int buf) {
+    kreg.store(glds + buf * 2 * L::TILE, gtid);
+    vreg.store(glds + buf * 2 * L::TILE + L::TILE, gtid);
+  };
+  if (grp <= td.tile) load_tile(grp);
 
-  // Q fragments of the wave's two query blocks, rotated in fp32 (group 0).
-  Frag qf[QB][NKD];
-  Frag* const qlds = reinterpret_cast<Frag*>(lds + 2 * G * L::TILE) + qh * QB * NKD * 64 + lane;
+  // Q fragments, rotated in fp32 then rounded to bf16 (group 0).
+  Frag qf[NKD];
+  Frag* const qlds = reinterpret_cast<Frag*>(lds + 4 * G * L::TILE) + wq * NKD * 64 + lane;
   if (grp == 0) {
 #pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
-      const int qrow = kTile * td.tile + 32 * qh + 16 * qb + c;
-      const bool qvalid = qrow < td.len;
-      const long qbase = ((long)(td.tok0 + qrow) * n_heads_q + h) * D;
+    for (int kk = 0; kk < NKD / 2; ++kk) {
+      const int d0 = kk * M::KSTEP + 8 * g;
+      float x0[8], x1[8], y0[8], y1[8], cs[8], sn[8];
+      if (qvalid) {
+        load8(q + qbase + d0, x0);
+        load8(q + qbase + d0 + H, x1);
+      } else {
 #pragma unroll
-      for (int kk = 0; kk < NKD / 2; ++kk) {
-        const int d0 = kk * M::KSTEP + 8 * g;
-        float x0[8], x1[8], y0[8], y1[8], cs[8], sn[8];
-        if (qvalid) {
-          load8(q + qbase + d0, x0);
-          load8(q + qbase + d0 + H, x1);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) x0[e] = x1[e] = 0.0f;
-        }
-        const long ti = (long)(qvalid ? qrow : 0) * H + d0;
-        load8(cos_t + ti, cs);
-        load8(sin_t + ti, sn);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          rope_fwd(x0[e], x1[e], cs[e], sn[e], y0[e], y1[e]);
-          qf[qb][kk][e] = (bf16)y0[e];
-          qf[qb][kk + NKD / 2][e] = (bf16)y1[e];
-        }
-        if (q_rot != nullptr && qvalid) {
-          store8(q_rot + qbase + d0, y0);
-          store8(q_rot + qbase + d0 + H, y1);
-        }
+        for (int e = 0; e < 8; ++e) x0[e] = x1[e] = 0.0f;
       }
+      const long ti = (long)(qvalid ? qrow : 0) * H + d0;
+      load8(cos_t + ti, cs);
+      load8(sin_t + ti, sn);
 #pragma unroll
-      for (int kk = 0; kk < NKD; ++kk) qlds[(qb * NKD + kk) * 64] = qf[qb][kk];
+      for (int e = 0; e < 8; ++e) {
+        rope_fwd(x0[e], x1[e], cs[e], sn[e], y0[e], y1[e]);
+        qf[kk][e] = (bf16)y0[e];
+        qf[kk + NKD / 2][e] = (bf16)y1[e];
+      }
+      if (q_rot != nullptr && qvalid) {
+        store8(q_rot + qbase + d0, y0);
+        store8(q_rot + qbase + d0 + H, y1);
+      }
     }
+#pragma unroll
+    for (int kk = 0; kk < NKD; ++kk) qlds[kk * 64] = qf[kk];
   }
 
-  f32x4 o[QB][D / 16];
-  float m_run[QB], l_lane[QB];
-#pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
-#pragma unroll
-    for (int db = 0; db < D / 16; ++db) o[qb][db] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    m_run[qb] = kNegBig;
-    l_lane[qb] = 0.0f;
-  }
-
-  // One key tile.  DIAG: the tile holding the queries (causal mask inside);
-  // there the wave needs key blocks b <= 2*qh + 1 only.
-  auto step = [&](const bf16* ks, const bf16* vs, auto diag) {
-    constexpr bool DIAG = decltype(diag)::value;
-    float sc[QB][4][4];
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      f32x4 acc[QB];
-#pragma unroll
-      for (int qb = 0; qb < QB; ++qb) acc[qb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-      if (!DIAG || b <= 2 * qh + 1) {
-#pragma unroll
-        for (int kk = 0; kk < NKD; ++kk) {
-          const Frag kf = frag_rm<bf16, D>(ks, 16 * b + c, kk, g);
-#pragma unroll
-          for (int qb = 0; qb < QB; ++qb) acc[qb] = M::mma(kf, qf[qb][kk], acc[qb]);
-        }
-      }
-#pragma unroll
-      for (int qb = 0; qb < QB; ++qb)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          float x = acc[qb][r];
-          if (DIAG) x = (16 * b + 4 * g + r <= 32 * qh + 16 * qb + c) ? x : -INFINITY;
-          sc[qb][b][r] = x;
-        }
-    }
-    float p[QB][4][4];
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
-      float mloc = -INFINITY;
-#pragma unroll
-      for (int b = 0; b < 4; ++b)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) mloc = fmaxf(mloc, sc[qb][b][r]);
-      const float m_tile = col_max(mloc) * scale_log2;
-      if (__builtin_amdgcn_ballot_w64(m_tile > m_run[qb] + kRescaleTau) != 0) {
-        const float m_new = fmaxf(m_run[qb], m_tile);
-        const float alpha = __builtin_amdgcn_exp2f(m_run[qb] - m_new);
-        l_lane[qb] *= alpha;
-#pragma unroll
-        for (int db = 0; db < D / 16; ++db) o[qb][db] *= alpha;
-        m_run[qb] = m_new;
-      }
-      float psum = 0.0f;
-#pragma unroll
-      for (int b = 0; b < 4; ++b)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          p[qb][b][r] =
-              __builtin_amdgcn_exp2f(__builtin_fmaf(sc[qb][b][r], scale_log2, -m_run[qb]));
-          psum += p[qb][b][r];
-        }
-      l_lane[qb] += psum;
-    }
-    // O^T += V^T P^T: each V^T fragment (transpose read) feeds both blocks.
-#pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2) {
-      if (DIAG && s2 > qh) break;
-      Frag pf[QB];
-#pragma unroll
-      for (int qb = 0; qb < QB; ++qb)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          pf[qb][r] = (bf16)p[qb][2 * s2][r];
-          pf[qb][4 + r] = (bf16)p[qb][2 * s2 + 1][r];
-        }
-#pragma unroll
-      for (int db = 0; db < D / 16; ++db) {
-        const bf16x4 lo = read_tr<L::STRIDE>(vs, 32 * s2, 16 * db, lane);
-        const bf16x4 hi = read_tr<L::STRIDE>(vs, 32 * s2 + 16, 16 * db, lane);
-        Frag a;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          a[r] = lo[r];
-          a[4 + r] = hi[r];
-        }
-#pragma unroll
-        for (int qb = 0; qb < QB; ++qb) o[qb][db] = M::mma(a, pf[qb], o[qb][db]);
-      }
-    }
-  };
-
-  if (grp <= td.tile) {
-    kreg.store(glds, gtid);
-    vreg.store(glds + L::TILE, gtid);
+  // The group's first two tiles into its two buffers (both loads in flight
+  // together; the second set of registers is dead once the loop starts).
+  if (grp + G <= td.tile) {
+    TileRegs<bf16, D, GT> kreg1, vreg1;
+    const long roff = (long)kTile * (grp + G) * kvstride;
+    kreg1.load(kbase + roff, kvstride, td.len - kTile * (grp + G), gtid);
+    vreg1.load(vbase + roff, kvstride, td.len - kTile * (grp + G), gtid);
+    store_tile(0);
+    kreg1.store(glds + 2 * L::TILE, gtid);
+    vreg1.store(glds + 3 * L::TILE, gtid);
+  } else if (grp <= td.tile) {
+    store_tile(0);
   }
   __syncthreads();
   if (grp != 0) {
 #pragma unroll
-    for (int qb = 0; qb < QB; ++qb)
-#pragma unroll
-      for (int kk = 0; kk < NKD; ++kk) qf[qb][kk] = qlds[(qb * NKD + kk) * 64];
+    for (int kk = 0; kk < NKD; ++kk) qf[kk] = qlds[kk * 64];
   }
+
+  f32x4 o[D / 16];
+#pragma unroll
+  for (int db = 0; db < D / 16; ++db) o[db] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  float m_run = kNegBig, l_lane = 0.0f;
+
+  // Raw scores S^T = K Q^T of one resident key tile (all four key blocks).
+  auto scores = [&](const bf16* ks, float (&sc)[4][4]) {
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int kk = 0; kk < NKD; ++kk)
+        acc = M::mma(frag_rm<bf16, D>(ks, 16 * b + c, kk, g), qf[kk], acc);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sc[b][r] = acc[r];
+    }
+  };
+
+  float sc[4][4];
+  if (grp <= td.tile) scores(glds, sc);
+
+  // Softmax of the current tile's scores (masked on the diagonal tile),
+  // interleaved with the next tile's scores, then O^T += V^T P^T.
+  auto step = [&](const bf16* vcur, const bf16* knext, float (&scn)[4][4], auto diag) {
+    constexpr bool DIAG = decltype(diag)::value;
+    float mloc = -INFINITY;
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        if (DIAG) sc[b][r] = (16 * b + 4 * g + r <= 16 * wq + c) ? sc[b][r] : -INFINITY;
+        mloc = fmaxf(mloc, sc[b][r]);
+      }
+    const float m_tile = col_max(mloc) * scale_log2;
+    if (__builtin_amdgcn_ballot_w64(m_tile > m_run + kRescaleTau) != 0) {
+      const float m_new = fmaxf(m_run, m_tile);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      l_lane *= alpha;
+#pragma unroll
+      for (int db = 0; db < D / 16; ++db) o[db] *= alpha;
+      m_run = m_new;
+    }
+    float p[4][4];
+    float psum = 0.0f;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int kk = 0; kk < NKD; ++kk)
+        acc = M::mma(frag_rm<bf16, D>(knext, 16 * b + c, kk, g), qf[kk], acc);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        scn[b][r] = acc[r];
+        p[b][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[b][r], scale_log2, -m_run));
+        psum += p[b][r];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4 * NKD; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // four VALU
+    }
+    l_lane += psum;
+    acc_rows<bf16, D>(o, vcur, p, DIAG ? wq + 1 : 4, lane);
+  };
 
   const int nit = (td.tile + G) / G;  // iterations of group 0 (the most)
   for (int it = 0; it < nit; ++it) {
     const int kt = grp + G * it;
-    const bool more = kt + G <= td.tile;
-    if (more) {  // prefetch this group's next tile into registers
-      const long roff = (long)kTile * (kt + G) * kvstride;
-      const int nv = td.len - kTile * (kt + G);
-      kreg.load(kbase + roff, kvstride, nv, gtid);
-      vreg.load(vbase + roff, kvstride, nv, gtid);
-    }
+    const int cur = it & 1;
+    const bool pre = kt + 2 * G <= td.tile;
+    if (pre) load_tile(kt + 2 * G);
+    float scn[4][4];
+    const bf16* vcur = glds + cur * 2 * L::TILE + L::TILE;
+    const bf16* knext = glds + (cur ^ 1) * 2 * L::TILE;
     if (kt < td.tile)
-      step(glds, glds + L::TILE, std::false_type{});
+      step(vcur, knext, scn, std::false_type{});
     else if (kt == td.tile)
-      step(glds, glds + L::TILE, std::true_type{});
+      step(vcur, knext, scn, std::true_type{});
     if (it + 1 < nit) {
       __syncthreads();
-      if (more) {
-        kreg.store(glds, gtid);
-        vreg.store(glds + L::TILE, gtid);
-      }
+      if (pre) store_tile(cur);
       __syncthreads();
     }
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sc[b][r] = scn[b][r];
   }
 
-  // Merge groups 1..3 into group 0, in group order, lane for lane (waves
-  // (grp, qh) all own the same queries with the same lane layout).
-  constexpr int NF = QB * (D / 4 + 2);  // floats per lane: per block O, max, sum
+  // Merge group 1 into group 0 (lane for lane: waves wq and wq + 4 own the
+  // same queries); 16-byte LDS accesses: (max, sum), then O.  Then O goes
+  // through LDS (row-major, output dtype, in group 1's region) so that all
+  // eight waves store whole 256-byte rows.
+  constexpr int NS = 1 + D / 16;
   __syncthreads();
-  float* const cmb = reinterpret_cast<float*>(smem_raw) + qh * NF * 64 + lane;
-  constexpr int GSTRIDE = 2 * NF * 64;  // floats per group
+  f32x4* const cmb = reinterpret_cast<f32x4*>(smem_raw) + wq * NS * 64 + lane;
   if (grp != 0) {
-    float* dst = cmb + (grp - 1) * GSTRIDE;
+    cmb[0] = f32x4{m_run, l_lane, 0.0f, 0.0f};
 #pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
-      float* d = dst + qb * (D / 4 + 2) * 64;
-      d[0] = m_run[qb];
-      d[64] = l_lane[qb];
-#pragma unroll
-      for (int db = 0; db < D / 16; ++db)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) d[(2 + 4 * db + r) * 64] = o[qb][db][r];
-    }
+    for (int db = 0; db < D / 16; ++db) cmb[(1 + db) * 64] = o[db];
   }
   __syncthreads();
-  if (grp != 0) return;
+  IO* const ot = reinterpret_cast<IO*>(lds + 4 * L::TILE);
+  constexpr int OS = D + 16 / sizeof(IO);  // padded row stride
+  if (grp == 0) {
+    const f32x4 ml = cmb[0];
+    const float m_new = fmaxf(m_run, ml[0]);
+    const float a0 = __builtin_amdgcn_exp2f(m_run - m_new);
+    const float a1 = __builtin_amdgcn_exp2f(ml[0] - m_new);
+    l_lane = l_lane * a0 + ml[1] * a1;
 #pragma unroll
-  for (int src = 0; src < G - 1; ++src) {
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
-      const float* d = cmb + src * GSTRIDE + qb * (D / 4 + 2) * 64;
-      const float m1 = d[0], l1 = d[64];
-      const float m_new = fmaxf(m_run[qb], m1);
-      const float a0 = __builtin_amdgcn_exp2f(m_run[qb] - m_new);
-      const float a1 = __builtin_amdgcn_exp2f(m1 - m_new);
-      l_lane[qb] = l_lane[qb] * a0 + l1 * a1;
-#pragma unroll
-      for (int db = 0; db < D / 16; ++db)
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          o[qb][db][r] = o[qb][db][r] * a0 + d[(2 + 4 * db + r) * 64] * a1;
-      m_run[qb] = m_new;
-    }
-  }
-
-#pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
-    const int qrow = kTile * td.tile + 32 * qh + 16 * qb + c;
-    const long qbase = ((long)(td.tok0 + qrow) * n_heads_q + h) * D;
-    const float l_tot = col_sum(l_lane[qb]);
+    for (int db = 0; db < D / 16; ++db) o[db] = o[db] * a0 + cmb[(1 + db) * 64] * a1;
+    m_run = m_new;
+    const float l_tot = col_sum(l_lane);
     const float inv = 1.0f / l_tot;
-    if (qrow < td.len) {
+    if (lse != nullptr && qvalid && g == 0)
+      lse[(long)h * total_tokens + td.tok0 + qrow] = (m_run + log2f(l_tot)) * kLn2;
 #pragma unroll
-      for (int db = 0; db < D / 16; ++db)
-        store4(out + qbase + 16 * db + 4 * g, o[qb][db] * inv);
-      if (lse != nullptr && g == 0)
-        lse[(long)h * total_tokens + td.tok0 + qrow] = (m_run[qb] + log2f(l_tot)) * kLn2;
-    }
+    for (int db = 0; db < D / 16; ++db) store4(ot + (16 * wq + c) * OS + 16 * db + 4 * g, o[db] * inv);
+  }
+  __syncthreads();
+  constexpr int CPR = D * sizeof(IO) / 16;  // 16-byte chunks per row
+  const long orow0 = (long)td.tok0 + kTile * td.tile;
+#pragma unroll
+  for (int i = 0; i < kTile * CPR / kFwdThreads; ++i) {
+    const int idx = tid + i * kFwdThreads;
+    const int r = idx / CPR, ch = idx % CPR;
+    if (kTile * td.tile + r < td.len)
+      *reinterpret_cast<uint4*>(out + ((orow0 + r) * n_heads_q + h) * D + ch * (16 / sizeof(IO))) =
+          *reinterpret_cast<const uint4*>(ot + r * OS + ch * (16 / sizeof(IO)));
   }
 }
 
 // ---------------------------------------------------------------------------
-// attn_dq: grid (Hq, ntiles), 256 * G threads; G key groups split the query
-// tile's key tiles like attn_fwd and their dQ partials are summed in a fixed
-// order (group 0 + group 1).  Also writes dvec = D_i = dO_i . O_i for
-// attn_dkdv.  tiles == nullptr: one sequence, longest tiles first.
+// Backward, two launches:
+//   attn_dkdv   grid (Hq/Hkv, Hkv, ntiles in key order): per (query head, key
+//               tile) the head's dK/dV partial; it also forms D_i = dO_i.O_i
+//               for every query tile it stages and, for the tile holding its
+//               own keys, writes D to dvec.
+//   attn_dq     grid (Hq/Hkv, Hkv, ntiles + nred): z < ntiles is the dQ of a
+//               (query head, query tile), reading D from dvec; z >= ntiles
+//               are reduction workgroups that sum the group's dK/dV partials
+//               in ascending head order (CausalAttentionKernel.cs:184-206),
+//               apply the inverse RoPE to dK and write dk/dv.  They run on
+//               the CUs freed by the short dQ tiles.
+// G groups of 4 waves split a tile's loop (2 in the bf16 mode, 1 in fp32);
+// their partial sums are added in group order.
 // ---------------------------------------------------------------------------
 template <typename T>
 constexpr int bwd_groups() {
   return sizeof(T) == 2 ? 2 : 1;
 }
 
-template <typename IO, typename T, int D>
+// Rows of the (token, kv head) space that one reduction workgroup finishes.
+constexpr int kRedRows = 16;
+
+template <typename IO, int D>
+__device__ inline void dkdv_reduce_rows(const float* __restrict__ wk,
+                                        const float* __restrict__ wv, IO* __restrict__ dk,
+                                        IO* __restrict__ dv, const int32_t* __restrict__ pos_of,
+                                        int total_tokens, int ratio, int n_heads_kv, int unit,
+                                        const float* __restrict__ cos_t,
+                                        const float* __restrict__ sin_t) {
+  constexpr int H = D / 2;
+  constexpr int CH = H / 4;  // 4-pair chunks per row
+  const int item = threadIdx.x;
+  if (item >= kRedRows * CH) return;
+  const long row = (long)unit * kRedRows + item / CH;  // token * Hkv + kv head
+  if (row >= (long)total_tokens * n_heads_kv) return;
+  const int p0 = 4 * (item % CH);
+  const long tok = row / n_heads_kv;
+  const int j = (int)(row % n_heads_kv);
+  const int n_heads_q = ratio * n_heads_kv;
+  f32x4 k0 = {0.0f, 0.0f, 0.0f, 0.0f}, k1 = k0, v0 = k0, v1 = k0;
+  for (int hh = 0; hh < ratio; ++hh) {
+    const long src = (tok * n_heads_q + (long)j * ratio + hh) * D + p0;
+    k0 += *reinterpret_cast<const f32x4*>(wk + src);
+    k1 += *reinterpret_cast<const f32x4*>(wk + src + H);
+    v0 += *reinterpret_cast<const f32x4*>(wv + src);
+    v1 += *reinterpret_cast<const f32x4*>(wv + src + H);
+  }
+  const long pos = pos_of != nullptr ? pos_of[tok] : tok;
+  const f32x4 cs = *reinterpret_cast<const f32x4*>(cos_t + pos * H + p0);
+  const f32x4 sn = *reinterpret_cast<const f32x4*>(sin_t + pos * H + p0);
+  f32x4 y0, y1;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    float a, b;
+    rope_inv(k0[e], k1[e], cs[e], sn[e], a, b);
+    y0[e] = a;
+    y1[e] = b;
+  }
+  const long dst = row * D + p0;
+  store4(dk + dst, y0);
+  store4(dk + dst + H, y1);
+  store4(dv + dst, v0);
+  store4(dv + dst + H, v1);
+}
+
+template <typename IO, typename T, int D, bool VARLEN>
 __global__ __launch_bounds__(kThreads * bwd_groups<T>()) void attn_dq_kernel(
     const IO* __restrict__ q_rot, const IO* __restrict__ d_out,
-    const IO* __restrict__ out, const IO* __restrict__ k_rot,
-    const IO* __restrict__ v, const float* __restrict__ lse,
-    float* __restrict__ dvec, IO* __restrict__ dq,
-    const TileDesc* __restrict__ tiles, int n_tiles, int n_heads_q, int n_heads_kv,
-    int total_tokens, float scale_log2, float scale,
-    const float* __restrict__ cos_t, const float* __restrict__ sin_t) {
+    const IO* __restrict__ k_rot, const IO* __restrict__ v, const float* __restrict__ lse,
+    const float* __restrict__ dvec, IO* __restrict__ dq, const TileDesc* __restrict__ tiles,
+    int n_tiles, int total_tokens, float scale_log2, float scale,
+    const float* __restrict__ cos_t, const float* __restrict__ sin_t,
+    const float* __restrict__ wk, const float* __restrict__ wv, IO* __restrict__ dk,
+    IO* __restrict__ dv, const int32_t* __restrict__ pos_of) {
   using M = Mfma<T>;
   using L = Lds<T, D>;
   constexpr int G = bwd_groups<T>();
@@ -643,11 +666,16 @@ __global__ __launch_bounds__(kThreads * bwd_groups<T>()) void attn_dq_kernel(
   extern __shared__ __align__(16) unsigned char smem_raw[];
   T* const lds = reinterpret_cast<T*>(smem_raw);  // [G][2 buffers][K tile, V tile]
 
-  const int h = blockIdx.x;
-  const TileDesc td = tiles != nullptr
-                          ? tiles[blockIdx.y]
-                          : TileDesc{0, total_tokens, n_tiles - 1 - (int)blockIdx.y, 0};
-  const int kvh = h / (n_heads_q / n_heads_kv);
+  const int ratio = gridDim.x, n_heads_kv = gridDim.y, n_heads_q = ratio * n_heads_kv;
+  const int kvh = blockIdx.y, h = kvh * ratio + blockIdx.x;
+  if ((int)blockIdx.z >= n_tiles) {
+    const int unit = ((int)blockIdx.z - n_tiles) * n_heads_q + h;
+    dkdv_reduce_rows<IO, D>(wk, wv, dk, dv, VARLEN ? pos_of : nullptr, total_tokens, ratio,
+                            n_heads_kv, unit, cos_t, sin_t);
+    return;
+  }
+  const TileDesc td = VARLEN ? tiles[blockIdx.z]
+                             : TileDesc{0, total_tokens, n_tiles - 1 - (int)blockIdx.z, 0};
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int grp = w >> 2, wq = w & 3, gtid = tid & (kThreads - 1);
   const int g = lane >> 4, c = lane & 15;
@@ -667,21 +695,13 @@ __global__ __launch_bounds__(kThreads * bwd_groups<T>()) void attn_dq_kernel(
   }
 
   typename M::Frag qf[NKD], df[NKD];
-  float dot = 0.0f;
 #pragma unroll
   for (int kk = 0; kk < NKD; ++kk) {
     qf[kk] = qvalid ? frag_global<T>(q_rot + qbase, kk, g) : frag_zero<T>();
     df[kk] = qvalid ? frag_global<T>(d_out + qbase, kk, g) : frag_zero<T>();
-    if (qvalid) {  // D_i partial over this lane's columns, in the caller's precision
-      const IO* po = out + qbase + kk * M::KSTEP + M::KPL * g;
-      const IO* pd = d_out + qbase + kk * M::KSTEP + M::KPL * g;
-#pragma unroll
-      for (int e = 0; e < M::KPL; ++e) dot += to_f32(pd[e]) * to_f32(po[e]);
-    }
   }
-  const float drow = col_sum(dot);
   const long si = (long)h * total_tokens + td.tok0 + qrow;
-  if (grp == 0 && qvalid && g == 0) dvec[si] = drow;
+  const float drow = qvalid ? dvec[si] : 0.0f;
   const float nlse2 = qvalid ? -lse[si] * kLog2e : 0.0f;
 
   f32x4 acc_dq[D / 16];
@@ -744,19 +764,15 @@ __global__ __launch_bounds__(kThreads * bwd_groups<T>()) void attn_dq_kernel(
   }
 
   if constexpr (G == 2) {
-    float* cmb = reinterpret_cast<float*>(lds + 4 * L::TILE) + wq * (D / 4) * 64 + lane;
+    f32x4* const cmb = reinterpret_cast<f32x4*>(lds + 4 * L::TILE) + wq * (D / 16) * 64 + lane;
     if (grp == 1) {
 #pragma unroll
-      for (int db = 0; db < D / 16; ++db)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) cmb[(4 * db + r) * 64] = acc_dq[db][r];
+      for (int db = 0; db < D / 16; ++db) cmb[db * 64] = acc_dq[db];
     }
     __syncthreads();
     if (grp == 1) return;
 #pragma unroll
-    for (int db = 0; db < D / 16; ++db)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) acc_dq[db][r] += cmb[(4 * db + r) * 64];
+    for (int db = 0; db < D / 16; ++db) acc_dq[db] += cmb[db * 64];
   }
 
   if (qvalid) {
@@ -779,32 +795,24 @@ __global__ __launch_bounds__(kThreads * bwd_groups<T>()) void attn_dq_kernel(
   }
 }
 
-// ---------------------------------------------------------------------------
-// attn_dkdv: grid (Hq, ntiles in key order), 256 * G threads; G query groups
-// split the key tile's query tiles (group grp takes td.tile + grp, + G, ...),
-// each double-buffering its own Q tile, dO tile and 64 lse / 64 D values in
-// LDS; the partial dK/dV are summed in a fixed order at the end.
-// tiles == nullptr: one sequence, key tile 0 (the most query tiles) first.
-// ---------------------------------------------------------------------------
-template <typename IO, typename T, int D>
+template <typename IO, typename T, int D, bool VARLEN>
 __global__ __launch_bounds__(kThreads * bwd_groups<T>()) void attn_dkdv_kernel(
-    const IO* __restrict__ q_rot, const IO* __restrict__ d_out,
-    const IO* __restrict__ k_rot, const IO* __restrict__ v,
-    const float* __restrict__ lse, const float* __restrict__ dvec,
-    float* __restrict__ wk, float* __restrict__ wv,
-    const TileDesc* __restrict__ tiles, int n_tiles, int n_heads_q, int n_heads_kv,
-    int total_tokens, float scale_log2, float scale) {
+    const IO* __restrict__ q_rot, const IO* __restrict__ d_out, const IO* __restrict__ out,
+    const IO* __restrict__ k_rot, const IO* __restrict__ v, const float* __restrict__ lse,
+    float* __restrict__ dvec, float* __restrict__ wk, float* __restrict__ wv,
+    const TileDesc* __restrict__ tiles, int n_tiles, int total_tokens, float scale_log2,
+    float scale) {
   using M = Mfma<T>;
   using L = Lds<T, D>;
+  using Regs = TileRegs<IO, D>;
   constexpr int G = bwd_groups<T>();
   constexpr int NKD = D / M::KSTEP;
   constexpr int BUF = 2 * L::TILE * sizeof(T) + 2 * kTile * sizeof(float);  // bytes
   extern __shared__ __align__(16) unsigned char smem_raw[];
 
-  const int h = blockIdx.x;
-  const TileDesc td = tiles != nullptr ? tiles[blockIdx.y]
-                                       : TileDesc{0, total_tokens, (int)blockIdx.y, 0};
-  const int kvh = h / (n_heads_q / n_heads_kv);
+  const int ratio = gridDim.x, n_heads_kv = gridDim.y, n_heads_q = ratio * n_heads_kv;
+  const int kvh = blockIdx.y, h = kvh * ratio + blockIdx.x;
+  const TileDesc td = VARLEN ? tiles[blockIdx.z] : TileDesc{0, total_tokens, (int)blockIdx.z, 0};
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int grp = w >> 2, wq = w & 3, gtid = tid & (kThreads - 1);
   const int g = lane >> 4, c = lane & 15;
@@ -817,32 +825,47 @@ __global__ __launch_bounds__(kThreads * bwd_groups<T>()) void attn_dkdv_kernel(
   const long qstride = (long)n_heads_q * D;
   const IO* qb = q_rot + ((long)td.tok0 * n_heads_q + h) * D;
   const IO* dob = d_out + ((long)td.tok0 * n_heads_q + h) * D;
+  const IO* ob = out + ((long)td.tok0 * n_heads_q + h) * D;
   const float* lseb = lse + (long)h * total_tokens + td.tok0;
-  const float* dvb = dvec + (long)h * total_tokens + td.tok0;
+  float* const dvb = dvec + (long)h * total_tokens + td.tok0;
 
-  // Stage one query tile: Q, dO rows into registers, -lse*log2(e) or D into
-  // one float (rows past the sequence get -inf / 0, so their P and dS are 0).
-  TileRegs<IO, D> qreg, dreg;
-  float vecv = 0.0f;
+  // Stage one query tile: Q, dO and O rows into registers, -lse*log2(e)
+  // (-inf past the sequence, so P and dS are 0 there) into one float.
+  Regs qreg, dreg, oreg;
+  float nlse = 0.0f;
   auto load_tile = [&](int qt) {
     const long roff = (long)kTile * qt * qstride;
     const int nv = td.len - kTile * qt;
     qreg.load(qb + roff, qstride, nv, gtid);
     dreg.load(dob + roff, qstride, nv, gtid);
-    if (gtid < 2 * kTile) {
-      const int r = gtid & (kTile - 1);
-      if (gtid < kTile)
-        vecv = r < nv ? -lseb[kTile * qt + r] * kLog2e : -INFINITY;
-      else
-        vecv = r < nv ? dvb[kTile * qt + r] : 0.0f;
-    }
+    oreg.load(ob + roff, qstride, nv, gtid);
+    if (gtid < kTile) nlse = gtid < nv ? -lseb[kTile * qt + gtid] * kLog2e : -INFINITY;
   };
-  auto store_tile = [&](int buf) {
+  // ... and write it to LDS buffer `buf` with D_i = dO_i . O_i (the row's
+  // CPR chunks sit on CPR consecutive lanes; summed in a fixed order).
+  auto store_tile = [&](int buf, int qt) {
     unsigned char* base = gsm + buf * BUF;
     qreg.store(reinterpret_cast<T*>(base), gtid);
     dreg.store(reinterpret_cast<T*>(base) + L::TILE, gtid);
-    if (gtid < 2 * kTile)
-      reinterpret_cast<float*>(base + 2 * L::TILE * sizeof(T))[gtid] = vecv;
+    float* vec = reinterpret_cast<float*>(base + 2 * L::TILE * sizeof(T));
+    if (gtid < kTile) vec[gtid] = nlse;
+#pragma unroll
+    for (int i = 0; i < Regs::N; ++i) {
+      float xd[8], xo[8];
+      load8(reinterpret_cast<const IO*>(&dreg.w[i][0]), xd);
+      load8(reinterpret_cast<const IO*>(&oreg.w[i][0]), xo);
+      float part = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) part += xd[e] * xo[e];
+#pragma unroll
+      for (int m = 1; m < Regs::CPR; m <<= 1) part += __shfl_xor(part, m);
+      const int idx = gtid + i * kThreads;
+      const int r = idx / Regs::CPR;
+      if (idx % Regs::CPR == 0) {
+        vec[kTile + r] = part;
+        if (qt == td.tile && kTile * qt + r < td.len) dvb[kTile * qt + r] = part;
+      }
+    }
   };
 
   const int first = td.tile + grp;
@@ -895,7 +918,7 @@ __global__ __launch_bounds__(kThreads * bwd_groups<T>()) void attn_dkdv_kernel(
     acc_rows<T, D>(acc_dk, qs, ds, 4, lane);
   };
 
-  if (first < ntq) store_tile(0);
+  if (first < ntq) store_tile(0, first);
   __syncthreads();
 
   const int nit = (ntq - td.tile + G - 1) / G;  // iterations of group 0 (the most)
@@ -908,30 +931,26 @@ __global__ __launch_bounds__(kThreads * bwd_groups<T>()) void attn_dkdv_kernel(
       step(base, std::true_type{});
     else if (qt < ntq)
       step(base, std::false_type{});
-    if (more) store_tile((it + 1) & 1);
+    if (more) store_tile((it + 1) & 1, qt + G);
     __syncthreads();
   }
 
   if constexpr (G == 2) {
-    float* cmb = reinterpret_cast<float*>(smem_raw + 2 * BUF) + wq * (D / 2) * 64 + lane;
+    f32x4* const cmb = reinterpret_cast<f32x4*>(smem_raw + 2 * BUF) + wq * (D / 8) * 64 + lane;
     if (grp == 1) {
 #pragma unroll
-      for (int db = 0; db < D / 16; ++db)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          cmb[(4 * db + r) * 64] = acc_dk[db][r];
-          cmb[(D / 4 + 4 * db + r) * 64] = acc_dv[db][r];
-        }
+      for (int db = 0; db < D / 16; ++db) {
+        cmb[db * 64] = acc_dk[db];
+        cmb[(D / 16 + db) * 64] = acc_dv[db];
+      }
     }
     __syncthreads();
     if (grp == 1) return;
 #pragma unroll
-    for (int db = 0; db < D / 16; ++db)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        acc_dk[db][r] += cmb[(4 * db + r) * 64];
-        acc_dv[db][r] += cmb[(D / 4 + 4 * db + r) * 64];
-      }
+    for (int db = 0; db < D / 16; ++db) {
+      acc_dk[db] += cmb[db * 64];
+      acc_dv[db] += cmb[(D / 16 + db) * 64];
+    }
   }
 
   if (kvalid) {
@@ -942,41 +961,6 @@ __global__ __launch_bounds__(kThreads * bwd_groups<T>()) void attn_dkdv_kernel(
       store4(wv + wb + 16 * db + 4 * g, acc_dv[db]);
     }
   }
-}
-
-// ---------------------------------------------------------------------------
-// dkdv_reduce: one thread per (token, kv head, pair p < D/2).
-// ---------------------------------------------------------------------------
-template <typename IO, int D>
-__global__ __launch_bounds__(kThreads) void dkdv_reduce_kernel(
-    const float* __restrict__ wk, const float* __restrict__ wv,
-    IO* __restrict__ dk, IO* __restrict__ dv, const int32_t* __restrict__ pos_of,
-    int total_tokens, int n_heads_q, int n_heads_kv,
-    const float* __restrict__ cos_t, const float* __restrict__ sin_t) {
-  constexpr int H = D / 2;
-  const long idx = (long)blockIdx.x * kThreads + threadIdx.x;
-  const long n = (long)total_tokens * n_heads_kv * H;
-  if (idx >= n) return;
-  const int p = idx % H;
-  const int j = (idx / H) % n_heads_kv;
-  const long tok = idx / ((long)H * n_heads_kv);
-  const int ratio = n_heads_q / n_heads_kv;
-  float k0 = 0.0f, k1 = 0.0f, v0 = 0.0f, v1 = 0.0f;
-  for (int hh = 0; hh < ratio; ++hh) {
-    const long src = (tok * n_heads_q + (long)j * ratio + hh) * D;
-    k0 += wk[src + p];
-    k1 += wk[src + p + H];
-    v0 += wv[src + p];
-    v1 += wv[src + p + H];
-  }
-  const int pos = pos_of[tok];
-  float y0, y1;
-  rope_inv(k0, k1, cos_t[(long)pos * H + p], sin_t[(long)pos * H + p], y0, y1);
-  const long dst = (tok * n_heads_kv + j) * D;
-  dk[dst + p] = from_f32<IO>(y0);
-  dk[dst + p + H] = from_f32<IO>(y1);
-  dv[dst + p] = from_f32<IO>(v0);
-  dv[dst + p + H] = from_f32<IO>(v1);
 }
 
 // ---------------------------------------------------------------------------
@@ -1030,17 +1014,16 @@ hipError_t forward_impl(const FwdLaunch& a, hipStream_t st, KernelTimer* tm) {
     GL_CHECK(hipGetLastError());
   }
   if constexpr (sizeof(T) == 2) {
-    auto fn = attn_fwd_bf16_kernel<IO, D>;
+    auto fn = a.single_seq ? attn_fwd_bf16_kernel<IO, D, false> : attn_fwd_bf16_kernel<IO, D, true>;
     constexpr size_t lds = fwd_bf16_lds<D>();
     GL_CHECK(allow_lds(fn, lds));
     ScopedTiming t(tm, kKernFwd, st);
-    hipLaunchKernelGGL(fn, dim3(a.n_heads_q, a.n_tiles), dim3(kFwdThreads), lds, st,
-                       static_cast<const IO*>(a.q), static_cast<const bf16*>(a.kc),
+    hipLaunchKernelGGL(fn, dim3(a.n_heads_q / a.n_heads_kv, a.n_heads_kv, a.n_tiles),
+                       dim3(kFwdThreads), lds, st, static_cast<const IO*>(a.q),
+                       static_cast<const bf16*>(a.kc),
                        static_cast<const bf16*>(a.vc != nullptr ? a.vc : a.v),
-                       static_cast<IO*>(a.out), a.lse,
-                       static_cast<IO*>(a.q_rot), a.single_seq ? nullptr : a.tiles_fwd,
-                       a.n_tiles, a.n_heads_q, a.n_heads_kv, a.total_tokens, a.scale_log2,
-                       a.cos_t, a.sin_t);
+                       static_cast<IO*>(a.out), a.lse, static_cast<IO*>(a.q_rot), a.tiles_fwd,
+                       a.n_tiles, a.total_tokens, a.scale_log2, a.cos_t, a.sin_t);
     GL_CHECK(hipGetLastError());
   } else {
     auto fn = attn_fwd_kernel<IO, T, D>;
@@ -1060,41 +1043,35 @@ hipError_t forward_impl(const FwdLaunch& a, hipStream_t st, KernelTimer* tm) {
 
 template <typename IO, typename T, int D>
 hipError_t backward_impl(const BwdLaunch& a, hipStream_t st, KernelTimer* tm) {
-  const dim3 blk(kThreads);
+  const int ratio = a.n_heads_q / a.n_heads_kv;
+  const dim3 blk(kThreads * bwd_groups<T>());
   const IO* q_rot = static_cast<const IO*>(a.q_rot);
   const IO* k_rot = static_cast<const IO*>(a.k_rot);
   const IO* v = static_cast<const IO*>(a.v);
   const IO* d_out = static_cast<const IO*>(a.d_out);
   {
-    auto fn = attn_dq_kernel<IO, T, D>;
-    constexpr size_t lds = dq_lds<T, D>();
-    GL_CHECK(allow_lds(fn, lds));
-    ScopedTiming t(tm, kKernDq, st);
-    hipLaunchKernelGGL(fn, dim3(a.n_heads_q, a.n_tiles), dim3(kThreads * bwd_groups<T>()), lds,
-                       st, q_rot, d_out, static_cast<const IO*>(a.out), k_rot, v, a.lse,
-                       a.dvec, static_cast<IO*>(a.dq), a.single_seq ? nullptr : a.tiles_fwd,
-                       a.n_tiles, a.n_heads_q, a.n_heads_kv, a.total_tokens, a.scale_log2,
-                       a.scale, a.cos_t, a.sin_t);
-    GL_CHECK(hipGetLastError());
-  }
-  {
-    auto fn = attn_dkdv_kernel<IO, T, D>;
+    auto fn = a.single_seq ? attn_dkdv_kernel<IO, T, D, false> : attn_dkdv_kernel<IO, T, D, true>;
     constexpr size_t lds = dkdv_lds<T, D>();
     GL_CHECK(allow_lds(fn, lds));
     ScopedTiming t(tm, kKernDkdv, st);
-    hipLaunchKernelGGL(fn, dim3(a.n_heads_q, a.n_tiles), dim3(kThreads * bwd_groups<T>()), lds,
-                       st, q_rot, d_out, k_rot, v, a.lse, a.dvec, a.wk, a.wv,
-                       a.single_seq ? nullptr : a.tiles_kv, a.n_tiles, a.n_heads_q,
-                       a.n_heads_kv, a.total_tokens, a.scale_log2, a.scale);
+    hipLaunchKernelGGL(fn, dim3(ratio, a.n_heads_kv, a.n_tiles), blk, lds, st, q_rot, d_out,
+                       static_cast<const IO*>(a.out), k_rot, v, a.lse, a.dvec, a.wk, a.wv,
+                       a.tiles_kv, a.n_tiles, a.total_tokens, a.scale_log2, a.scale);
     GL_CHECK(hipGetLastError());
   }
   {
-    const long n = (long)a.total_tokens * a.n_heads_kv * (D / 2);
-    const unsigned grid = static_cast<unsigned>((n + kThreads - 1) / kThreads);
-    ScopedTiming t(tm, kKernReduce, st);
-    hipLaunchKernelGGL((dkdv_reduce_kernel<IO, D>), dim3(grid), blk, 0, st, a.wk, a.wv,
-                       static_cast<IO*>(a.dk), static_cast<IO*>(a.dv), a.pos_of,
-                       a.total_tokens, a.n_heads_q, a.n_heads_kv, a.cos_t, a.sin_t);
+    auto fn = a.single_seq ? attn_dq_kernel<IO, T, D, false> : attn_dq_kernel<IO, T, D, true>;
+    constexpr size_t lds = dq_lds<T, D>();
+    GL_CHECK(allow_lds(fn, lds));
+    // reduction workgroups: kRedRows (token, kv head) rows each, a.n_heads_q per z-slice
+    const long rows = (long)a.total_tokens * a.n_heads_kv;
+    const long units = (rows + kRedRows - 1) / kRedRows;
+    const int nred = static_cast<int>((units + a.n_heads_q - 1) / a.n_heads_q);
+    ScopedTiming t(tm, kKernDq, st);
+    hipLaunchKernelGGL(fn, dim3(ratio, a.n_heads_kv, a.n_tiles + nred), blk, lds, st, q_rot,
+                       d_out, k_rot, v, a.lse, a.dvec, static_cast<IO*>(a.dq), a.tiles_fwd,
+                       a.n_tiles, a.total_tokens, a.scale_log2, a.scale, a.cos_t, a.sin_t,
+                       a.wk, a.wv, static_cast<IO*>(a.dk), static_cast<IO*>(a.dv), a.pos_of);
     GL_CHECK(hipGetLastError());
   }
   return hipSuccess;

@@ -33,10 +33,9 @@ constexpr int kPrecBf16 = 1;
 enum KernelId : int {
   kKernRopeK = 0,
   kKernFwd = 1,
-  kKernDq = 2,
-  kKernDkdv = 3,
-  kKernReduce = 4,
-  kKernCount = 5,
+  kKernDkdv = 2,
+  kKernDq = 3,
+  kKernCount = 4,
 };
 
 // Optional per-kernel hipEvent timing on the launch stream.

@@ -447,7 +447,7 @@ int guarded(F&& f) {
 }
 
 const char* const kKernelNames[kKernCount] = {
-    "rope_k", "attn_fwd", "attn_bwd_dq", "attn_bwd_dkdv", "dkdv_reduce",
+    "rope_k", "attn_fwd", "attn_bwd_dkdv", "attn_bwd_dq",
 };
 
 }  // namespace
