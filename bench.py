@@ -89,6 +89,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="qwen7b_s512", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="first run 5 plain device copies of MIB MiB (a known-size kernel that "
+                         "calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; use --gpus 1 "
@@ -104,6 +107,13 @@ def main():
     T = sum(lengths)
     cu = None if len(lengths) == 1 else np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
     dev = torch.device("cuda:0")
+    if args.copy_probe > 0:
+        src = torch.ones(args.copy_probe << 18, device=dev, dtype=torch.float32)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     g = torch.Generator(device=dev).manual_seed(0)
     q = torch.randn(T, Hq, D, device=dev, generator=g).bfloat16()
     k = torch.randn(T, Hkv, D, device=dev, generator=g).bfloat16()

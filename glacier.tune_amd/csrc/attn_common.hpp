@@ -276,6 +276,23 @@ __device__ inline void acc_rows(f32x4 (&acc)[D / 16], const T* tile,
   }
 }
 
+// Sum over groups of N (8, 16 or 32) consecutive lanes: DPP lane moves
+// (quad xor 1, quad xor 2, half-row mirror, row mirror) run at ALU speed;
+// only N = 32 needs one cross-row permute.  Every lane of a group ends with
+// the same bits (each step adds two equal-order partial sums).
+template <int N>
+__device__ inline float lanes_sum(float x) {
+  static_assert(N == 8 || N == 16 || N == 32, "8-, 16- or 32-lane groups");
+  // (the DPP control operand must be a literal)
+  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0xB1, 0xF, 0xF, false));
+  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x4E, 0xF, 0xF, false));
+  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x141, 0xF, 0xF, false));
+  if constexpr (N >= 16)
+    x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x140, 0xF, 0xF, false));
+  if constexpr (N == 32) x += __shfl_xor(x, 16);
+  return x;
+}
+
 // Sum over the 4 lanes that share a column (xor 16, xor 32), in a fixed
 // order so every lane gets the same bits.
 __device__ inline float col_sum(float x) {

@@ -857,8 +857,7 @@ __global__ __launch_bounds__(kThreads * bwd_groups<T>()) void attn_dkdv_kernel(
       float part = 0.0f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) part += xd[e] * xo[e];
-#pragma unroll
-      for (int m = 1; m < Regs::CPR; m <<= 1) part += __shfl_xor(part, m);
+      part = lanes_sum<Regs::CPR>(part);
       const int idx = gtid + i * kThreads;
       const int r = idx / Regs::CPR;
       if (idx % Regs::CPR == 0) {
@@ -935,30 +934,50 @@ __global__ __launch_bounds__(kThreads * bwd_groups<T>()) void attn_dkdv_kernel(
     __syncthreads();
   }
 
+  // Merge the groups and write whole rows: the [64 keys][D] fp32 dK and dV
+  // tiles are staged in LDS (row stride D + 4 floats, so the 16 key rows of
+  // a wave's store fall in distinct banks), then every thread stores 16-byte
+  // pieces of consecutive rows.  Lane (g, c) holds d = 16 db + 4 g + 0..3 of
+  // key 16 wq + c.
+  constexpr int SR = D + 4;
+  static_assert(2 * kTile * SR * sizeof(float) <= 2 * BUF * G, "staging exceeds the LDS buffers");
+  float* const stk = reinterpret_cast<float*>(smem_raw);
+  float* const stv = stk + kTile * SR;
+  f32x4* const pk = reinterpret_cast<f32x4*>(stk + (16 * wq + c) * SR + 4 * g);
+  f32x4* const pv = reinterpret_cast<f32x4*>(stv + (16 * wq + c) * SR + 4 * g);
   if constexpr (G == 2) {
-    f32x4* const cmb = reinterpret_cast<f32x4*>(smem_raw + 2 * BUF) + wq * (D / 8) * 64 + lane;
     if (grp == 1) {
 #pragma unroll
       for (int db = 0; db < D / 16; ++db) {
-        cmb[db * 64] = acc_dk[db];
-        cmb[(D / 16 + db) * 64] = acc_dv[db];
+        pk[4 * db] = acc_dk[db];
+        pv[4 * db] = acc_dv[db];
       }
     }
     __syncthreads();
-    if (grp == 1) return;
+    if (grp == 0) {
+#pragma unroll
+      for (int db = 0; db < D / 16; ++db) {
+        pk[4 * db] = (acc_dk[db] + pk[4 * db]) * scale;
+        pv[4 * db] = acc_dv[db] + pv[4 * db];
+      }
+    }
+  } else {
 #pragma unroll
     for (int db = 0; db < D / 16; ++db) {
-      acc_dk[db] += cmb[db * 64];
-      acc_dv[db] += cmb[(D / 16 + db) * 64];
+      pk[4 * db] = acc_dk[db] * scale;
+      pv[4 * db] = acc_dv[db];
     }
   }
-
-  if (kvalid) {
-    const long wb = ((long)(td.tok0 + krow) * n_heads_q + h) * D;
+  __syncthreads();
+  constexpr int V4 = D / 4;  // 16-byte pieces per row
 #pragma unroll
-    for (int db = 0; db < D / 16; ++db) {
-      store4(wk + wb + 16 * db + 4 * g, acc_dk[db] * scale);
-      store4(wv + wb + 16 * db + 4 * g, acc_dv[db]);
+  for (int i = tid; i < kTile * V4; i += kThreads * G) {
+    const int r = i / V4, c4 = i % V4;
+    const int key = kTile * td.tile + r;
+    if (key < td.len) {
+      const long wb = ((long)(td.tok0 + key) * n_heads_q + h) * D + 4 * c4;
+      store4(wk + wb, *reinterpret_cast<const f32x4*>(stk + r * SR + 4 * c4));
+      store4(wv + wb, *reinterpret_cast<const f32x4*>(stv + r * SR + 4 * c4));
     }
   }
 }
