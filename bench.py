@@ -40,9 +40,9 @@ CONFIGS = {
 }
 
 # Algorithmic FLOPs per unmasked (query, key, head) triple, per kernel: the
-# forward does QK^T and PV (4 D); the dK/dV kernel is credited with dP, dV,
-# dK (6 D) and the dQ kernel with dQ (2 D).  Sum: 12 D.
-FLOPS_PER_PAIR = {"attn_fwd": 4, "attn_bwd_dkdv": 6, "attn_bwd_dq": 2}
+# forward does QK^T and PV (4 D); the backward kernel dP, dV, dK and dQ (8 D);
+# rope_k and the dK/dV head reduction are credited with none.  Sum: 12 D.
+FLOPS_PER_PAIR = {"attn_fwd": 4, "attn_bwd": 8, "rope_k": 0, "attn_bwd_reduce": 0}
 
 
 def pairs(lengths):

@@ -36,6 +36,11 @@ using bf16 = __bf16;
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// Word 3 of a raw buffer resource on gfx9-family GPUs: 32-bit data format
+// (a zero format would make every load return 0), no swizzle, no stride.
+constexpr int kBufferWord3 = 0x00020000;
 
 #define GLACIER_LDS __attribute__((address_space(3)))
 
@@ -124,29 +129,34 @@ struct TileRegs {
   static constexpr int N = kTile * CPR / NT;         // chunks per thread
   static constexpr int W = 8 * sizeof(IO) / 16;      // 16-byte words per chunk
   static_assert(N * NT == kTile * CPR, "tile must split evenly");
-  uint4 w[N][W];
+  i32x4 w[N][W];
 
-  // Rows r >= nvalid are zero (past the end of the sequence).  nvalid is
-  // uniform, so a full tile takes the branch-free path.
+  // Rows r >= nvalid read as zero (past the end of the sequence): the loads
+  // go through a buffer resource whose range ends with row nvalid - 1, and
+  // the hardware returns 0 for offsets beyond it.  Full and partial tiles
+  // share one branch-free code path.  (With a separate bounds-checked path
+  // writing the same registers, the compiler has to drain each tile's loads
+  // before issuing the next tile's, serialising the memory round trips.)
+  // src, gstride and nvalid must be uniform over the wave (they are read
+  // from its first lane).
   __device__ inline void load(const IO* src, long gstride, int nvalid, int tid) {
-    if (nvalid >= kTile) {
-#pragma unroll
-      for (int i = 0; i < N; ++i) {
-        const int idx = tid + i * NT;
-        const int r = idx / CPR, ch = idx % CPR;
-        const uint4* p = reinterpret_cast<const uint4*>(src + (long)r * gstride + ch * 8);
-#pragma unroll
-        for (int j = 0; j < W; ++j) w[i][j] = p[j];
-      }
-      return;
-    }
+    const int rowb = __builtin_amdgcn_readfirstlane(static_cast<int>(gstride * (long)sizeof(IO)));
+    const int nv = nvalid < kTile ? nvalid : kTile;
+    const int nrec = __builtin_amdgcn_readfirstlane(
+        nv <= 0 ? 0 : (nv - 1) * rowb + D * static_cast<int>(sizeof(IO)));
+    const unsigned long long a = reinterpret_cast<unsigned long long>(src);
+    const unsigned long long au =
+        (static_cast<unsigned long long>(__builtin_amdgcn_readfirstlane(static_cast<int>(a >> 32))) << 32) |
+        static_cast<unsigned>(__builtin_amdgcn_readfirstlane(static_cast<int>(a & 0xffffffffu)));
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        reinterpret_cast<void*>(au), (short)0, nrec, kBufferWord3);
 #pragma unroll
     for (int i = 0; i < N; ++i) {
       const int idx = tid + i * NT;
       const int r = idx / CPR, ch = idx % CPR;
-      const uint4* p = reinterpret_cast<const uint4*>(src + (long)r * gstride + ch * 8);
+      const int off = r * rowb + ch * 8 * static_cast<int>(sizeof(IO));
 #pragma unroll
-      for (int j = 0; j < W; ++j) w[i][j] = r < nvalid ? p[j] : make_uint4(0, 0, 0, 0);
+      for (int j = 0; j < W; ++j) w[i][j] = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16 * j, 0, 0);
     }
   }
 
@@ -161,7 +171,7 @@ struct TileRegs {
       T* dst = lds + r * S + ch * 8;
       if constexpr (sizeof(IO) == sizeof(T)) {
 #pragma unroll
-        for (int j = 0; j < W; ++j) reinterpret_cast<uint4*>(dst)[j] = w[i][j];
+        for (int j = 0; j < W; ++j) reinterpret_cast<i32x4*>(dst)[j] = w[i][j];
       } else {
         float x[8];
         load8(reinterpret_cast<const IO*>(&w[i][0]), x);
@@ -275,6 +285,23 @@ __device__ inline void acc_rows(f32x4 (&acc)[D / 16], const T* tile,
     }
   }
 }
+
+// Index of this wave in the workgroup, as a scalar: the compiler cannot
+// prove threadIdx.x / 64 uniform, and values derived from it (the group's
+// tile, its base pointers) must live in scalar registers to form buffer
+// resources without a per-lane loop.
+__device__ inline int wave_id() {
+  return __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+}
+
+// s_waitcnt vmcnt(0): wait for every outstanding vector-memory access of
+// this wave (expcnt and lgkmcnt fields at their maxima, i.e. not waited on).
+// Issued at the end of a kernel prologue it tells the compiler's wait
+// tracking that the prologue's conditional loads (operand fragments kept in
+// registers for the whole loop) are complete on every path; otherwise it
+// guards their first use inside the loop with a wait that also drains the
+// loop's own prefetch loads.
+__device__ inline void wait_vmem_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 // Sum over groups of N (8, 16 or 32) consecutive lanes: DPP lane moves
 // (quad xor 1, quad xor 2, half-row mirror, row mirror) run at ALU speed;

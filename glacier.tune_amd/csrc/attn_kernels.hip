@@ -132,7 +132,7 @@ __global__ __launch_bounds__(kThreads * fwd_groups<T>()) void attn_fwd_kernel(
                           ? tiles[blockIdx.y]
                           : TileDesc{0, total_tokens, n_tiles - 1 - (int)blockIdx.y, 0};
   const int kvh = h / (n_heads_q / n_heads_kv);
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, w = wave_id(), lane = tid & 63;
   const int grp = w >> 2, wq = w & 3, gtid = tid & (kThreads - 1);
   const int g = lane >> 4, c = lane & 15;
   const int qrow = kTile * td.tile + 16 * wq + c;
@@ -373,7 +373,7 @@ __global__ __launch_bounds__(kFwdThreads) void attn_fwd_bf16_kernel(
   const int kvh = blockIdx.y, h = kvh * gridDim.x + blockIdx.x;
   const TileDesc td = VARLEN ? tiles[blockIdx.z]
                              : TileDesc{0, total_tokens, n_tiles - 1 - (int)blockIdx.z, 0};
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, w = wave_id(), lane = tid & 63;
   const int grp = w >> 2, wq = w & 3, gtid = tid & (GT - 1);
   const int g = lane >> 4, c = lane & 15;
   const int qrow = kTile * td.tile + 16 * wq + c;
@@ -442,6 +442,7 @@ __global__ __launch_bounds__(kFwdThreads) void attn_fwd_bf16_kernel(
   } else if (grp <= td.tile) {
     store_tile(0);
   }
+  wait_vmem_all();
   __syncthreads();
   if (grp != 0) {
 #pragma unroll
@@ -585,16 +586,17 @@ __global__ __launch_bounds__(kFwdThreads) void attn_fwd_bf16_kernel(
 
 // ---------------------------------------------------------------------------
 // Backward, two launches:
-//   attn_dkdv   grid (Hq/Hkv, Hkv, ntiles in key order): per (query head, key
-//               tile) the head's dK/dV partial; it also forms D_i = dO_i.O_i
-//               for every query tile it stages and, for the tile holding its
-//               own keys, writes D to dvec.
-//   attn_dq     grid (Hq/Hkv, Hkv, ntiles + nred): z < ntiles is the dQ of a
-//               (query head, query tile), reading D from dvec; z >= ntiles
-//               are reduction workgroups that sum the group's dK/dV partials
-//               in ascending head order (CausalAttentionKernel.cs:184-206),
-//               apply the inverse RoPE to dK and write dk/dv.  They run on
-//               the CUs freed by the short dQ tiles.
+//   attn_bwd    grid (Hq/Hkv, Hkv, 2 ntiles).  z < ntiles: dK/dV of one
+//               (query head, key tile), accumulated in registers over the
+//               query tiles and written as that head's fp32 partial;
+//               z >= ntiles: dQ of one (query head, query tile), inverse RoPE
+//               applied on the store.  Both kinds form the row terms
+//               D_i = dO_i . O_i of the query tiles they stage with the same
+//               arithmetic (row_term), so neither waits for the other and one
+//               launch runs them side by side: the CUs that finish short tiles
+//               of one kind pick up tiles of the other.
+//   attn_bwd_reduce  dK/dV = the group's partials summed in ascending head
+//               order (CausalAttentionKernel.cs:184-206), inverse RoPE on dK.
 // G groups of 4 waves split a tile's loop (2 in the bf16 mode, 1 in fp32);
 // their partial sums are added in group order.
 // ---------------------------------------------------------------------------
@@ -603,80 +605,46 @@ constexpr int bwd_groups() {
   return sizeof(T) == 2 ? 2 : 1;
 }
 
-// Rows of the (token, kv head) space that one reduction workgroup finishes.
-constexpr int kRedRows = 16;
-
-template <typename IO, int D>
-__device__ inline void dkdv_reduce_rows(const float* __restrict__ wk,
-                                        const float* __restrict__ wv, IO* __restrict__ dk,
-                                        IO* __restrict__ dv, const int32_t* __restrict__ pos_of,
-                                        int total_tokens, int ratio, int n_heads_kv, int unit,
-                                        const float* __restrict__ cos_t,
-                                        const float* __restrict__ sin_t) {
-  constexpr int H = D / 2;
-  constexpr int CH = H / 4;  // 4-pair chunks per row
-  const int item = threadIdx.x;
-  if (item >= kRedRows * CH) return;
-  const long row = (long)unit * kRedRows + item / CH;  // token * Hkv + kv head
-  if (row >= (long)total_tokens * n_heads_kv) return;
-  const int p0 = 4 * (item % CH);
-  const long tok = row / n_heads_kv;
-  const int j = (int)(row % n_heads_kv);
-  const int n_heads_q = ratio * n_heads_kv;
-  f32x4 k0 = {0.0f, 0.0f, 0.0f, 0.0f}, k1 = k0, v0 = k0, v1 = k0;
-  for (int hh = 0; hh < ratio; ++hh) {
-    const long src = (tok * n_heads_q + (long)j * ratio + hh) * D + p0;
-    k0 += *reinterpret_cast<const f32x4*>(wk + src);
-    k1 += *reinterpret_cast<const f32x4*>(wk + src + H);
-    v0 += *reinterpret_cast<const f32x4*>(wv + src);
-    v1 += *reinterpret_cast<const f32x4*>(wv + src + H);
-  }
-  const long pos = pos_of != nullptr ? pos_of[tok] : tok;
-  const f32x4 cs = *reinterpret_cast<const f32x4*>(cos_t + pos * H + p0);
-  const f32x4 sn = *reinterpret_cast<const f32x4*>(sin_t + pos * H + p0);
-  f32x4 y0, y1;
+// D_i = dO_i . O_i for register-staged dO/O tiles: the thread's chunk i (8
+// elements of one row) is multiplied out in order, then the partial sums of
+// the CPR lanes that hold the row are added in a fixed order.  Every lane of
+// the row gets the same bits, and both backward tile kinds use this, so they
+// agree bit for bit.
+template <typename IO, int D, int NT>
+__device__ inline float row_term(const TileRegs<IO, D, NT>& dreg, const TileRegs<IO, D, NT>& oreg,
+                                 int i) {
+  float xd[8], xo[8];
+  load8(reinterpret_cast<const IO*>(&dreg.w[i][0]), xd);
+  load8(reinterpret_cast<const IO*>(&oreg.w[i][0]), xo);
+  float part = 0.0f;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    float a, b;
-    rope_inv(k0[e], k1[e], cs[e], sn[e], a, b);
-    y0[e] = a;
-    y1[e] = b;
-  }
-  const long dst = row * D + p0;
-  store4(dk + dst, y0);
-  store4(dk + dst + H, y1);
-  store4(dv + dst, v0);
-  store4(dv + dst + H, v1);
+  for (int e = 0; e < 8; ++e) part += xd[e] * xo[e];
+  return lanes_sum<TileRegs<IO, D, NT>::CPR>(part);
 }
 
+// dQ of one (query head, query tile); z indexes the query tiles (longest
+// first for a single sequence).
 template <typename IO, typename T, int D, bool VARLEN>
-__global__ __launch_bounds__(kThreads * bwd_groups<T>()) void attn_dq_kernel(
-    const IO* __restrict__ q_rot, const IO* __restrict__ d_out,
-    const IO* __restrict__ k_rot, const IO* __restrict__ v, const float* __restrict__ lse,
-    const float* __restrict__ dvec, IO* __restrict__ dq, const TileDesc* __restrict__ tiles,
+__device__ inline void bwd_dq_tile(
+    int z, const IO* __restrict__ q_rot, const IO* __restrict__ d_out,
+    const IO* __restrict__ out, const IO* __restrict__ k_rot, const IO* __restrict__ v,
+    const float* __restrict__ lse, IO* __restrict__ dq, const TileDesc* __restrict__ tiles,
     int n_tiles, int total_tokens, float scale_log2, float scale,
-    const float* __restrict__ cos_t, const float* __restrict__ sin_t,
-    const float* __restrict__ wk, const float* __restrict__ wv, IO* __restrict__ dk,
-    IO* __restrict__ dv, const int32_t* __restrict__ pos_of) {
+    const float* __restrict__ cos_t, const float* __restrict__ sin_t) {
   using M = Mfma<T>;
   using L = Lds<T, D>;
   constexpr int G = bwd_groups<T>();
   constexpr int NKD = D / M::KSTEP;
   constexpr int H = D / 2;
+  using Regs = TileRegs<IO, D, kThreads * G>;
   extern __shared__ __align__(16) unsigned char smem_raw[];
   T* const lds = reinterpret_cast<T*>(smem_raw);  // [G][2 buffers][K tile, V tile]
+  float* const dsm = reinterpret_cast<float*>(lds + 4 * G * L::TILE);  // [64] row terms
 
   const int ratio = gridDim.x, n_heads_kv = gridDim.y, n_heads_q = ratio * n_heads_kv;
   const int kvh = blockIdx.y, h = kvh * ratio + blockIdx.x;
-  if ((int)blockIdx.z >= n_tiles) {
-    const int unit = ((int)blockIdx.z - n_tiles) * n_heads_q + h;
-    dkdv_reduce_rows<IO, D>(wk, wv, dk, dv, VARLEN ? pos_of : nullptr, total_tokens, ratio,
-                            n_heads_kv, unit, cos_t, sin_t);
-    return;
-  }
-  const TileDesc td = VARLEN ? tiles[blockIdx.z]
-                             : TileDesc{0, total_tokens, n_tiles - 1 - (int)blockIdx.z, 0};
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const TileDesc td = VARLEN ? tiles[z] : TileDesc{0, total_tokens, n_tiles - 1 - z, 0};
+  const int tid = threadIdx.x, w = wave_id(), lane = tid & 63;
   const int grp = w >> 2, wq = w & 3, gtid = tid & (kThreads - 1);
   const int g = lane >> 4, c = lane & 15;
   const int qrow = kTile * td.tile + 16 * wq + c;
@@ -694,6 +662,13 @@ __global__ __launch_bounds__(kThreads * bwd_groups<T>()) void attn_dq_kernel(
     vreg.load(vbase + roff, kvstride, td.len - kTile * grp, gtid);
   }
 
+  // This tile's dO and O rows for the row terms D_i (all threads).
+  const long qstride = (long)n_heads_q * D;
+  const long trow = ((long)(td.tok0 + kTile * td.tile) * n_heads_q + h) * D;
+  Regs dreg, oreg;
+  dreg.load(d_out + trow, qstride, td.len - kTile * td.tile, tid);
+  oreg.load(out + trow, qstride, td.len - kTile * td.tile, tid);
+
   typename M::Frag qf[NKD], df[NKD];
 #pragma unroll
   for (int kk = 0; kk < NKD; ++kk) {
@@ -701,13 +676,13 @@ __global__ __launch_bounds__(kThreads * bwd_groups<T>()) void attn_dq_kernel(
     df[kk] = qvalid ? frag_global<T>(d_out + qbase, kk, g) : frag_zero<T>();
   }
   const long si = (long)h * total_tokens + td.tok0 + qrow;
-  const float drow = qvalid ? dvec[si] : 0.0f;
-  const float nlse2 = qvalid ? -lse[si] * kLog2e : 0.0f;
+  const float lse_q = qvalid ? lse[si] : 0.0f;
 
   f32x4 acc_dq[D / 16];
 #pragma unroll
   for (int db = 0; db < D / 16; ++db) acc_dq[db] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
+  float drow = 0.0f, nlse2 = 0.0f;  // set once the row terms are staged
   // One key tile: S, dP, P from lse, dS = P (dP - D), dQ^T += K^T dS^T.
   auto step = [&](const T* ks, const T* vs, auto diag) {
     constexpr bool DIAG = decltype(diag)::value;
@@ -738,7 +713,16 @@ __global__ __launch_bounds__(kThreads * bwd_groups<T>()) void attn_dq_kernel(
     kreg.store(glds, gtid);
     vreg.store(glds + L::TILE, gtid);
   }
+#pragma unroll
+  for (int i = 0; i < Regs::N; ++i) {
+    const float part = row_term(dreg, oreg, i);
+    const int idx = tid + i * kThreads * G;
+    if (idx % Regs::CPR == 0) dsm[idx / Regs::CPR] = part;
+  }
+  wait_vmem_all();
   __syncthreads();
+  drow = qvalid ? dsm[16 * wq + c] : 0.0f;
+  nlse2 = qvalid ? -lse_q * kLog2e : 0.0f;
 
   const int nit = (td.tile + G) / G;
   for (int it = 0; it < nit; ++it) {
@@ -770,36 +754,57 @@ __global__ __launch_bounds__(kThreads * bwd_groups<T>()) void attn_dq_kernel(
       for (int db = 0; db < D / 16; ++db) cmb[db * 64] = acc_dq[db];
     }
     __syncthreads();
-    if (grp == 1) return;
+    if (grp == 0) {
 #pragma unroll
-    for (int db = 0; db < D / 16; ++db) acc_dq[db] += cmb[db * 64];
+      for (int db = 0; db < D / 16; ++db) acc_dq[db] += cmb[db * 64];
+    }
   }
 
-  if (qvalid) {
+  // Scale, inverse RoPE at the query's position, and write whole rows: the
+  // [64][D] dQ tile is staged in LDS in the output dtype (row stride D + 8),
+  // then every thread stores 16-byte pieces of consecutive rows.  Lane
+  // (g, c) holds d = 16 db + 4 g + 0..3 (and d + D/2) of query 16 wq + c.
+  constexpr int SR = D + 8;
+  IO* const stq = reinterpret_cast<IO*>(smem_raw);
+  if (grp == 0) {
+    const long ti0 = (long)(qvalid ? qrow : 0) * H;
 #pragma unroll
     for (int db = 0; db < D / 32; ++db) {
-      f32x4 lo = acc_dq[db] * scale, hi = acc_dq[db + D / 32] * scale;
+      const f32x4 lo = acc_dq[db] * scale, hi = acc_dq[db + D / 32] * scale;
+      const int d0 = 16 * db + 4 * g;
+      const f32x4 cs = *reinterpret_cast<const f32x4*>(cos_t + ti0 + d0);
+      const f32x4 sn = *reinterpret_cast<const f32x4*>(sin_t + ti0 + d0);
       f32x4 y0, y1;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int d = 16 * db + 4 * g + r;
-        const long ti = (long)qrow * H + d;
         float a, b;
-        rope_inv(lo[r], hi[r], cos_t[ti], sin_t[ti], a, b);
+        rope_inv(lo[r], hi[r], cs[r], sn[r], a, b);
         y0[r] = a;
         y1[r] = b;
       }
-      store4(dq + qbase + 16 * db + 4 * g, y0);
-      store4(dq + qbase + H + 16 * db + 4 * g, y1);
+      store4(stq + (16 * wq + c) * SR + d0, y0);
+      store4(stq + (16 * wq + c) * SR + H + d0, y1);
     }
+  }
+  __syncthreads();
+  constexpr int EPC = 16 / sizeof(IO);  // elements per 16-byte piece
+  constexpr int PPR = D / EPC;          // pieces per row
+#pragma unroll
+  for (int i = tid; i < kTile * PPR; i += kThreads * G) {
+    const int r = i / PPR, pc = i % PPR;
+    if (kTile * td.tile + r < td.len)
+      *reinterpret_cast<uint4*>(dq + ((long)(td.tok0 + kTile * td.tile + r) * n_heads_q + h) * D +
+                                pc * EPC) =
+          *reinterpret_cast<const uint4*>(stq + r * SR + pc * EPC);
   }
 }
 
+// dK/dV partial of one (query head, key tile); z indexes the key tiles.
 template <typename IO, typename T, int D, bool VARLEN>
-__global__ __launch_bounds__(kThreads * bwd_groups<T>()) void attn_dkdv_kernel(
-    const IO* __restrict__ q_rot, const IO* __restrict__ d_out, const IO* __restrict__ out,
-    const IO* __restrict__ k_rot, const IO* __restrict__ v, const float* __restrict__ lse,
-    float* __restrict__ dvec, float* __restrict__ wk, float* __restrict__ wv,
+__device__ inline void bwd_dkdv_tile(
+    int z, const IO* __restrict__ q_rot, const IO* __restrict__ d_out,
+    const IO* __restrict__ out, const IO* __restrict__ k_rot, const IO* __restrict__ v,
+    const float* __restrict__ lse, float* __restrict__ wk, float* __restrict__ wv,
     const TileDesc* __restrict__ tiles, int n_tiles, int total_tokens, float scale_log2,
     float scale) {
   using M = Mfma<T>;
@@ -812,8 +817,8 @@ __global__ __launch_bounds__(kThreads * bwd_groups<T>()) void attn_dkdv_kernel(
 
   const int ratio = gridDim.x, n_heads_kv = gridDim.y, n_heads_q = ratio * n_heads_kv;
   const int kvh = blockIdx.y, h = kvh * ratio + blockIdx.x;
-  const TileDesc td = VARLEN ? tiles[blockIdx.z] : TileDesc{0, total_tokens, (int)blockIdx.z, 0};
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const TileDesc td = VARLEN ? tiles[z] : TileDesc{0, total_tokens, z, 0};
+  const int tid = threadIdx.x, w = wave_id(), lane = tid & 63;
   const int grp = w >> 2, wq = w & 3, gtid = tid & (kThreads - 1);
   const int g = lane >> 4, c = lane & 15;
   const int krow = kTile * td.tile + 16 * wq + c;
@@ -827,43 +832,34 @@ __global__ __launch_bounds__(kThreads * bwd_groups<T>()) void attn_dkdv_kernel(
   const IO* dob = d_out + ((long)td.tok0 * n_heads_q + h) * D;
   const IO* ob = out + ((long)td.tok0 * n_heads_q + h) * D;
   const float* lseb = lse + (long)h * total_tokens + td.tok0;
-  float* const dvb = dvec + (long)h * total_tokens + td.tok0;
 
   // Stage one query tile: Q, dO and O rows into registers, -lse*log2(e)
   // (-inf past the sequence, so P and dS are 0 there) into one float.
+  // The loaded lse is used only when the tile is stored: any arithmetic on
+  // it here would make the wave wait for every load just issued (loads
+  // complete in order), exposing the prefetch instead of hiding it.
   Regs qreg, dreg, oreg;
-  float nlse = 0.0f;
+  float lse_raw = 0.0f;
   auto load_tile = [&](int qt) {
     const long roff = (long)kTile * qt * qstride;
     const int nv = td.len - kTile * qt;
     qreg.load(qb + roff, qstride, nv, gtid);
     dreg.load(dob + roff, qstride, nv, gtid);
     oreg.load(ob + roff, qstride, nv, gtid);
-    if (gtid < kTile) nlse = gtid < nv ? -lseb[kTile * qt + gtid] * kLog2e : -INFINITY;
+    if (gtid < kTile && gtid < nv) lse_raw = lseb[kTile * qt + gtid];
   };
-  // ... and write it to LDS buffer `buf` with D_i = dO_i . O_i (the row's
-  // CPR chunks sit on CPR consecutive lanes; summed in a fixed order).
+  // ... and write it to LDS buffer `buf` with the row terms D_i.
   auto store_tile = [&](int buf, int qt) {
     unsigned char* base = gsm + buf * BUF;
     qreg.store(reinterpret_cast<T*>(base), gtid);
     dreg.store(reinterpret_cast<T*>(base) + L::TILE, gtid);
     float* vec = reinterpret_cast<float*>(base + 2 * L::TILE * sizeof(T));
-    if (gtid < kTile) vec[gtid] = nlse;
+    if (gtid < kTile) vec[gtid] = gtid < td.len - kTile * qt ? -lse_raw * kLog2e : -INFINITY;
 #pragma unroll
     for (int i = 0; i < Regs::N; ++i) {
-      float xd[8], xo[8];
-      load8(reinterpret_cast<const IO*>(&dreg.w[i][0]), xd);
-      load8(reinterpret_cast<const IO*>(&oreg.w[i][0]), xo);
-      float part = 0.0f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) part += xd[e] * xo[e];
-      part = lanes_sum<Regs::CPR>(part);
+      const float part = row_term(dreg, oreg, i);
       const int idx = gtid + i * kThreads;
-      const int r = idx / Regs::CPR;
-      if (idx % Regs::CPR == 0) {
-        vec[kTile + r] = part;
-        if (qt == td.tile && kTile * qt + r < td.len) dvb[kTile * qt + r] = part;
-      }
+      if (idx % Regs::CPR == 0) vec[kTile + idx / Regs::CPR] = part;
     }
   };
 
@@ -918,6 +914,7 @@ __global__ __launch_bounds__(kThreads * bwd_groups<T>()) void attn_dkdv_kernel(
   };
 
   if (first < ntq) store_tile(0, first);
+  wait_vmem_all();
   __syncthreads();
 
   const int nit = (ntq - td.tile + G - 1) / G;  // iterations of group 0 (the most)
@@ -982,6 +979,67 @@ __global__ __launch_bounds__(kThreads * bwd_groups<T>()) void attn_dkdv_kernel(
   }
 }
 
+template <typename IO, typename T, int D, bool VARLEN>
+__global__ __launch_bounds__(kThreads * bwd_groups<T>()) void attn_bwd_kernel(
+    const IO* __restrict__ q_rot, const IO* __restrict__ d_out, const IO* __restrict__ out,
+    const IO* __restrict__ k_rot, const IO* __restrict__ v, const float* __restrict__ lse,
+    IO* __restrict__ dq, float* __restrict__ wk, float* __restrict__ wv,
+    const TileDesc* __restrict__ tiles_q, const TileDesc* __restrict__ tiles_kv, int n_tiles,
+    int total_tokens, float scale_log2, float scale, const float* __restrict__ cos_t,
+    const float* __restrict__ sin_t) {
+  const int z = blockIdx.z;
+  if (z < n_tiles)
+    bwd_dkdv_tile<IO, T, D, VARLEN>(z, q_rot, d_out, out, k_rot, v, lse, wk, wv, tiles_kv,
+                                    n_tiles, total_tokens, scale_log2, scale);
+  else
+    bwd_dq_tile<IO, T, D, VARLEN>(z - n_tiles, q_rot, d_out, out, k_rot, v, lse, dq, tiles_q,
+                                  n_tiles, total_tokens, scale_log2, scale, cos_t, sin_t);
+}
+
+// Threads of a reduction workgroup; each finishes 4 rotation pairs of one
+// (token, kv head) row, so a workgroup covers kRedThreads / (D / 8) rows.
+constexpr int kRedThreads = 128;
+
+template <typename IO, int D>
+__global__ __launch_bounds__(kRedThreads) void attn_bwd_reduce_kernel(
+    const float* __restrict__ wk, const float* __restrict__ wv, IO* __restrict__ dk,
+    IO* __restrict__ dv, const int32_t* __restrict__ pos_of, int total_tokens, int ratio,
+    int n_heads_kv, const float* __restrict__ cos_t, const float* __restrict__ sin_t) {
+  constexpr int H = D / 2;
+  constexpr int CH = H / 4;  // 4-pair chunks per row
+  constexpr int ROWS = kRedThreads / CH;
+  const long row = (long)blockIdx.x * ROWS + threadIdx.x / CH;  // token * Hkv + kv head
+  if (row >= (long)total_tokens * n_heads_kv) return;
+  const int p0 = 4 * (threadIdx.x % CH);
+  const long tok = row / n_heads_kv;
+  const int j = (int)(row % n_heads_kv);
+  const int n_heads_q = ratio * n_heads_kv;
+  f32x4 k0 = {0.0f, 0.0f, 0.0f, 0.0f}, k1 = k0, v0 = k0, v1 = k0;
+  for (int hh = 0; hh < ratio; ++hh) {
+    const long src = (tok * n_heads_q + (long)j * ratio + hh) * D + p0;
+    k0 += *reinterpret_cast<const f32x4*>(wk + src);
+    k1 += *reinterpret_cast<const f32x4*>(wk + src + H);
+    v0 += *reinterpret_cast<const f32x4*>(wv + src);
+    v1 += *reinterpret_cast<const f32x4*>(wv + src + H);
+  }
+  const long pos = pos_of != nullptr ? pos_of[tok] : tok;
+  const f32x4 cs = *reinterpret_cast<const f32x4*>(cos_t + pos * H + p0);
+  const f32x4 sn = *reinterpret_cast<const f32x4*>(sin_t + pos * H + p0);
+  f32x4 y0, y1;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    float a, b;
+    rope_inv(k0[e], k1[e], cs[e], sn[e], a, b);
+    y0[e] = a;
+    y1[e] = b;
+  }
+  const long dst = row * D + p0;
+  store4(dk + dst, y0);
+  store4(dk + dst + H, y1);
+  store4(dv + dst, v0);
+  store4(dv + dst + H, v1);
+}
+
 // ---------------------------------------------------------------------------
 // Host launchers
 // ---------------------------------------------------------------------------
@@ -994,12 +1052,13 @@ constexpr size_t fwd_lds() {
          (fwd_groups<T>() == 2 ? sizeof(T) * kTile * D : 0);
 }
 template <typename T, int D>
-constexpr size_t dq_lds() {
-  return sizeof(T) * 4 * Lds<T, D>::TILE * bwd_groups<T>();
-}
-template <typename T, int D>
-constexpr size_t dkdv_lds() {
-  return 2 * (sizeof(T) * 2 * Lds<T, D>::TILE + 2 * kTile * sizeof(float)) * bwd_groups<T>();
+constexpr size_t bwd_lds() {
+  // dQ tiles: K/V double buffers per group plus the 64 row terms; dK/dV
+  // tiles: Q/dO double buffers per group with the lse and D vectors.
+  constexpr size_t dq = sizeof(T) * 4 * Lds<T, D>::TILE * bwd_groups<T>() + kTile * sizeof(float);
+  constexpr size_t dkdv =
+      2 * (sizeof(T) * 2 * Lds<T, D>::TILE + 2 * kTile * sizeof(float)) * bwd_groups<T>();
+  return dq > dkdv ? dq : dkdv;
 }
 
 template <typename F>
@@ -1063,34 +1122,29 @@ hipError_t forward_impl(const FwdLaunch& a, hipStream_t st, KernelTimer* tm) {
 template <typename IO, typename T, int D>
 hipError_t backward_impl(const BwdLaunch& a, hipStream_t st, KernelTimer* tm) {
   const int ratio = a.n_heads_q / a.n_heads_kv;
-  const dim3 blk(kThreads * bwd_groups<T>());
-  const IO* q_rot = static_cast<const IO*>(a.q_rot);
-  const IO* k_rot = static_cast<const IO*>(a.k_rot);
-  const IO* v = static_cast<const IO*>(a.v);
-  const IO* d_out = static_cast<const IO*>(a.d_out);
   {
-    auto fn = a.single_seq ? attn_dkdv_kernel<IO, T, D, false> : attn_dkdv_kernel<IO, T, D, true>;
-    constexpr size_t lds = dkdv_lds<T, D>();
+    auto fn = a.single_seq ? attn_bwd_kernel<IO, T, D, false> : attn_bwd_kernel<IO, T, D, true>;
+    constexpr size_t lds = bwd_lds<T, D>();
     GL_CHECK(allow_lds(fn, lds));
-    ScopedTiming t(tm, kKernDkdv, st);
-    hipLaunchKernelGGL(fn, dim3(ratio, a.n_heads_kv, a.n_tiles), blk, lds, st, q_rot, d_out,
-                       static_cast<const IO*>(a.out), k_rot, v, a.lse, a.dvec, a.wk, a.wv,
-                       a.tiles_kv, a.n_tiles, a.total_tokens, a.scale_log2, a.scale);
+    ScopedTiming t(tm, kKernBwd, st);
+    hipLaunchKernelGGL(fn, dim3(ratio, a.n_heads_kv, 2 * a.n_tiles),
+                       dim3(kThreads * bwd_groups<T>()), lds, st,
+                       static_cast<const IO*>(a.q_rot), static_cast<const IO*>(a.d_out),
+                       static_cast<const IO*>(a.out), static_cast<const IO*>(a.k_rot),
+                       static_cast<const IO*>(a.v), a.lse, static_cast<IO*>(a.dq), a.wk, a.wv,
+                       a.tiles_fwd, a.tiles_kv, a.n_tiles, a.total_tokens, a.scale_log2,
+                       a.scale, a.cos_t, a.sin_t);
     GL_CHECK(hipGetLastError());
   }
   {
-    auto fn = a.single_seq ? attn_dq_kernel<IO, T, D, false> : attn_dq_kernel<IO, T, D, true>;
-    constexpr size_t lds = dq_lds<T, D>();
-    GL_CHECK(allow_lds(fn, lds));
-    // reduction workgroups: kRedRows (token, kv head) rows each, a.n_heads_q per z-slice
+    constexpr int rows_per_wg = kRedThreads / (D / 8);
     const long rows = (long)a.total_tokens * a.n_heads_kv;
-    const long units = (rows + kRedRows - 1) / kRedRows;
-    const int nred = static_cast<int>((units + a.n_heads_q - 1) / a.n_heads_q);
-    ScopedTiming t(tm, kKernDq, st);
-    hipLaunchKernelGGL(fn, dim3(ratio, a.n_heads_kv, a.n_tiles + nred), blk, lds, st, q_rot,
-                       d_out, k_rot, v, a.lse, a.dvec, static_cast<IO*>(a.dq), a.tiles_fwd,
-                       a.n_tiles, a.total_tokens, a.scale_log2, a.scale, a.cos_t, a.sin_t,
-                       a.wk, a.wv, static_cast<IO*>(a.dk), static_cast<IO*>(a.dv), a.pos_of);
+    const unsigned grid = static_cast<unsigned>((rows + rows_per_wg - 1) / rows_per_wg);
+    ScopedTiming t(tm, kKernReduce, st);
+    hipLaunchKernelGGL((attn_bwd_reduce_kernel<IO, D>), dim3(grid), dim3(kRedThreads), 0, st,
+                       a.wk, a.wv, static_cast<IO*>(a.dk), static_cast<IO*>(a.dv),
+                       a.single_seq ? nullptr : a.pos_of, a.total_tokens, ratio, a.n_heads_kv,
+                       a.cos_t, a.sin_t);
     GL_CHECK(hipGetLastError());
   }
   return hipSuccess;

@@ -33,8 +33,8 @@ constexpr int kPrecBf16 = 1;
 enum KernelId : int {
   kKernRopeK = 0,
   kKernFwd = 1,
-  kKernDkdv = 2,
-  kKernDq = 3,
+  kKernBwd = 2,
+  kKernReduce = 3,
   kKernCount = 4,
 };
 
@@ -129,7 +129,6 @@ struct BwdLaunch {
   const void *d_out, *q_rot, *k_rot, *v, *out;
   const float* lse;
   void *dq, *dk, *dv;
-  float* dvec;                   // [Hq][T] row terms dO.O
   float *wk, *wv;                // per-query-head dK/dV partials [T][Hq][D]
   const TileDesc* tiles_fwd;
   const TileDesc* tiles_kv;      // key tiles with the most query tiles first

@@ -192,7 +192,6 @@ class GpuAttentionEngine {
     a.scale_log2 = kLog2e * a.scale;
     a.d_out = d_out; a.q_rot = q_rot; a.k_rot = k_rot; a.v = v; a.out = out;
     a.lse = lse; a.dq = dq; a.dk = dk; a.dv = dv;
-    a.dvec = static_cast<float*>(dvec_.ensure(Hq * T * sizeof(float), "dO.O scratch"));
     a.wk = static_cast<float*>(wk_.ensure(T * Hq * D * sizeof(float), "dK partials"));
     a.wv = static_cast<float*>(wv_.ensure(T * Hq * D * sizeof(float), "dV partials"));
     const TileDesc* t = static_cast<const TileDesc*>(ts.tiles.ptr);
@@ -351,7 +350,7 @@ class GpuAttentionEngine {
   int rope_len_ = 0, rope_dim_ = 0;
   float rope_base_ = 0.0f;
   // device-path scratch
-  DeviceBuffer kc_, vc_, dvec_, wk_, wv_;
+  DeviceBuffer kc_, vc_, wk_, wv_;
   // host-path device copies
   DeviceBuffer h_q_, h_k_, h_v_, h_out_, h_lse_, h_qr_, h_kr_, h_dout_, h_dq_, h_dk_, h_dv_;
 };
@@ -447,7 +446,7 @@ int guarded(F&& f) {
 }
 
 const char* const kKernelNames[kKernCount] = {
-    "rope_k", "attn_fwd", "attn_bwd_dkdv", "attn_bwd_dq",
+    "rope_k", "attn_fwd", "attn_bwd", "attn_bwd_reduce",
 };
 
 }  // namespace
