@@ -1014,17 +1014,43 @@ __global__ __launch_bounds__(kRedThreads) void attn_bwd_reduce_kernel(
   const long tok = row / n_heads_kv;
   const int j = (int)(row % n_heads_kv);
   const int n_heads_q = ratio * n_heads_kv;
-  f32x4 k0 = {0.0f, 0.0f, 0.0f, 0.0f}, k1 = k0, v0 = k0, v1 = k0;
-  for (int hh = 0; hh < ratio; ++hh) {
-    const long src = (tok * n_heads_q + (long)j * ratio + hh) * D + p0;
-    k0 += *reinterpret_cast<const f32x4*>(wk + src);
-    k1 += *reinterpret_cast<const f32x4*>(wk + src + H);
-    v0 += *reinterpret_cast<const f32x4*>(wv + src);
-    v1 += *reinterpret_cast<const f32x4*>(wv + src + H);
-  }
   const long pos = pos_of != nullptr ? pos_of[tok] : tok;
   const f32x4 cs = *reinterpret_cast<const f32x4*>(cos_t + pos * H + p0);
   const f32x4 sn = *reinterpret_cast<const f32x4*>(sin_t + pos * H + p0);
+  const float* wkr = wk + (tok * n_heads_q + (long)j * ratio) * D + p0;
+  const float* wvr = wv + (tok * n_heads_q + (long)j * ratio) * D + p0;
+  f32x4 k0 = {0.0f, 0.0f, 0.0f, 0.0f}, k1 = k0, v0 = k0, v1 = k0;
+  constexpr int RMAX = 8;
+  if (ratio <= RMAX) {
+    // Every head's partial in flight at once (a load per head that the sum
+    // waits on would cost one memory round trip per head), then the sum in
+    // ascending head order; heads past the group add nothing.
+    f32x4 pk0[RMAX], pk1[RMAX], pv0[RMAX], pv1[RMAX];
+#pragma unroll
+    for (int hh = 0; hh < RMAX; ++hh) {
+      const long o = (long)(hh < ratio ? hh : 0) * D;
+      pk0[hh] = *reinterpret_cast<const f32x4*>(wkr + o);
+      pk1[hh] = *reinterpret_cast<const f32x4*>(wkr + o + H);
+      pv0[hh] = *reinterpret_cast<const f32x4*>(wvr + o);
+      pv1[hh] = *reinterpret_cast<const f32x4*>(wvr + o + H);
+    }
+#pragma unroll
+    for (int hh = 0; hh < RMAX; ++hh) {
+      if (hh < ratio) {
+        k0 += pk0[hh];
+        k1 += pk1[hh];
+        v0 += pv0[hh];
+        v1 += pv1[hh];
+      }
+    }
+  } else {
+    for (int hh = 0; hh < ratio; ++hh) {
+      k0 += *reinterpret_cast<const f32x4*>(wkr + (long)hh * D);
+      k1 += *reinterpret_cast<const f32x4*>(wkr + (long)hh * D + H);
+      v0 += *reinterpret_cast<const f32x4*>(wvr + (long)hh * D);
+      v1 += *reinterpret_cast<const f32x4*>(wvr + (long)hh * D + H);
+    }
+  }
   f32x4 y0, y1;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
