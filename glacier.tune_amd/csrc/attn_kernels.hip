@@ -25,6 +25,8 @@
 #include "attn_common.hpp"
 #include "attn_launch.hpp"
 
+#include <hip/hip_ext.h>
+
 #include <type_traits>
 
 namespace glacier {
@@ -569,7 +571,8 @@ __global__ __launch_bounds__(kFwdThreads) void attn_fwd_bf16_kernel(
     if (lse != nullptr && qvalid && g == 0)
       lse[(long)h * total_tokens + td.tok0 + qrow] = (m_run + log2f(l_tot)) * kLn2;
 #pragma unroll
-    for (int db = 0; db < D / 16; ++db) store4(ot + (16 * wq + c) * OS + 16 * db + 4 * g, o[db] * inv);
+    for (int db = 0; db < D / 16; ++db)
+      store4(ot + (16 * wq + c) * OS + 16 * db + 4 * g, o[db] * inv);
   }
   __syncthreads();
   constexpr int CPR = D * sizeof(IO) / 16;  // 16-byte chunks per row
@@ -1109,38 +1112,41 @@ hipError_t forward_impl(const FwdLaunch& a, hipStream_t st, KernelTimer* tm) {
     const long n = (long)a.total_tokens * a.n_heads_kv * (D / 16);
     const unsigned grid = static_cast<unsigned>((n + kThreads - 1) / kThreads);
     IO* k_rot = static_cast<IO*>(a.k_rot);
-    ScopedTiming t(tm, kKernRopeK, st);
-    hipLaunchKernelGGL((rope_k_kernel<IO, T, D>), dim3(grid), blk, 0, st,
-                       static_cast<const IO*>(a.k), k_rot,
-                       (static_cast<void*>(kc) == static_cast<void*>(k_rot)) ? nullptr : kc,
-                       static_cast<const IO*>(a.v), static_cast<T*>(a.vc), a.pos_of,
-                       a.total_tokens, a.n_heads_kv, a.cos_t, a.sin_t);
+    LaunchTiming t(tm, kKernRopeK);
+    hipExtLaunchKernelGGL((rope_k_kernel<IO, T, D>), dim3(grid), blk, 0, st, t.start(), t.stop(), 0,
+                          static_cast<const IO*>(a.k), k_rot,
+                          (static_cast<void*>(kc) == static_cast<void*>(k_rot)) ? nullptr : kc,
+                          static_cast<const IO*>(a.v), static_cast<T*>(a.vc), a.pos_of,
+                          a.total_tokens, a.n_heads_kv, a.cos_t, a.sin_t);
     GL_CHECK(hipGetLastError());
+    t.launched();
   }
   if constexpr (sizeof(T) == 2) {
     auto fn = a.single_seq ? attn_fwd_bf16_kernel<IO, D, false> : attn_fwd_bf16_kernel<IO, D, true>;
     constexpr size_t lds = fwd_bf16_lds<D>();
     GL_CHECK(allow_lds(fn, lds));
-    ScopedTiming t(tm, kKernFwd, st);
-    hipLaunchKernelGGL(fn, dim3(a.n_heads_q / a.n_heads_kv, a.n_heads_kv, a.n_tiles),
-                       dim3(kFwdThreads), lds, st, static_cast<const IO*>(a.q),
-                       static_cast<const bf16*>(a.kc),
-                       static_cast<const bf16*>(a.vc != nullptr ? a.vc : a.v),
-                       static_cast<IO*>(a.out), a.lse, static_cast<IO*>(a.q_rot), a.tiles_fwd,
-                       a.n_tiles, a.total_tokens, a.scale_log2, a.cos_t, a.sin_t);
+    LaunchTiming t(tm, kKernFwd);
+    hipExtLaunchKernelGGL(fn, dim3(a.n_heads_q / a.n_heads_kv, a.n_heads_kv, a.n_tiles),
+                          dim3(kFwdThreads), lds, st, t.start(), t.stop(), 0,
+                          static_cast<const IO*>(a.q), static_cast<const bf16*>(a.kc),
+                          static_cast<const bf16*>(a.vc != nullptr ? a.vc : a.v),
+                          static_cast<IO*>(a.out), a.lse, static_cast<IO*>(a.q_rot), a.tiles_fwd,
+                          a.n_tiles, a.total_tokens, a.scale_log2, a.cos_t, a.sin_t);
     GL_CHECK(hipGetLastError());
+    t.launched();
   } else {
     auto fn = attn_fwd_kernel<IO, T, D>;
     constexpr size_t lds = fwd_lds<T, D>();
     GL_CHECK(allow_lds(fn, lds));
-    ScopedTiming t(tm, kKernFwd, st);
-    hipLaunchKernelGGL(fn, dim3(a.n_heads_q, a.n_tiles), dim3(kThreads * fwd_groups<T>()), lds,
-                       st, static_cast<const IO*>(a.q), static_cast<const T*>(kc),
-                       static_cast<const IO*>(a.v), static_cast<IO*>(a.out), a.lse,
-                       static_cast<IO*>(a.q_rot), a.single_seq ? nullptr : a.tiles_fwd,
-                       a.n_tiles, a.n_heads_q, a.n_heads_kv, a.total_tokens, a.scale_log2,
-                       a.cos_t, a.sin_t);
+    LaunchTiming t(tm, kKernFwd);
+    hipExtLaunchKernelGGL(fn, dim3(a.n_heads_q, a.n_tiles), dim3(kThreads * fwd_groups<T>()), lds,
+                          st, t.start(), t.stop(), 0, static_cast<const IO*>(a.q),
+                          static_cast<const T*>(kc), static_cast<const IO*>(a.v),
+                          static_cast<IO*>(a.out), a.lse, static_cast<IO*>(a.q_rot),
+                          a.single_seq ? nullptr : a.tiles_fwd, a.n_tiles, a.n_heads_q,
+                          a.n_heads_kv, a.total_tokens, a.scale_log2, a.cos_t, a.sin_t);
     GL_CHECK(hipGetLastError());
+    t.launched();
   }
   return hipSuccess;
 }
@@ -1152,26 +1158,28 @@ hipError_t backward_impl(const BwdLaunch& a, hipStream_t st, KernelTimer* tm) {
     auto fn = a.single_seq ? attn_bwd_kernel<IO, T, D, false> : attn_bwd_kernel<IO, T, D, true>;
     constexpr size_t lds = bwd_lds<T, D>();
     GL_CHECK(allow_lds(fn, lds));
-    ScopedTiming t(tm, kKernBwd, st);
-    hipLaunchKernelGGL(fn, dim3(ratio, a.n_heads_kv, 2 * a.n_tiles),
-                       dim3(kThreads * bwd_groups<T>()), lds, st,
-                       static_cast<const IO*>(a.q_rot), static_cast<const IO*>(a.d_out),
-                       static_cast<const IO*>(a.out), static_cast<const IO*>(a.k_rot),
-                       static_cast<const IO*>(a.v), a.lse, static_cast<IO*>(a.dq), a.wk, a.wv,
-                       a.tiles_fwd, a.tiles_kv, a.n_tiles, a.total_tokens, a.scale_log2,
-                       a.scale, a.cos_t, a.sin_t);
+    LaunchTiming t(tm, kKernBwd);
+    hipExtLaunchKernelGGL(fn, dim3(ratio, a.n_heads_kv, 2 * a.n_tiles),
+                          dim3(kThreads * bwd_groups<T>()), lds, st, t.start(), t.stop(), 0,
+                          static_cast<const IO*>(a.q_rot), static_cast<const IO*>(a.d_out),
+                          static_cast<const IO*>(a.out), static_cast<const IO*>(a.k_rot),
+                          static_cast<const IO*>(a.v), a.lse, static_cast<IO*>(a.dq), a.wk, a.wv,
+                          a.tiles_fwd, a.tiles_kv, a.n_tiles, a.total_tokens, a.scale_log2, a.scale,
+                          a.cos_t, a.sin_t);
     GL_CHECK(hipGetLastError());
+    t.launched();
   }
   {
     constexpr int rows_per_wg = kRedThreads / (D / 8);
     const long rows = (long)a.total_tokens * a.n_heads_kv;
     const unsigned grid = static_cast<unsigned>((rows + rows_per_wg - 1) / rows_per_wg);
-    ScopedTiming t(tm, kKernReduce, st);
-    hipLaunchKernelGGL((attn_bwd_reduce_kernel<IO, D>), dim3(grid), dim3(kRedThreads), 0, st,
-                       a.wk, a.wv, static_cast<IO*>(a.dk), static_cast<IO*>(a.dv),
-                       a.single_seq ? nullptr : a.pos_of, a.total_tokens, ratio, a.n_heads_kv,
-                       a.cos_t, a.sin_t);
+    LaunchTiming t(tm, kKernReduce);
+    hipExtLaunchKernelGGL((attn_bwd_reduce_kernel<IO, D>), dim3(grid), dim3(kRedThreads), 0, st,
+                          t.start(), t.stop(), 0, a.wk, a.wv, static_cast<IO*>(a.dk),
+                          static_cast<IO*>(a.dv), a.single_seq ? nullptr : a.pos_of, a.total_tokens,
+                          ratio, a.n_heads_kv, a.cos_t, a.sin_t);
     GL_CHECK(hipGetLastError());
+    t.launched();
   }
   return hipSuccess;
 }

@@ -78,27 +78,42 @@ class KernelTimer {
   int64_t launches_[kKernCount] = {};
 };
 
-// Records a start event now and a stop event when it goes out of scope.
-class ScopedTiming {
+// Event pair for one timed launch.  The launch itself timestamps the events
+// (hipExtLaunchKernelGGL writes them from the kernel's dispatch packet), so
+// the interval is the kernel's own execution and no extra packets enter the
+// stream.  With timing off both events are null and the launch is a plain one.
+class LaunchTiming {
  public:
-  ScopedTiming(KernelTimer* tm, int id, hipStream_t st) : tm_(tm), id_(id), st_(st) {
+  LaunchTiming(KernelTimer* tm, int id) : tm_(tm), id_(id) {
     if (tm_ != nullptr && tm_->enabled) {
-      if (hipEventCreate(&a_) == hipSuccess && hipEventCreate(&b_) == hipSuccess &&
-          hipEventRecord(a_, st_) == hipSuccess) {
+      if (hipEventCreate(&a_) == hipSuccess && hipEventCreate(&b_) == hipSuccess) {
         on_ = true;
+      } else {
+        release();
       }
     }
   }
-  ~ScopedTiming() {
-    if (on_ && hipEventRecord(b_, st_) == hipSuccess) tm_->record(id_, a_, b_);
+  hipEvent_t start() const { return a_; }
+  hipEvent_t stop() const { return b_; }
+  // Call after a successful launch: the pair joins the timer's pending list.
+  void launched() {
+    if (on_) tm_->record(id_, a_, b_);
+    on_ = false;
+    a_ = b_ = nullptr;
   }
+  ~LaunchTiming() { release(); }
 
  private:
+  void release() {
+    if (a_ != nullptr) (void)hipEventDestroy(a_);
+    if (b_ != nullptr) (void)hipEventDestroy(b_);
+    a_ = b_ = nullptr;
+    on_ = false;
+  }
   KernelTimer* tm_;
   int id_;
-  hipStream_t st_;
-  hipEvent_t a_ = nullptr, b_ = nullptr;
   bool on_ = false;
+  hipEvent_t a_ = nullptr, b_ = nullptr;
 };
 
 // Everything one forward launch needs (device pointers).
