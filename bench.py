@@ -13,9 +13,11 @@ value  = algorithmic FLOPs per step / wall time per step, where algorithmic
          FLOPs = 12 * D * Hq * sum_b L_b (L_b + 1) / 2 (4 D per unmasked
          (query, key, head) triple forward, 8 D backward; no credit for the
          score recompute, softmax or RoPE).
-roofline = the dominant kernel (largest share of device time), timed with
-         hipEvents on the stream it is launched on, against the 2.5 PFLOP/s
-         dense bf16 MFMA peak of MI355X.
+roofline = the dominant kernel (largest share of device time), its average
+         duration from events that its own launches timestamp (on the stream
+         it runs on), against the 2.5 PFLOP/s dense bf16 MFMA peak of MI355X;
+         traffic = its HBM bytes per launch measured with rocprofv3 counters
+         (profiles/attn_kernels_qwen7b_s512_pmc.md).
 cpu_baseline = the C restatement of the reference CPU path (oracle/), fp32,
          on this host's cores, over a bounded sample.
 """
@@ -43,6 +45,22 @@ CONFIGS = {
 # forward does QK^T and PV (4 D); the backward kernel dP, dV, dK and dQ (8 D);
 # rope_k and the dK/dV head reduction are credited with none.  Sum: 12 D.
 FLOPS_PER_PAIR = {"attn_fwd": 4, "attn_bwd": 8, "rope_k": 0, "attn_bwd_reduce": 0}
+
+
+# HBM bytes per launch of each kernel at qwen7b_s512, from two rocprofv3 --pmc
+# runs (FETCH_SIZE, WRITE_SIZE) scaled by a plain copy of known size; the file
+# gives the commands and the calibration.
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "attn_kernels_qwen7b_s512_pmc.md")
+
+
+def measured_traffic(config, kernel):
+    if config != "qwen7b_s512" or not os.path.exists(TRAFFIC_FILE):
+        return None
+    for line in open(TRAFFIC_FILE):
+        f = line.split()
+        if len(f) == 3 and f[0] == "traffic_bytes" and f[1] == kernel:
+            return int(f[2])
+    return None
 
 
 def pairs(lengths):
@@ -147,8 +165,8 @@ def main():
     flops = 12.0 * D * Hq * pairs(lengths)
     tflops = flops / (ms * 1e-3) / 1e12
 
-    # Per-kernel device time (hipEvents recorded around each launch on the
-    # stream it runs on), in a separate pass so the events do not perturb `ms`.
+    # Per-kernel device time (events timestamped by each launch itself on the
+    # stream it runs on), in a separate pass so timing does not perturb `ms`.
     eng.set_kernel_timing(True)
     for _ in range(args.steps):
         step()
@@ -165,7 +183,7 @@ def main():
         "peak": PEAK_BF16_TFLOPS,
         "unit": "TFLOP/s",
         "frac": round(achieved / PEAK_BF16_TFLOPS, 5),
-        "traffic": None,
+        "traffic": measured_traffic(args.config, dom),
         "kernel_avg_us": {n: round(a * 1e3, 3) for n, a in avg.items()},
     }
 

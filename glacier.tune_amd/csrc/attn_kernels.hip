@@ -1,23 +1,25 @@
 // attn_kernels.hip -- gfx950 kernels of the causal GQA attention path.
 //
 // Forward  (GpuLoraEngine.Forward.cs:401-465 rope_batch + tune_attn_causal_gqa_fwd):
-//   rope_k    K -> RoPE -> k_rot (caller dtype) and/or a compute-dtype copy.
-//   attn_fwd  one workgroup = 64 queries of one head; 4 waves x 16 queries.
-//             Q is rotated in registers on load (q_rot written if asked);
-//             rotated-K and V tiles of 64 keys are staged row-major in LDS
-//             (double-buffered, the next tile's global loads in flight while
-//             the current one is multiplied) and shared by the 4 waves;
-//             online softmax in fp32 (exp2 domain); O and the row
-//             log-sum-exp are written at the end.  No [S,S] matrix exists.
+//   rope_k    K -> RoPE -> k_rot (caller dtype) and/or a compute-dtype copy
+//             (plus a bf16 copy of V when fp32 tensors feed bf16 matrix cores).
+//   attn_fwd  one workgroup = 64 queries of one head, two groups of 4 waves
+//             (16 queries per wave) splitting the key tiles.  Q is rotated in
+//             registers on load (q_rot written if asked); rotated-K and V
+//             tiles of 64 keys are staged row-major in LDS (double-buffered,
+//             later tiles' global loads in flight meanwhile) and shared by the
+//             group's 4 waves; online softmax in fp32 (exp2 domain, lazy
+//             rescaling); O and the row log-sum-exp are written at the end.
+//             No [S,S] matrix exists.
 // Backward (GpuLoraEngine.Backward.cs:354-412 dq_ds + dk_dv, :452 inverse rope):
-//   attn_dq   one workgroup = 64 queries of one head: D_i = dO_i . O_i
-//             (written for attn_dkdv), P recomputed from the saved lse,
-//             dS = P (dP - D), dQ = scale * dS K, inverse RoPE on the store.
-//   attn_dkdv one workgroup = 64 keys of one query head: dV_h = P^T dO,
-//             dK_h = scale * dS^T Q accumulated in registers over all query
-//             tiles, written as this head's partial (fp32).
-//   dkdv_reduce  dK/dV = sum of the partials over the heads of the KV group
-//             in ascending head order (the reference's lock-free workspace
+//   attn_bwd  one launch with two kinds of workgroup.  dK/dV tiles: 64 keys of
+//             one query head; dV_h = P^T dO and dK_h = scale dS^T Q accumulated
+//             in registers over all query tiles, written as this head's fp32
+//             partial.  dQ tiles: 64 queries of one head; P recomputed from
+//             the saved lse, dS = P (dP - D), dQ = scale dS K, inverse RoPE on
+//             the store.  Both form D_i = dO_i . O_i themselves.
+//   attn_bwd_reduce  dK/dV = sum of the partials over the heads of the KV
+//             group in ascending head order (the reference's workspace
 //             reduction, CausalAttentionKernel.cs:184-206), inverse RoPE on dK.
 // Every reduction has a fixed order and no kernel uses floating-point
 // atomics, so results are bitwise repeatable (the activation-checkpoint
