@@ -629,13 +629,12 @@ __device__ inline float row_term(const TileRegs<IO, D, NT>& dreg, const TileRegs
 
 // dQ of one (query head, query tile); z indexes the query tiles (longest
 // first for a single sequence).
-template <typename IO, typename T, int D, bool VARLEN>
+template <typename IO, typename T, int D>
 __device__ inline void bwd_dq_tile(
-    int z, const IO* __restrict__ q_rot, const IO* __restrict__ d_out,
+    const TileDesc td, const IO* __restrict__ q_rot, const IO* __restrict__ d_out,
     const IO* __restrict__ out, const IO* __restrict__ k_rot, const IO* __restrict__ v,
-    const float* __restrict__ lse, IO* __restrict__ dq, const TileDesc* __restrict__ tiles,
-    int n_tiles, int total_tokens, float scale_log2, float scale,
-    const float* __restrict__ cos_t, const float* __restrict__ sin_t) {
+    const float* __restrict__ lse, IO* __restrict__ dq, int total_tokens, float scale_log2,
+    float scale, const float* __restrict__ cos_t, const float* __restrict__ sin_t) {
   using M = Mfma<T>;
   using L = Lds<T, D>;
   constexpr int G = bwd_groups<T>();
@@ -648,7 +647,6 @@ __device__ inline void bwd_dq_tile(
 
   const int ratio = gridDim.x, n_heads_kv = gridDim.y, n_heads_q = ratio * n_heads_kv;
   const int kvh = blockIdx.y, h = kvh * ratio + blockIdx.x;
-  const TileDesc td = VARLEN ? tiles[z] : TileDesc{0, total_tokens, n_tiles - 1 - z, 0};
   const int tid = threadIdx.x, w = wave_id(), lane = tid & 63;
   const int grp = w >> 2, wq = w & 3, gtid = tid & (kThreads - 1);
   const int g = lane >> 4, c = lane & 15;
@@ -805,13 +803,12 @@ __device__ inline void bwd_dq_tile(
 }
 
 // dK/dV partial of one (query head, key tile); z indexes the key tiles.
-template <typename IO, typename T, int D, bool VARLEN>
+template <typename IO, typename T, int D>
 __device__ inline void bwd_dkdv_tile(
-    int z, const IO* __restrict__ q_rot, const IO* __restrict__ d_out,
+    const TileDesc td, const IO* __restrict__ q_rot, const IO* __restrict__ d_out,
     const IO* __restrict__ out, const IO* __restrict__ k_rot, const IO* __restrict__ v,
     const float* __restrict__ lse, float* __restrict__ wk, float* __restrict__ wv,
-    const TileDesc* __restrict__ tiles, int n_tiles, int total_tokens, float scale_log2,
-    float scale) {
+    int total_tokens, float scale_log2, float scale) {
   using M = Mfma<T>;
   using L = Lds<T, D>;
   using Regs = TileRegs<IO, D>;
@@ -822,7 +819,6 @@ __device__ inline void bwd_dkdv_tile(
 
   const int ratio = gridDim.x, n_heads_kv = gridDim.y, n_heads_q = ratio * n_heads_kv;
   const int kvh = blockIdx.y, h = kvh * ratio + blockIdx.x;
-  const TileDesc td = VARLEN ? tiles[z] : TileDesc{0, total_tokens, z, 0};
   const int tid = threadIdx.x, w = wave_id(), lane = tid & 63;
   const int grp = w >> 2, wq = w & 3, gtid = tid & (kThreads - 1);
   const int g = lane >> 4, c = lane & 15;
@@ -984,21 +980,22 @@ __device__ inline void bwd_dkdv_tile(
   }
 }
 
-template <typename IO, typename T, int D, bool VARLEN>
+// z indexes tiles_bwd, the dK/dV and dQ tiles in launch order.  The
+// table is read through the scalar cache (one uniform load per workgroup).
+template <typename IO, typename T, int D>
 __global__ __launch_bounds__(kThreads * bwd_groups<T>()) void attn_bwd_kernel(
     const IO* __restrict__ q_rot, const IO* __restrict__ d_out, const IO* __restrict__ out,
     const IO* __restrict__ k_rot, const IO* __restrict__ v, const float* __restrict__ lse,
     IO* __restrict__ dq, float* __restrict__ wk, float* __restrict__ wv,
-    const TileDesc* __restrict__ tiles_q, const TileDesc* __restrict__ tiles_kv, int n_tiles,
-    int total_tokens, float scale_log2, float scale, const float* __restrict__ cos_t,
-    const float* __restrict__ sin_t) {
-  const int z = blockIdx.z;
-  if (z < n_tiles)
-    bwd_dkdv_tile<IO, T, D, VARLEN>(z, q_rot, d_out, out, k_rot, v, lse, wk, wv, tiles_kv,
-                                    n_tiles, total_tokens, scale_log2, scale);
+    const TileDesc* __restrict__ tiles_bwd, int total_tokens, float scale_log2, float scale,
+    const float* __restrict__ cos_t, const float* __restrict__ sin_t) {
+  const TileDesc td = tiles_bwd[blockIdx.z];
+  if (td.kind == 0)
+    bwd_dkdv_tile<IO, T, D>(td, q_rot, d_out, out, k_rot, v, lse, wk, wv, total_tokens,
+                            scale_log2, scale);
   else
-    bwd_dq_tile<IO, T, D, VARLEN>(z - n_tiles, q_rot, d_out, out, k_rot, v, lse, dq, tiles_q,
-                                  n_tiles, total_tokens, scale_log2, scale, cos_t, sin_t);
+    bwd_dq_tile<IO, T, D>(td, q_rot, d_out, out, k_rot, v, lse, dq, total_tokens, scale_log2,
+                          scale, cos_t, sin_t);
 }
 
 // Threads of a reduction workgroup; each finishes 4 rotation pairs of one
@@ -1157,7 +1154,7 @@ template <typename IO, typename T, int D>
 hipError_t backward_impl(const BwdLaunch& a, hipStream_t st, KernelTimer* tm) {
   const int ratio = a.n_heads_q / a.n_heads_kv;
   {
-    auto fn = a.single_seq ? attn_bwd_kernel<IO, T, D, false> : attn_bwd_kernel<IO, T, D, true>;
+    auto fn = attn_bwd_kernel<IO, T, D>;
     constexpr size_t lds = bwd_lds<T, D>();
     GL_CHECK(allow_lds(fn, lds));
     LaunchTiming t(tm, kKernBwd);
@@ -1166,8 +1163,7 @@ hipError_t backward_impl(const BwdLaunch& a, hipStream_t st, KernelTimer* tm) {
                           static_cast<const IO*>(a.q_rot), static_cast<const IO*>(a.d_out),
                           static_cast<const IO*>(a.out), static_cast<const IO*>(a.k_rot),
                           static_cast<const IO*>(a.v), a.lse, static_cast<IO*>(a.dq), a.wk, a.wv,
-                          a.tiles_fwd, a.tiles_kv, a.n_tiles, a.total_tokens, a.scale_log2, a.scale,
-                          a.cos_t, a.sin_t);
+                          a.tiles_bwd, a.total_tokens, a.scale_log2, a.scale, a.cos_t, a.sin_t);
     GL_CHECK(hipGetLastError());
     t.launched();
   }

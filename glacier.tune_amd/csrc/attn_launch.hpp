@@ -23,7 +23,7 @@ struct TileDesc {
   int32_t tok0;   // first token of the sequence in the [T][H][D] tensors
   int32_t len;    // tokens in the sequence
   int32_t tile;   // tile index inside the sequence (rows 64*tile ..)
-  int32_t pad;
+  int32_t kind;   // backward table: 0 = dK/dV tile, 1 = dQ tile (unused elsewhere)
 };
 
 constexpr int kPrecFp32 = 0;
@@ -145,8 +145,7 @@ struct BwdLaunch {
   const float* lse;
   void *dq, *dk, *dv;
   float *wk, *wv;                // per-query-head dK/dV partials [T][Hq][D]
-  const TileDesc* tiles_fwd;
-  const TileDesc* tiles_kv;      // key tiles with the most query tiles first
+  const TileDesc* tiles_bwd;     // [2 n_tiles] dK/dV and dQ tiles, longest expected first
   const int32_t* pos_of;
   const float *cos_t, *sin_t;
 };
