@@ -388,17 +388,22 @@ __global__ __launch_bounds__(kFwdThreads) void attn_fwd_bf16_kernel(
   const long kvstride = (long)n_heads_kv * D;
   const bf16* kbase = kc + ((long)td.tok0 * n_heads_kv + kvh) * D;
   const bf16* vbase = v + ((long)td.tok0 * n_heads_kv + kvh) * D;
-  TileRegs<bf16, D, GT> kreg, vreg;
-  auto load_tile = [&](int kt) {
+  // Two register sets for K/V tiles between their global loads and LDS
+  // stores, so each tile's loads are issued two iterations before its LDS
+  // store (a round trip under load outlasts one iteration's arithmetic).
+  using Regs = TileRegs<bf16, D, GT>;
+  Regs kA, vA, kB, vB;
+  auto load_into = [&](Regs& kr, Regs& vr, int kt) {
     const long roff = (long)kTile * kt * kvstride;
-    kreg.load(kbase + roff, kvstride, td.len - kTile * kt, gtid);
-    vreg.load(vbase + roff, kvstride, td.len - kTile * kt, gtid);
+    kr.load(kbase + roff, kvstride, td.len - kTile * kt, gtid);
+    vr.load(vbase + roff, kvstride, td.len - kTile * kt, gtid);
   };
-  auto store_tile = [&](int buf) {
-    kreg.store(glds + buf * 2 * L::TILE, gtid);
-    vreg.store(glds + buf * 2 * L::TILE + L::TILE, gtid);
+  auto store_from = [&](const Regs& kr, const Regs& vr, int buf) {
+    kr.store(glds + buf * 2 * L::TILE, gtid);
+    vr.store(glds + buf * 2 * L::TILE + L::TILE, gtid);
   };
-  if (grp <= td.tile) load_tile(grp);
+  if (grp <= td.tile) load_into(kA, vA, grp);
+  if (grp + G <= td.tile) load_into(kB, vB, grp + G);
 
   // Q fragments, rotated in fp32 then rounded to bf16 (group 0).
   Frag qf[NKD];
@@ -433,20 +438,13 @@ __global__ __launch_bounds__(kFwdThreads) void attn_fwd_bf16_kernel(
     for (int kk = 0; kk < NKD; ++kk) qlds[kk * 64] = qf[kk];
   }
 
-  // The group's first two tiles into its two buffers (both loads in flight
-  // together; the second set of registers is dead once the loop starts).
-  if (grp + G <= td.tile) {
-    TileRegs<bf16, D, GT> kreg1, vreg1;
-    const long roff = (long)kTile * (grp + G) * kvstride;
-    kreg1.load(kbase + roff, kvstride, td.len - kTile * (grp + G), gtid);
-    vreg1.load(vbase + roff, kvstride, td.len - kTile * (grp + G), gtid);
-    store_tile(0);
-    kreg1.store(glds + 2 * L::TILE, gtid);
-    vreg1.store(glds + 3 * L::TILE, gtid);
-  } else if (grp <= td.tile) {
-    store_tile(0);
-  }
+  // The group's first two tiles into its two buffers; the third tile's loads
+  // go out once everything before them has completed, and stay in flight
+  // through the first iteration.
+  if (grp <= td.tile) store_from(kA, vA, 0);
+  if (grp + G <= td.tile) store_from(kB, vB, 1);
   wait_vmem_all();
+  if (grp + 2 * G <= td.tile) load_into(kA, vA, grp + 2 * G);
   __syncthreads();
   if (grp != 0) {
 #pragma unroll
@@ -520,12 +518,14 @@ __global__ __launch_bounds__(kFwdThreads) void attn_fwd_bf16_kernel(
     acc_rows<bf16, D>(o, vcur, p, DIAG ? wq + 1 : 4, lane);
   };
 
+  // Iteration it: buffer it&1 holds tile kt (its V multiplies now), the other
+  // buffer tile kt + G (its K gives the next scores).  (kl, vl) receive tile
+  // kt + 3G; (ks, vs) hold tile kt + 2G, stored into buffer it&1 at the end.
   const int nit = (td.tile + G) / G;  // iterations of group 0 (the most)
-  for (int it = 0; it < nit; ++it) {
+  auto iter = [&](int it, Regs& kl, Regs& vl, const Regs& ks, const Regs& vs) {
     const int kt = grp + G * it;
     const int cur = it & 1;
-    const bool pre = kt + 2 * G <= td.tile;
-    if (pre) load_tile(kt + 2 * G);
+    if (kt + 3 * G <= td.tile) load_into(kl, vl, kt + 3 * G);
     float scn[4][4];
     const bf16* vcur = glds + cur * 2 * L::TILE + L::TILE;
     const bf16* knext = glds + (cur ^ 1) * 2 * L::TILE;
@@ -535,13 +535,17 @@ __global__ __launch_bounds__(kFwdThreads) void attn_fwd_bf16_kernel(
       step(vcur, knext, scn, std::true_type{});
     if (it + 1 < nit) {
       __syncthreads();
-      if (pre) store_tile(cur);
+      if (kt + 2 * G <= td.tile) store_from(ks, vs, cur);
       __syncthreads();
     }
 #pragma unroll
     for (int b = 0; b < 4; ++b)
 #pragma unroll
       for (int r = 0; r < 4; ++r) sc[b][r] = scn[b][r];
+  };
+  for (int it = 0; it < nit; it += 2) {
+    iter(it, kB, vB, kA, vA);
+    if (it + 1 < nit) iter(it + 1, kA, vA, kB, vB);
   }
 
   // Merge group 1 into group 0 (lane for lane: waves wq and wq + 4 own the
