@@ -656,7 +656,6 @@ __device__ inline void bwd_dq_tile(
   const int g = lane >> 4, c = lane & 15;
   const int qrow = kTile * td.tile + 16 * wq + c;
   const bool qvalid = qrow < td.len;
-  const long qbase = ((long)(td.tok0 + qrow) * n_heads_q + h) * D;
   T* const glds = lds + grp * 4 * L::TILE;
 
   const long kvstride = (long)n_heads_kv * D;
@@ -669,19 +668,19 @@ __device__ inline void bwd_dq_tile(
     vreg.load(vbase + roff, kvstride, td.len - kTile * grp, gtid);
   }
 
-  // This tile's dO and O rows for the row terms D_i (all threads).
+  // This tile's Q, dO and O rows (all threads, coalesced): dO and O give
+  // the row terms D_i; Q and dO go through LDS to become the waves' operand
+  // fragments.
   const long qstride = (long)n_heads_q * D;
   const long trow = ((long)(td.tok0 + kTile * td.tile) * n_heads_q + h) * D;
-  Regs dreg, oreg;
+  Regs qreg, dreg, oreg;
+  qreg.load(q_rot + trow, qstride, td.len - kTile * td.tile, tid);
   dreg.load(d_out + trow, qstride, td.len - kTile * td.tile, tid);
   oreg.load(out + trow, qstride, td.len - kTile * td.tile, tid);
-
+  // Q and dO staging: group 0's second buffer, first written at the end of
+  // its first iteration.
+  T* const stg = lds + 2 * L::TILE;
   typename M::Frag qf[NKD], df[NKD];
-#pragma unroll
-  for (int kk = 0; kk < NKD; ++kk) {
-    qf[kk] = qvalid ? frag_global<T>(q_rot + qbase, kk, g) : frag_zero<T>();
-    df[kk] = qvalid ? frag_global<T>(d_out + qbase, kk, g) : frag_zero<T>();
-  }
   const long si = (long)h * total_tokens + td.tok0 + qrow;
   const float lse_q = qvalid ? lse[si] : 0.0f;
 
@@ -720,6 +719,8 @@ __device__ inline void bwd_dq_tile(
     kreg.store(glds, gtid);
     vreg.store(glds + L::TILE, gtid);
   }
+  qreg.store(stg, tid);
+  dreg.store(stg + L::TILE, tid);
 #pragma unroll
   for (int i = 0; i < Regs::N; ++i) {
     const float part = row_term(dreg, oreg, i);
@@ -728,8 +729,14 @@ __device__ inline void bwd_dq_tile(
   }
   wait_vmem_all();
   __syncthreads();
+#pragma unroll
+  for (int kk = 0; kk < NKD; ++kk) {
+    qf[kk] = frag_rm<T, D>(stg, 16 * wq + c, kk, g);
+    df[kk] = frag_rm<T, D>(stg + L::TILE, 16 * wq + c, kk, g);
+  }
   drow = qvalid ? dsm[16 * wq + c] : 0.0f;
   nlse2 = qvalid ? -lse_q * kLog2e : 0.0f;
+  __syncthreads();  // the staging area is free again
 
   const int nit = (td.tile + G) / G;
   for (int it = 0; it < nit; ++it) {
@@ -826,9 +833,6 @@ __device__ inline void bwd_dkdv_tile(
   const int tid = threadIdx.x, w = wave_id(), lane = tid & 63;
   const int grp = w >> 2, wq = w & 3, gtid = tid & (kThreads - 1);
   const int g = lane >> 4, c = lane & 15;
-  const int krow = kTile * td.tile + 16 * wq + c;
-  const bool kvalid = krow < td.len;
-  const long kbase = ((long)(td.tok0 + krow) * n_heads_kv + kvh) * D;
   unsigned char* const gsm = smem_raw + grp * 2 * BUF;
 
   const int ntq = (td.len + kTile - 1) / kTile;
@@ -868,15 +872,24 @@ __device__ inline void bwd_dkdv_tile(
     }
   };
 
+  // The key tile's K and V rows (all threads, coalesced), staged in group
+  // 0's second buffer (first written at the end of its first iteration) and
+  // read back as the waves' operand fragments; then each group's first query
+  // tile.
+  using KRegs = TileRegs<IO, D, kThreads * G>;
+  KRegs kst, vst;
+  {
+    const long krow0 = ((long)(td.tok0 + kTile * td.tile) * n_heads_kv + kvh) * D;
+    const long kvstride = (long)n_heads_kv * D;
+    kst.load(k_rot + krow0, kvstride, td.len - kTile * td.tile, tid);
+    vst.load(v + krow0, kvstride, td.len - kTile * td.tile, tid);
+  }
   const int first = td.tile + grp;
   if (first < ntq) load_tile(first);
-
+  T* const kvs = reinterpret_cast<T*>(smem_raw + BUF);
+  kst.store(kvs, tid);
+  vst.store(kvs + L::TILE, tid);
   typename M::Frag kf[NKD], vf[NKD];
-#pragma unroll
-  for (int kk = 0; kk < NKD; ++kk) {
-    kf[kk] = kvalid ? frag_global<T>(k_rot + kbase, kk, g) : frag_zero<T>();
-    vf[kk] = kvalid ? frag_global<T>(v + kbase, kk, g) : frag_zero<T>();
-  }
 
   f32x4 acc_dk[D / 16], acc_dv[D / 16];
 #pragma unroll
@@ -921,6 +934,12 @@ __device__ inline void bwd_dkdv_tile(
   if (first < ntq) store_tile(0, first);
   wait_vmem_all();
   __syncthreads();
+#pragma unroll
+  for (int kk = 0; kk < NKD; ++kk) {
+    kf[kk] = frag_rm<T, D>(kvs, 16 * wq + c, kk, g);
+    vf[kk] = frag_rm<T, D>(kvs + L::TILE, 16 * wq + c, kk, g);
+  }
+  __syncthreads();  // the staging area is free again
 
   const int nit = (ntq - td.tile + G - 1) / G;  // iterations of group 0 (the most)
   for (int it = 0; it < nit; ++it) {
