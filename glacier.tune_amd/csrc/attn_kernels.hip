@@ -382,7 +382,6 @@ __global__ __launch_bounds__(kFwdThreads) void attn_fwd_bf16_kernel(
   const int g = lane >> 4, c = lane & 15;
   const int qrow = kTile * td.tile + 16 * wq + c;
   const bool qvalid = qrow < td.len;
-  const long qbase = ((long)(td.tok0 + qrow) * n_heads_q + h) * D;
   bf16* const glds = lds + grp * 4 * L::TILE;  // buffer b: glds + b * 2 * TILE
 
   const long kvstride = (long)n_heads_kv * D;
@@ -405,38 +404,42 @@ __global__ __launch_bounds__(kFwdThreads) void attn_fwd_bf16_kernel(
   if (grp <= td.tile) load_into(kA, vA, grp);
   if (grp + G <= td.tile) load_into(kB, vB, grp + G);
 
-  // Q fragments, rotated in fp32 then rounded to bf16 (group 0).
-  Frag qf[NKD];
-  Frag* const qlds = reinterpret_cast<Frag*>(lds + 4 * G * L::TILE) + wq * NKD * 64 + lane;
-  if (grp == 0) {
-#pragma unroll
-    for (int kk = 0; kk < NKD / 2; ++kk) {
-      const int d0 = kk * M::KSTEP + 8 * g;
-      float x0[8], x1[8], y0[8], y1[8], cs[8], sn[8];
-      if (qvalid) {
-        load8(q + qbase + d0, x0);
-        load8(q + qbase + d0 + H, x1);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) x0[e] = x1[e] = 0.0f;
-      }
-      const long ti = (long)(qvalid ? qrow : 0) * H + d0;
+  // Q: the tile's rows are loaded by all threads (coalesced, 8 rotation pairs
+  // per thread), rotated in fp32 (rope_fwd) and rounded to bf16, written to
+  // q_rot as whole rows and to LDS, from where every wave reads its operand
+  // fragments.  The LDS copy is unpadded ([64][D]) with its 16-byte chunks
+  // XOR-swizzled by row (chunk ch of row r at ch ^ (r mod CPR)), so that the
+  // 16 rows of a fragment read fall in distinct banks.
+  constexpr int QCPR = D / 8;  // 16-byte bf16 chunks per row
+  bf16* const qst = lds + 4 * G * L::TILE;
+  {
+    constexpr int PPR = H / 8;  // 8-pair chunks per row
+    const long qrow0 = (long)td.tok0 + kTile * td.tile;
+    const int nv = td.len - kTile * td.tile;
+    for (int idx = tid; idx < kTile * PPR; idx += kFwdThreads) {
+      const int r = idx / PPR, j = idx % PPR;
+      const bool valid = r < nv;
+      const long gq = ((qrow0 + (valid ? r : 0)) * n_heads_q + h) * D + 8 * j;
+      float x0[8], x1[8], cs[8], sn[8], y0[8], y1[8];
+      load8(q + gq, x0);
+      load8(q + gq + H, x1);
+      const long ti = (long)(kTile * td.tile + (valid ? r : 0)) * H + 8 * j;
       load8(cos_t + ti, cs);
       load8(sin_t + ti, sn);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        rope_fwd(x0[e], x1[e], cs[e], sn[e], y0[e], y1[e]);
-        qf[kk][e] = (bf16)y0[e];
-        qf[kk + NKD / 2][e] = (bf16)y1[e];
+        rope_fwd(valid ? x0[e] : 0.0f, valid ? x1[e] : 0.0f, cs[e], sn[e], y0[e], y1[e]);
       }
-      if (q_rot != nullptr && qvalid) {
-        store8(q_rot + qbase + d0, y0);
-        store8(q_rot + qbase + d0 + H, y1);
+      if (q_rot != nullptr && valid) {
+        store8(q_rot + gq, y0);
+        store8(q_rot + gq + H, y1);
       }
+      const int sw = r & (QCPR - 1);
+      store8(qst + r * D + 8 * (j ^ sw), y0);
+      store8(qst + r * D + 8 * ((PPR + j) ^ sw), y1);
     }
-#pragma unroll
-    for (int kk = 0; kk < NKD; ++kk) qlds[kk * 64] = qf[kk];
   }
+  Frag qf[NKD];
 
   // The group's first two tiles into its two buffers; the third tile's loads
   // go out once everything before them has completed, and stay in flight
@@ -446,9 +449,13 @@ __global__ __launch_bounds__(kFwdThreads) void attn_fwd_bf16_kernel(
   wait_vmem_all();
   if (grp + 2 * G <= td.tile) load_into(kA, vA, grp + 2 * G);
   __syncthreads();
-  if (grp != 0) {
+  {
+    const int row = 16 * wq + c;
 #pragma unroll
-    for (int kk = 0; kk < NKD; ++kk) qf[kk] = qlds[kk * 64];
+    for (int kk = 0; kk < NKD; ++kk) {
+      const int ch = (kk * M::KSTEP + M::KPL * g) / 8;  // logical chunk of the fragment
+      qf[kk] = *reinterpret_cast<const bf16x8*>(qst + row * D + 8 * (ch ^ (row & (QCPR - 1))));
+    }
   }
 
   f32x4 o[D / 16];
