@@ -1,6 +1,12 @@
 """Builds libglacier_attn.so (gfx950) in place with hipcc.
 
     python glacier.tune_amd/build.py
+    python glacier.tune_amd/build.py --stamps OUT.so   # profiling build
+
+The profiling build defines GLACIER_PHASE_STAMPS: every workgroup records
+wall-clock stamps at the phases of its kernel (GL_STAMP in attn_common.hpp),
+readable with glacier_attn_debug_stamps().  It is written to OUT.so, never
+over the product library.
 
 Every HIP translation unit is compiled with the packed-fp32 target feature
 disabled (-Xclang -target-feature -Xclang -packed-fp32-ops): the compiler
@@ -37,9 +43,9 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (ROCm is required to build libglacier_attn.so)")
 
 
-def _compile(src: str) -> str:
-    obj = os.path.join(OBJDIR, os.path.basename(src) + ".o")
-    cmd = [hipcc(), *COMMON, "-c", os.path.join(CSRC, src), "-o", obj]
+def _compile(src: str, objdir: str = OBJDIR, extra: tuple = ()) -> str:
+    obj = os.path.join(objdir, os.path.basename(src) + ".o")
+    cmd = [hipcc(), *COMMON, *extra, "-c", os.path.join(CSRC, src), "-o", obj]
     res = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     err = "\n".join(l for l in res.stderr.splitlines() if noise not in l)
@@ -50,20 +56,28 @@ def _compile(src: str) -> str:
     return obj
 
 
-def build(verbose: bool = False) -> str:
-    os.makedirs(OBJDIR, exist_ok=True)
+def build(verbose: bool = False, out: str = OUT, stamps: bool = False) -> str:
+    objdir = OBJDIR + ("_stamps" if stamps else "")
+    extra = ("-DGLACIER_PHASE_STAMPS",) if stamps else ()
+    os.makedirs(objdir, exist_ok=True)
     with cf.ThreadPoolExecutor(max_workers=len(SOURCES)) as ex:
-        objs = list(ex.map(_compile, SOURCES))
-    tmp = OUT + ".tmp"
+        objs = list(ex.map(lambda src: _compile(src, objdir, extra), SOURCES))
+    tmp = out + ".tmp"
     cmd = [hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError("link failed:\n" + res.stderr)
-    os.replace(tmp, OUT)
+    os.replace(tmp, out)
     if verbose:
-        print("built", OUT)
-    return OUT
+        print("built", out)
+    return out
 
 
 if __name__ == "__main__":
-    build(verbose=True)
+    if len(sys.argv) == 3 and sys.argv[1] == "--stamps":
+        target = os.path.abspath(sys.argv[2])
+        if target == OUT:
+            sys.exit("--stamps must not overwrite the product library")
+        build(verbose=True, out=target, stamps=True)
+    else:
+        build(verbose=True)

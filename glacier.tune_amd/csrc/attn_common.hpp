@@ -286,6 +286,27 @@ __device__ inline void acc_rows(f32x4 (&acc)[D / 16], const T* tile,
   }
 }
 
+// Phase timestamps for profiling builds (-DGLACIER_PHASE_STAMPS, see
+// build.py --stamps): thread 0 of a workgroup records the wall clock (100 MHz)
+// at named points of a kernel into glacier_stamps[kernel][workgroup][slot];
+// GL_STAMP_VALUE records a plain value (which tile the workgroup took).  In
+// the product build both expand to nothing.
+#ifdef GLACIER_PHASE_STAMPS
+constexpr int kStampKernels = 4, kStampBlocks = 4096, kStampSlots = 32;
+extern __device__ unsigned long long glacier_stamps[kStampKernels][kStampBlocks][kStampSlots];
+__device__ inline void phase_stamp(int kernel, int slot, unsigned long long value) {
+  if (threadIdx.x == 0) {
+    const unsigned b = (blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
+    if (b < kStampBlocks) glacier_stamps[kernel][b][slot] = value;
+  }
+}
+#define GL_STAMP(kernel, slot) ::glacier::phase_stamp(kernel, slot, wall_clock64())
+#define GL_STAMP_VALUE(kernel, slot, v) ::glacier::phase_stamp(kernel, slot, (v))
+#else
+#define GL_STAMP(kernel, slot) ((void)0)
+#define GL_STAMP_VALUE(kernel, slot, v) ((void)0)
+#endif
+
 // Index of this wave in the workgroup, as a scalar: the compiler cannot
 // prove threadIdx.x / 64 uniform, and values derived from it (the group's
 // tile, its base pointers) must live in scalar registers to form buffer

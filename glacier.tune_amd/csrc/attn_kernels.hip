@@ -33,6 +33,10 @@
 
 namespace glacier {
 
+#ifdef GLACIER_PHASE_STAMPS
+__device__ unsigned long long glacier_stamps[kStampKernels][kStampBlocks][kStampSlots];
+#endif
+
 // ---------------------------------------------------------------------------
 // RoPE, written without contraction so that q_rot/k_rot are the exact fp32
 // results of RoPEKernel.cs:84-85 (v0*c - v1*s, v0*s + v1*c) given the same
@@ -378,6 +382,8 @@ __global__ __launch_bounds__(kFwdThreads) void attn_fwd_bf16_kernel(
   const TileDesc td = VARLEN ? tiles[blockIdx.z]
                              : TileDesc{0, total_tokens, n_tiles - 1 - (int)blockIdx.z, 0};
   const int tid = threadIdx.x, w = wave_id(), lane = tid & 63;
+  GL_STAMP(kKernFwd, 0);
+  GL_STAMP_VALUE(kKernFwd, 31, td.tile);
   const int grp = w >> 2, wq = w & 3, gtid = tid & (GT - 1);
   const int g = lane >> 4, c = lane & 15;
   const int qrow = kTile * td.tile + 16 * wq + c;
@@ -439,6 +445,7 @@ __global__ __launch_bounds__(kFwdThreads) void attn_fwd_bf16_kernel(
       store8(qst + r * D + 8 * ((PPR + j) ^ sw), y1);
     }
   }
+  GL_STAMP(kKernFwd, 1);
   Frag qf[NKD];
 
   // The group's first two tiles into its two buffers; the third tile's loads
@@ -446,9 +453,12 @@ __global__ __launch_bounds__(kFwdThreads) void attn_fwd_bf16_kernel(
   // through the first iteration.
   if (grp <= td.tile) store_from(kA, vA, 0);
   if (grp + G <= td.tile) store_from(kB, vB, 1);
+  GL_STAMP(kKernFwd, 22);
   wait_vmem_all();
   if (grp + 2 * G <= td.tile) load_into(kA, vA, grp + 2 * G);
+  GL_STAMP(kKernFwd, 23);
   __syncthreads();
+  GL_STAMP(kKernFwd, 2);
   {
     const int row = 16 * wq + c;
 #pragma unroll
@@ -478,6 +488,7 @@ __global__ __launch_bounds__(kFwdThreads) void attn_fwd_bf16_kernel(
 
   float sc[4][4];
   if (grp <= td.tile) scores(glds, sc);
+  GL_STAMP(kKernFwd, 3);
 
   // Softmax of the current tile's scores (masked on the diagonal tile),
   // interleaved with the next tile's scores, then O^T += V^T P^T.
@@ -540,11 +551,13 @@ __global__ __launch_bounds__(kFwdThreads) void attn_fwd_bf16_kernel(
       step(vcur, knext, scn, std::false_type{});
     else if (kt == td.tile)
       step(vcur, knext, scn, std::true_type{});
+    if (it < 8) GL_STAMP(kKernFwd, 4 + 2 * it);
     if (it + 1 < nit) {
       __syncthreads();
       if (kt + 2 * G <= td.tile) store_from(ks, vs, cur);
       __syncthreads();
     }
+    if (it < 8) GL_STAMP(kKernFwd, 5 + 2 * it);
 #pragma unroll
     for (int b = 0; b < 4; ++b)
 #pragma unroll
@@ -555,6 +568,7 @@ __global__ __launch_bounds__(kFwdThreads) void attn_fwd_bf16_kernel(
     if (it + 1 < nit) iter(it + 1, kA, vA, kB, vB);
   }
 
+  GL_STAMP(kKernFwd, 20);
   // Merge group 1 into group 0 (lane for lane: waves wq and wq + 4 own the
   // same queries); 16-byte LDS accesses: (max, sum), then O.  Then O goes
   // through LDS (row-major, output dtype, in group 1's region) so that all
@@ -598,6 +612,7 @@ __global__ __launch_bounds__(kFwdThreads) void attn_fwd_bf16_kernel(
       *reinterpret_cast<uint4*>(out + ((orow0 + r) * n_heads_q + h) * D + ch * (16 / sizeof(IO))) =
           *reinterpret_cast<const uint4*>(ot + r * OS + ch * (16 / sizeof(IO)));
   }
+  GL_STAMP(kKernFwd, 21);
 }
 
 // ---------------------------------------------------------------------------
@@ -659,6 +674,8 @@ __device__ inline void bwd_dq_tile(
   const int ratio = gridDim.x, n_heads_kv = gridDim.y, n_heads_q = ratio * n_heads_kv;
   const int kvh = blockIdx.y, h = kvh * ratio + blockIdx.x;
   const int tid = threadIdx.x, w = wave_id(), lane = tid & 63;
+  GL_STAMP(kKernBwd, 0);
+  GL_STAMP_VALUE(kKernBwd, 31, 100 + td.tile);
   const int grp = w >> 2, wq = w & 3, gtid = tid & (kThreads - 1);
   const int g = lane >> 4, c = lane & 15;
   const int qrow = kTile * td.tile + 16 * wq + c;
@@ -687,6 +704,7 @@ __device__ inline void bwd_dq_tile(
   // Q and dO staging: group 0's second buffer, first written at the end of
   // its first iteration.
   T* const stg = lds + 2 * L::TILE;
+  GL_STAMP(kKernBwd, 1);
   typename M::Frag qf[NKD], df[NKD];
   const long si = (long)h * total_tokens + td.tok0 + qrow;
   const float lse_q = qvalid ? lse[si] : 0.0f;
@@ -744,6 +762,7 @@ __device__ inline void bwd_dq_tile(
   drow = qvalid ? dsm[16 * wq + c] : 0.0f;
   nlse2 = qvalid ? -lse_q * kLog2e : 0.0f;
   __syncthreads();  // the staging area is free again
+  GL_STAMP(kKernBwd, 2);
 
   const int nit = (td.tile + G) / G;
   for (int it = 0; it < nit; ++it) {
@@ -760,14 +779,18 @@ __device__ inline void bwd_dq_tile(
       step(ks, ks + L::TILE, std::false_type{});
     else if (kt == td.tile)
       step(ks, ks + L::TILE, std::true_type{});
+    if (it < 6) GL_STAMP(kKernBwd, 3 + 3 * it);
     if (more) {
       T* nxt = glds + ((it + 1) & 1) * 2 * L::TILE;
       kreg.store(nxt, gtid);
       vreg.store(nxt + L::TILE, gtid);
     }
+    if (it < 6) GL_STAMP(kKernBwd, 4 + 3 * it);
     __syncthreads();
+    if (it < 6) GL_STAMP(kKernBwd, 5 + 3 * it);
   }
 
+  GL_STAMP(kKernBwd, 21);
   if constexpr (G == 2) {
     f32x4* const cmb = reinterpret_cast<f32x4*>(lds + 4 * L::TILE) + wq * (D / 16) * 64 + lane;
     if (grp == 1) {
@@ -818,6 +841,7 @@ __device__ inline void bwd_dq_tile(
                                 pc * EPC) =
           *reinterpret_cast<const uint4*>(stq + r * SR + pc * EPC);
   }
+  GL_STAMP(kKernBwd, 22);
 }
 
 // dK/dV partial of one (query head, key tile); z indexes the key tiles.
@@ -838,6 +862,8 @@ __device__ inline void bwd_dkdv_tile(
   const int ratio = gridDim.x, n_heads_kv = gridDim.y, n_heads_q = ratio * n_heads_kv;
   const int kvh = blockIdx.y, h = kvh * ratio + blockIdx.x;
   const int tid = threadIdx.x, w = wave_id(), lane = tid & 63;
+  GL_STAMP(kKernBwd, 0);
+  GL_STAMP_VALUE(kKernBwd, 31, td.tile);
   const int grp = w >> 2, wq = w & 3, gtid = tid & (kThreads - 1);
   const int g = lane >> 4, c = lane & 15;
   unsigned char* const gsm = smem_raw + grp * 2 * BUF;
@@ -893,6 +919,7 @@ __device__ inline void bwd_dkdv_tile(
   }
   const int first = td.tile + grp;
   if (first < ntq) load_tile(first);
+  GL_STAMP(kKernBwd, 1);
   T* const kvs = reinterpret_cast<T*>(smem_raw + BUF);
   kst.store(kvs, tid);
   vst.store(kvs + L::TILE, tid);
@@ -947,6 +974,7 @@ __device__ inline void bwd_dkdv_tile(
     vf[kk] = frag_rm<T, D>(kvs + L::TILE, 16 * wq + c, kk, g);
   }
   __syncthreads();  // the staging area is free again
+  GL_STAMP(kKernBwd, 2);
 
   const int nit = (ntq - td.tile + G - 1) / G;  // iterations of group 0 (the most)
   for (int it = 0; it < nit; ++it) {
@@ -958,10 +986,14 @@ __device__ inline void bwd_dkdv_tile(
       step(base, std::true_type{});
     else if (qt < ntq)
       step(base, std::false_type{});
+    if (it < 6) GL_STAMP(kKernBwd, 3 + 3 * it);
     if (more) store_tile((it + 1) & 1, qt + G);
+    if (it < 6) GL_STAMP(kKernBwd, 4 + 3 * it);
     __syncthreads();
+    if (it < 6) GL_STAMP(kKernBwd, 5 + 3 * it);
   }
 
+  GL_STAMP(kKernBwd, 21);
   // Merge the groups and write whole rows: the [64 keys][D] fp32 dK and dV
   // tiles are staged in LDS (row stride D + 4 floats, so the 16 key rows of
   // a wave's store fall in distinct banks), then every thread stores 16-byte
@@ -1008,6 +1040,7 @@ __device__ inline void bwd_dkdv_tile(
       store4(wv + wb, *reinterpret_cast<const f32x4*>(stv + r * SR + 4 * c4));
     }
   }
+  GL_STAMP(kKernBwd, 22);
 }
 
 // z indexes tiles_bwd, the dK/dV and dQ tiles in launch order.  The
@@ -1040,6 +1073,7 @@ __global__ __launch_bounds__(kRedThreads) void attn_bwd_reduce_kernel(
   constexpr int H = D / 2;
   constexpr int CH = H / 4;  // 4-pair chunks per row
   constexpr int ROWS = kRedThreads / CH;
+  GL_STAMP(kKernReduce, 0);
   const long row = (long)blockIdx.x * ROWS + threadIdx.x / CH;  // token * Hkv + kv head
   if (row >= (long)total_tokens * n_heads_kv) return;
   const int p0 = 4 * (threadIdx.x % CH);
@@ -1096,6 +1130,7 @@ __global__ __launch_bounds__(kRedThreads) void attn_bwd_reduce_kernel(
   store4(dk + dst + H, y1);
   store4(dv + dst, v0);
   store4(dv + dst + H, v1);
+  GL_STAMP(kKernReduce, 22);
 }
 
 // ---------------------------------------------------------------------------
@@ -1247,3 +1282,10 @@ size_t compute_elem_size(int precision, bool io_bf16) {
 }
 
 }  // namespace glacier
+
+#ifdef GLACIER_PHASE_STAMPS
+// Profiling builds only: copies the phase stamps to host memory.
+extern "C" int glacier_attn_debug_stamps(void* host, size_t bytes) {
+  return static_cast<int>(hipMemcpyFromSymbol(host, HIP_SYMBOL(glacier::glacier_stamps), bytes));
+}
+#endif
