@@ -34,11 +34,17 @@ PEAK_BF16_TFLOPS = 2500.0
 METRIC = "causal GQA attn fwd+bwd TFLOP/s + % bf16 MFMA peak, Qwen2.5-7B shape S=512"
 
 CONFIGS = {
-    # name: (lengths, Hq, Hkv, D, theta)
-    "qwen7b_s512": ([512], 28, 4, 128, 1.0e6),
-    "qwen05b_s512": ([512], 14, 2, 64, 1.0e6),
-    "qwen7b_s4096": ([4096], 28, 4, 128, 1.0e6),
-    "llama3_b2_s2048": ([2048, 2048], 32, 8, 128, 5.0e5),
+    # name: (lengths, Hq, Hkv, D, theta, layers).  layers == 1: one attention
+    # layer's forward + backward; layers > 1: a checkpointed training step,
+    # where every layer runs forward (no save), then, in reverse layer order,
+    # the recompute forward (saving lse, q_rot, k_rot) and the backward.
+    "qwen7b_s512": ([512], 28, 4, 128, 1.0e6, 1),
+    "qwen05b_s512": ([512], 14, 2, 64, 1.0e6, 1),
+    "qwen7b_s4096": ([4096], 28, 4, 128, 1.0e6, 1),
+    "llama3_b2_s2048": ([2048, 2048], 32, 8, 128, 5.0e5, 1),
+    # 28 layers, 4 packed sequences with lengths
+    # drawn from U[64, 512] by numpy.random.default_rng(5).integers(64, 513, 4)
+    "qwen7b_ckpt28_varlen": ([365, 425, 74, 426], 28, 4, 128, 1.0e6, 28),
 }
 
 # Algorithmic FLOPs per unmasked (query, key, head) triple, per kernel: the
@@ -121,7 +127,7 @@ def main():
 
     import glacier_attn as ga
 
-    lengths, Hq, Hkv, D, theta = CONFIGS[args.config]
+    lengths, Hq, Hkv, D, theta, layers = CONFIGS[args.config]
     T = sum(lengths)
     cu = None if len(lengths) == 1 else np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
     dev = torch.device("cuda:0")
@@ -133,22 +139,47 @@ def main():
         torch.cuda.synchronize()
         del src, dst
     g = torch.Generator(device=dev).manual_seed(0)
-    q = torch.randn(T, Hq, D, device=dev, generator=g).bfloat16()
-    k = torch.randn(T, Hkv, D, device=dev, generator=g).bfloat16()
-    v = torch.randn(T, Hkv, D, device=dev, generator=g).bfloat16()
-    dO = (0.01 * torch.randn(T, Hq, D, device=dev, generator=g)).bfloat16()
-    out = torch.empty_like(q)
-    lse = torch.empty(Hq, T, device=dev, dtype=torch.float32)
-    q_rot = torch.empty_like(q)
-    k_rot = torch.empty_like(k)
-    dq = torch.empty_like(q)
-    dk = torch.empty_like(k)
-    dv = torch.empty_like(v)
+
+    class Layer:
+        """One layer's device tensors (each layer has its own activations)."""
+
+        def __init__(self):
+            self.q = torch.randn(T, Hq, D, device=dev, generator=g).bfloat16()
+            self.k = torch.randn(T, Hkv, D, device=dev, generator=g).bfloat16()
+            self.v = torch.randn(T, Hkv, D, device=dev, generator=g).bfloat16()
+            self.dO = (0.01 * torch.randn(T, Hq, D, device=dev, generator=g)).bfloat16()
+            self.out = torch.empty_like(self.q)
+            self.lse = torch.empty(Hq, T, device=dev, dtype=torch.float32)
+            self.q_rot = torch.empty_like(self.q)
+            self.k_rot = torch.empty_like(self.k)
+            self.dq = torch.empty_like(self.q)
+            self.dk = torch.empty_like(self.k)
+            self.dv = torch.empty_like(self.v)
+
+    net = [Layer() for _ in range(layers)]
     eng = ga.GpuAttentionEngine(0, ga.PREC_BF16)
 
+    def fwd(L, save):
+        if save:
+            eng.forward(L.q, L.k, L.v, theta, cu_seqlens=cu, out=L.out, lse=L.lse,
+                        q_rot=L.q_rot, k_rot=L.k_rot)
+        else:
+            eng.forward(L.q, L.k, L.v, theta, cu_seqlens=cu, out=L.out, save=False)
+
+    def bwd(L):
+        eng.backward(L.dO, L.q_rot, L.k_rot, L.v, L.out, L.lse, theta, cu_seqlens=cu,
+                     dq=L.dq, dk=L.dk, dv=L.dv)
+
     def step():
-        eng.forward(q, k, v, theta, cu_seqlens=cu, out=out, lse=lse, q_rot=q_rot, k_rot=k_rot)
-        eng.backward(dO, q_rot, k_rot, v, out, lse, theta, cu_seqlens=cu, dq=dq, dk=dk, dv=dv)
+        if layers == 1:
+            fwd(net[0], True)
+            bwd(net[0])
+            return
+        for L in net:
+            fwd(L, False)
+        for L in reversed(net):
+            fwd(L, True)
+            bwd(L)
 
     for _ in range(args.warmup):
         step()
@@ -162,7 +193,9 @@ def main():
     torch.cuda.synchronize()
     ms = start.elapsed_time(stop) / args.steps
 
-    flops = 12.0 * D * Hq * pairs(lengths)
+    # 12 D flop per unmasked (query, key, head) per layer, plus 4 D for the
+    # checkpoint recompute forward in the multi-layer step.
+    flops = (12.0 if layers == 1 else 16.0) * D * Hq * pairs(lengths) * layers
     tflops = flops / (ms * 1e-3) / 1e12
 
     # Per-kernel device time (events timestamped by each launch itself on the
