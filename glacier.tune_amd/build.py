@@ -25,7 +25,14 @@ CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libglacier_attn.so")
 OBJDIR = os.path.join(HERE, "_build")
 
-SOURCES = ["attn_kernels.hip", "engine.cpp"]
+# source -> extra hipcc flags.  attn_fwd.hip: the MFMAs the compiler emits
+# write VGPRs (their results feed VALU code); its accumulators are pinned to
+# AGPRs by inline assembly.
+SOURCES = {
+    "attn_kernels.hip": (),
+    "attn_fwd.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form"),
+    "engine.cpp": (),
+}
 COMMON = [
     "--offload-arch=gfx950",
     "-O3",
@@ -61,7 +68,7 @@ def build(verbose: bool = False, out: str = OUT, stamps: bool = False) -> str:
     extra = ("-DGLACIER_PHASE_STAMPS",) if stamps else ()
     os.makedirs(objdir, exist_ok=True)
     with cf.ThreadPoolExecutor(max_workers=len(SOURCES)) as ex:
-        objs = list(ex.map(lambda src: _compile(src, objdir, extra), SOURCES))
+        objs = list(ex.map(lambda src: _compile(src, objdir, extra + SOURCES[src]), SOURCES))
     tmp = out + ".tmp"
     cmd = [hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp]
     res = subprocess.run(cmd, capture_output=True, text=True)

@@ -119,16 +119,17 @@ __device__ inline void store4(bf16* p, f32x4 v) {
   *reinterpret_cast<bf16x4*>(p) = b;
 }
 
-// This thread's share of a [64][D] tile held in registers between a global
-// load and an LDS store (the software pipeline of every kernel's main loop).
-// Chunks are 8 consecutive elements of one row; chunk index tid + i*NT maps
-// to (row, chunk) with the chunk fastest, so a wave reads whole rows.
-template <typename IO, int D, int NT = kThreads>
+// This thread's share of a [ROWS][D] tile (64 rows, or a 32-row key chunk)
+// held in registers between a global load and an LDS store (the software
+// pipeline of every kernel's main loop).  Chunks are 8 consecutive elements
+// of one row; chunk index tid + i*NT maps to (row, chunk) with the chunk
+// fastest, so a wave reads whole rows.
+template <typename IO, int D, int NT = kThreads, int ROWS = kTile>
 struct TileRegs {
   static constexpr int CPR = D / 8;                  // chunks per row
-  static constexpr int N = kTile * CPR / NT;         // chunks per thread
+  static constexpr int N = ROWS * CPR / NT;          // chunks per thread
   static constexpr int W = 8 * sizeof(IO) / 16;      // 16-byte words per chunk
-  static_assert(N * NT == kTile * CPR, "tile must split evenly");
+  static_assert(N * NT == ROWS * CPR, "tile must split evenly");
   i32x4 w[N][W];
 
   // Rows r >= nvalid read as zero (past the end of the sequence): the loads
@@ -141,7 +142,7 @@ struct TileRegs {
   // from its first lane).
   __device__ inline void load(const IO* src, long gstride, int nvalid, int tid) {
     const int rowb = __builtin_amdgcn_readfirstlane(static_cast<int>(gstride * (long)sizeof(IO)));
-    const int nv = nvalid < kTile ? nvalid : kTile;
+    const int nv = nvalid < ROWS ? nvalid : ROWS;
     const int nrec = __builtin_amdgcn_readfirstlane(
         nv <= 0 ? 0 : (nv - 1) * rowb + D * static_cast<int>(sizeof(IO)));
     const unsigned long long a = reinterpret_cast<unsigned long long>(src);
@@ -286,14 +287,32 @@ __device__ inline void acc_rows(f32x4 (&acc)[D / 16], const T* tile,
   }
 }
 
+// RoPE, written without contraction so that q_rot/k_rot are the exact fp32
+// results of RoPEKernel.cs:84-85 (v0*c - v1*s, v0*s + v1*c) given the same
+// cos/sin table.
+__device__ inline void rope_fwd(float x0, float x1, float c, float s, float& y0,
+                                float& y1) {
+#pragma clang fp contract(off)
+  y0 = x0 * c - x1 * s;
+  y1 = x0 * s + x1 * c;
+}
+// inverse rotation (sin negated, RoPEKernel.cs:60)
+__device__ inline void rope_inv(float x0, float x1, float c, float s, float& y0,
+                                float& y1) {
+#pragma clang fp contract(off)
+  y0 = x0 * c + x1 * s;
+  y1 = x1 * c - x0 * s;
+}
+
 // Phase timestamps for profiling builds (-DGLACIER_PHASE_STAMPS, see
 // build.py --stamps): thread 0 of a workgroup records the wall clock (100 MHz)
-// at named points of a kernel into glacier_stamps[kernel][workgroup][slot];
+// at named points of a kernel into glacier_stamps[kernel][workgroup][slot]
+// (one array per source file: each has its own device code object);
 // GL_STAMP_VALUE records a plain value (which tile the workgroup took).  In
 // the product build both expand to nothing.
 #ifdef GLACIER_PHASE_STAMPS
 constexpr int kStampKernels = 4, kStampBlocks = 4096, kStampSlots = 32;
-extern __device__ unsigned long long glacier_stamps[kStampKernels][kStampBlocks][kStampSlots];
+static __device__ unsigned long long glacier_stamps[kStampKernels][kStampBlocks][kStampSlots];
 __device__ inline void phase_stamp(int kernel, int slot, unsigned long long value) {
   if (threadIdx.x == 0) {
     const unsigned b = (blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
@@ -340,6 +359,29 @@ __device__ inline float lanes_sum(float x) {
   if constexpr (N == 32) x += __shfl_xor(x, 16);
   return x;
 }
+
+// Max / sum over the 4 lanes that share a column (lanes l, l^16, l^32,
+// l^48) with the gfx950 lane-swap instructions: v_permlane32_swap of a value
+// with itself leaves each lane one operand from its own half and one from
+// the other, v_permlane16_swap likewise for the two rows of a half; no LDS
+// traffic and no wait.  For the sum both lanes of a pair add the same two
+// operands in the same order, so every lane gets the same bits.
+__device__ inline float swap_max(float x, bool rows16) {
+  const unsigned u = __builtin_bit_cast(unsigned, x);
+  const auto r = rows16 ? __builtin_amdgcn_permlane16_swap(u, u, false, false)
+                        : __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  const unsigned a = r[0], b = r[1];
+  return fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+}
+__device__ inline float swap_sum(float x, bool rows16) {
+  const unsigned u = __builtin_bit_cast(unsigned, x);
+  const auto r = rows16 ? __builtin_amdgcn_permlane16_swap(u, u, false, false)
+                        : __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  const unsigned a = r[0], b = r[1];
+  return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+}
+__device__ inline float col_max_swap(float x) { return swap_max(swap_max(x, false), true); }
+__device__ inline float col_sum_swap(float x) { return swap_sum(swap_sum(x, false), true); }
 
 // Sum over the 4 lanes that share a column (xor 16, xor 32), in a fixed
 // order so every lane gets the same bits.

@@ -1,0 +1,692 @@
+// attn_fwd.hip -- the bf16-MFMA attention forward (gfx950, wave64).
+//
+// GpuLoraEngine.Forward.cs:401-465 (tune_attn_causal_gqa_fwd): for each
+// query head and query i, O_i = softmax_j<=i(q_i . k_j / sqrt(D)) V_j and the
+// row log-sum-exp, with q rotated here (q_rot written when saving) and K
+// already rotated by rope_k.
+//
+// Key-split waves.  One workgroup of 4 waves (one per SIMD) per (query head,
+// 64-query tile).  Every wave holds the whole tile's Q^T fragments (VGPRs)
+// and O^T accumulators (AGPRs) and walks its own 32-key chunks of the causal
+// range (chunks w, w + 4, w + 8, ...): a K fragment read from LDS feeds four
+// MFMAs (one per 16-query block) and so does a V fragment, a quarter of the
+// LDS traffic per MFMA of waves that own 16 queries each.
+//   * K and V chunks go from L2 straight into the wave's own two-slot LDS
+//     rings (buffer_load ... lds, 16 bytes per lane, XOR-swizzled rows), two
+//     chunks ahead, with no workgroup barrier inside the loop.
+//   * Software pipeline: an iteration issues chunk i + 1's scores while it
+//     takes chunk i's exponentials, and chunk i's PV products while it takes
+//     chunk i + 1's maxima; the row sums are four more MFMAs against ones.
+//   * No rescaling inside the loop: the probabilities are taken against each
+//     column's maximum in the wave's first chunk; a later chunk exceeding it
+//     by more than 2^16 makes the wave run its chunks again with the true
+//     maxima (exact either way; rare).
+//   * The four partial states (max, sum, O) are merged per 16-query block by
+//     the wave that owns the block, in wave order.
+// The compiler's own MFMAs write VGPRs (-mllvm -amdgpu-mfma-vgpr-form,
+// build.py); the accumulators are pinned to AGPRs by inline assembly, and
+// the LDS reads whose completion the compiler would otherwise tie to the
+// DMA are issued from inline assembly with explicit waits.
+#include "attn_common.hpp"
+#include "attn_launch.hpp"
+
+#include <hip/hip_ext.h>
+
+#include <type_traits>
+#include <utility>
+
+namespace glacier {
+namespace {
+
+constexpr int kFwdWaves = 4;
+constexpr int kChunk = 32;  // keys per chunk: one k-step of the PV product
+constexpr float kRescale = 16.0f;  // reference maxima may lag the true ones by 2^16
+
+// Unpadded [rows][D] bf16 LDS tiles keep row r's 16-byte piece p in slot
+// p ^ swz(r), so that the 16 rows read by one MFMA fragment (or by one
+// transposing read) fall in distinct banks: rows of 256 B (D=128) each span
+// all 64 banks, rows of 128 B (D=64) half of them, alternately.
+template <int D>
+__device__ inline int swz(int r) {
+  return D == 128 ? (r & 15) : ((r >> 1) & 7);
+}
+
+template <int D>
+struct FwdLayout {
+  static constexpr int CHUNK = kChunk * D;  // elements of one K or V chunk
+  static constexpr int WAVE = 4 * CHUNK;    // a wave's two (K, V) buffers
+  static constexpr size_t LOOP = sizeof(bf16) * (kFwdWaves * WAVE + kTile * D);
+  static constexpr int OS = D + 4;  // row stride (floats) of the merge area
+  static constexpr size_t BYTES = LOOP;  // the merge reuses each wave's ring region
+};
+
+// One 32-row chunk of K or V into the swizzled LDS tile dst, by DMA
+// (buffer_load ... lds, 16 bytes per lane): instruction n fills 1 KB of dst,
+// lane l the 16 bytes at l * 16, i.e. slot l % (D/8) of row
+// n * (512/D) + l / (D/8).  The per-lane offsets repeat every P
+// instructions (the swizzle period) and are computed once; the row offset
+// of instruction n goes into the scalar offset.  A chunk with fewer than 32
+// rows left in its sequence repeats row nvalid - 1 for the rest: those keys
+// lie past every query of the sequence, so their probabilities are exactly
+// 0 and any finite contents give the same sums.  Completion is tracked by
+// vmcnt only (the compiler does not track these writes): see wait_vmcnt.
+// The per-lane part of the offsets, by instruction index modulo P.
+struct DmaLanes {
+  int rowb, rl, slot;
+  int loff[4];
+};
+
+template <int D>
+struct DmaShape {
+  static constexpr int PPR = D / 8;           // 16-byte pieces per row
+  static constexpr int RPI = 64 / PPR;        // rows per instruction
+  static constexpr int NI = kChunk / RPI;     // instructions per chunk
+  static constexpr int P = D == 128 ? 4 : 2;  // swizzle period in instructions
+};
+
+template <int D>
+__device__ inline DmaLanes dma_lanes(long gstride, int lane) {
+  using L = DmaShape<D>;
+  DmaLanes dl;
+  dl.rowb = __builtin_amdgcn_readfirstlane(static_cast<int>(gstride * (long)sizeof(bf16)));
+  dl.rl = lane / L::PPR;
+  dl.slot = lane % L::PPR;
+#pragma unroll
+  for (int n = 0; n < 4; ++n)
+    dl.loff[n] = dl.rl * dl.rowb + 16 * (dl.slot ^ swz<D>((n % L::P) * L::RPI + dl.rl));
+  return dl;
+}
+
+// (The body is compiled for the device only: instantiated in the host pass,
+// the buffer-resource builtins invalidated the specialization for every
+// later kernel instantiation, which then lost its launch stub.)
+template <int D>
+__device__ inline void dma_chunk(const DmaLanes& dl, const bf16* src, int nvalid, bf16* dst) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  using L = DmaShape<D>;
+  const unsigned long long a = reinterpret_cast<unsigned long long>(src);
+  const unsigned long long au =
+      (static_cast<unsigned long long>(__builtin_amdgcn_readfirstlane(static_cast<int>(a >> 32))) << 32) |
+      static_cast<unsigned>(__builtin_amdgcn_readfirstlane(static_cast<int>(a & 0xffffffffu)));
+  const int nv = __builtin_amdgcn_readfirstlane(nvalid < kChunk ? nvalid : kChunk);
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(au), (short)0, nv * dl.rowb, kBufferWord3);
+  if (nv == kChunk) {
+#pragma unroll
+    for (int n = 0; n < L::NI; ++n)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (GLACIER_LDS void*)(dst + 512 * n), 16, dl.loff[n % L::P],
+                                               n * L::RPI * dl.rowb, 0, 0);
+  } else {
+#pragma unroll
+    for (int n = 0; n < L::NI; ++n) {
+      const int r = n * L::RPI + dl.rl;
+      const int rr = r < nv ? r : nv - 1;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (GLACIER_LDS void*)(dst + 512 * n), 16,
+                                               rr * dl.rowb + 16 * (dl.slot ^ swz<D>(r)), 0, 0, 0);
+    }
+  }
+#endif
+}
+
+// Waits until at most N vector-memory operations of this wave are
+// outstanding; a compiler barrier keeps LDS reads of the chunk below it.
+template <int N>
+__device__ inline void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);  // expcnt, lgkmcnt: no wait
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// 32-bit LDS address of a pointer into dynamic shared memory.
+__device__ inline unsigned lds_addr(const bf16* p) {
+  return static_cast<unsigned>(reinterpret_cast<uintptr_t>((const GLACIER_LDS void*)p));
+}
+
+// ds_read_b64_tr_b16 issued from inline assembly: lane (g, i) addresses row
+// R + i / 4 (R = the lane's row) at column c0 + 4 (i % 4) and receives rows
+// R .. R + 3 of column c0 + i.  The compiler's own form of this read makes
+// it wait for every outstanding LDS DMA of the wave (vmcnt(0)), i.e. for the
+// next chunk's prefetch; these reads are ordered against the DMA by
+// wait_vmcnt instead.  The result registers are valid only after wait_tr.
+template <int OFF>
+__device__ inline bf16x4 read_tr_async(unsigned addr) {
+  bf16x4 r;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
+  return r;
+}
+
+// ds_read_b128 issued from inline assembly (K fragments, OFF: the offset
+// field), valid after wait_kfrags<N>: LDS reads complete in order, so with
+// N reads issued after the fragments, lgkmcnt(N) covers them.
+template <int OFF>
+__device__ inline bf16x8 read_b128_async(unsigned addr) {
+  bf16x8 r;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
+  return r;
+}
+template <int N>
+__device__ inline void wait_kfrags(bf16x8 (&t)[4][2]) {
+  static_assert(N >= 0 && N < 16, "lgkmcnt range");
+  asm volatile("s_waitcnt lgkmcnt(%8)"
+               : "+v"(t[0][0]), "+v"(t[0][1]), "+v"(t[1][0]), "+v"(t[1][1]), "+v"(t[2][0]),
+                 "+v"(t[2][1]), "+v"(t[3][0]), "+v"(t[3][1])
+               : "i"(N));
+}
+template <int N>
+__device__ inline void wait_kfrags(bf16x8 (&t)[2][2]) {
+  static_assert(N >= 0 && N < 16, "lgkmcnt range");
+  asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(t[0][0]), "+v"(t[0][1]), "+v"(t[1][0]), "+v"(t[1][1]) : "i"(N));
+}
+
+// s_waitcnt lgkmcnt(0) that the compiler sees as redefining the results of
+// the preceding read_tr_async calls, so no use of them moves above it.
+__device__ inline void wait_tr(bf16x4 (&t)[8]) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(t[0]), "+v"(t[1]), "+v"(t[2]), "+v"(t[3]), "+v"(t[4]), "+v"(t[5]),
+                 "+v"(t[6]), "+v"(t[7]));
+}
+__device__ inline void wait_tr(bf16x4 (&t)[16]) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(t[0]), "+v"(t[1]), "+v"(t[2]), "+v"(t[3]), "+v"(t[4]), "+v"(t[5]),
+                 "+v"(t[6]), "+v"(t[7]), "+v"(t[8]), "+v"(t[9]), "+v"(t[10]), "+v"(t[11]),
+                 "+v"(t[12]), "+v"(t[13]), "+v"(t[14]), "+v"(t[15]));
+}
+
+// acc += A B (v_mfma_f32_16x16x32_bf16) with the accumulator pinned in
+// AGPRs: the O^T tiles stay in place across the loop instead of being
+// copied between register files.  The compiler does not see an MFMA here,
+// so the asm itself provides the two wait states a VALU-written operand
+// needs (s_nop 1), and fence_acc below the MFMA-to-reader wait states.
+__device__ inline void mma_acc(f32x4& acc, const bf16x8& a, const bf16x8& b) {
+  asm("s_nop 1\n\tv_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+
+// Wait states between the last mma_acc and any other access of the
+// accumulators (24 >= the 18 a 16-pass MFMA result needs); every
+// accumulator is tied through a volatile asm after the wait, so no access
+// moves above it.
+template <int NDB>
+__device__ inline void fence_acc(f32x4 (&o)[NDB][4], f32x4 (&l)[4]) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+#pragma unroll
+  for (int qb = 0; qb < 4; ++qb) {
+    asm volatile("" : "+a"(l[qb]));
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) asm volatile("" : "+a"(o[db][qb]));
+  }
+}
+
+// ds_write_b128 of an accumulator straight from its AGPRs (OFF: the offset
+// field, bytes).  Use after fence_acc; completion is waited for explicitly.
+template <int OFF>
+__device__ inline void write_acc(unsigned addr, const f32x4& v) {
+  asm volatile("ds_write_b128 %0, %1 offset:%2" : : "v"(addr), "a"(v), "i"(OFF) : "memory");
+}
+
+// the NDB 16-byte pieces of block qb of the accumulators at addr + 64 db
+template <int NDB, int... DB>
+__device__ inline void write_acc_block(unsigned addr, const f32x4 (&o)[NDB][4], int qb,
+                                       std::integer_sequence<int, DB...>) {
+  (write_acc<64 * DB>(addr, o[DB][qb]), ...);
+}
+
+template <typename IO, int D, bool VARLEN>
+__global__ __launch_bounds__(kFwdWaves * 64) void attn_fwd_kernel_ks(
+    const IO* __restrict__ q, const bf16* __restrict__ kc, const bf16* __restrict__ v,
+    IO* __restrict__ out, float* __restrict__ lse, IO* __restrict__ q_rot,
+    const TileDesc* __restrict__ tiles, int n_tiles, int total_tokens,
+    float scale_log2, const float* __restrict__ cos_t, const float* __restrict__ sin_t) {
+  using M = Mfma<bf16>;
+  using F = FwdLayout<D>;
+  using Frag = M::Frag;
+  constexpr int NKD = D / M::KSTEP;
+  constexpr int NDB = D / 16;
+  constexpr int H = D / 2;
+  constexpr int NT = kFwdWaves * 64;
+  constexpr int NDMA = 2 * (kChunk * D / 512);  // DMA instructions per chunk (K and V)
+  static_assert(NDMA < 64, "vmcnt range");
+  constexpr unsigned SLOT = F::CHUNK * sizeof(bf16);  // bytes of one ring slot
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  bf16* const lds = reinterpret_cast<bf16*>(smem_raw);  // [wave][K ring, V ring], Q
+
+  // grid (query heads per KV head, KV heads, tiles): no integer division
+  const int n_heads_kv = gridDim.y, n_heads_q = gridDim.x * gridDim.y;
+  const int kvh = blockIdx.y, h = kvh * gridDim.x + blockIdx.x;
+  const TileDesc td = VARLEN ? tiles[blockIdx.z]
+                             : TileDesc{0, total_tokens, n_tiles - 1 - (int)blockIdx.z, 0};
+  const int tid = threadIdx.x, w = wave_id(), lane = tid & 63;
+  GL_STAMP(kKernFwd, 0);
+  GL_STAMP_VALUE(kKernFwd, 31, td.tile);
+  const int g = lane >> 4, c = lane & 15;
+  const int q0 = kTile * td.tile;          // the tile's first query position
+  const int nq = min(kTile, td.len - q0);  // its valid queries
+  const int nch = (q0 + nq + kChunk - 1) / kChunk;  // key chunks of the causal range
+  const int nit = __builtin_amdgcn_readfirstlane(nch > w ? (nch - w + kFwdWaves - 1) / kFwdWaves : 0);
+  // This wave's LDS: a two-slot ring of K chunks, then one of V chunks
+  // (chunk i in slot i & 1).  K of chunk i + 1 is read one iteration ahead of
+  // V of chunk i, so the rings refill at different points of an iteration.
+  bf16* const kring = lds + w * F::WAVE;
+  bf16* const vring = kring + 2 * F::CHUNK;
+
+  const long kvstride = (long)n_heads_kv * D;
+  const bf16* kbase = kc + ((long)td.tok0 * n_heads_kv + kvh) * D;
+  const bf16* vbase = v + ((long)td.tok0 * n_heads_kv + kvh) * D;
+  const DmaLanes dl = dma_lanes<D>(kvstride, lane);
+  // chunk i of this wave: keys 32 (w + 4 i) .., into ring slot i & 1
+  auto dma_k = [&](int i) {
+    const int j = w + kFwdWaves * i;
+    dma_chunk<D>(dl, kbase + (long)kChunk * j * kvstride, td.len - kChunk * j, kring + (i & 1) * F::CHUNK);
+  };
+  auto dma_v = [&](int i) {
+    const int j = w + kFwdWaves * i;
+    dma_chunk<D>(dl, vbase + (long)kChunk * j * kvstride, td.len - kChunk * j, vring + (i & 1) * F::CHUNK);
+  };
+  if (nit > 0) {
+    dma_k(0);
+    dma_v(0);
+  }
+  if (nit > 1) {
+    dma_k(1);
+    dma_v(1);
+  }
+
+  // Q: the tile's rows are loaded by all threads (coalesced, 8 rotation pairs
+  // per thread), rotated in fp32 (rope_fwd) and rounded to bf16, written to
+  // LDS (swizzled), from where every wave reads the operand fragments of all
+  // 64 queries, and later to q_rot as whole rows.
+  bf16* const qst = lds + kFwdWaves * F::WAVE;
+  constexpr int PPR = H / 8;            // 8-pair pieces per row
+  constexpr int QI = kTile * PPR / NT;  // pieces per thread
+  static_assert(QI * NT == kTile * PPR, "Q tile must split evenly");
+  float qy[QI][2][8];
+  const long qrow0 = (long)td.tok0 + q0;
+#pragma unroll
+  for (int n = 0; n < QI; ++n) {
+    const int idx = tid + n * NT;
+    const int r = idx / PPR, j = idx % PPR;
+    const bool valid = r < nq;
+    const long gq = ((qrow0 + (valid ? r : 0)) * n_heads_q + h) * D + 8 * j;
+    float x0[8], x1[8], cs[8], sn[8];
+    load8(q + gq, x0);
+    load8(q + gq + H, x1);
+    const long ti = (long)(q0 + (valid ? r : 0)) * H + 8 * j;
+    load8(cos_t + ti, cs);
+    load8(sin_t + ti, sn);
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      rope_fwd(valid ? x0[e] : 0.0f, valid ? x1[e] : 0.0f, cs[e], sn[e], qy[n][0][e], qy[n][1][e]);
+    const int sw = swz<D>(r);
+    store8(qst + r * D + 8 * (j ^ sw), qy[n][0]);
+    store8(qst + r * D + 8 * ((PPR + j) ^ sw), qy[n][1]);
+  }
+  GL_STAMP(kKernFwd, 1);
+  __syncthreads();
+  Frag qf[4][NKD];
+  {
+    const int sq = swz<D>(c);  // rows 16 qb + c
+#pragma unroll
+    for (int qb = 0; qb < 4; ++qb)
+#pragma unroll
+      for (int kk = 0; kk < NKD; ++kk)
+        qf[qb][kk] = *reinterpret_cast<const bf16x8*>(qst + (16 * qb + c) * D + 8 * ((4 * kk + g) ^ sq));
+  }
+  GL_STAMP(kKernFwd, 2);
+
+  // Per-lane LDS addresses (bytes, slot 0) of the chunk reads; the slot and
+  // the 16-row block go into the instructions' offset fields.  K fragments:
+  // row 16 kb + c, piece 4 kk + g.  V transposing reads
+  // (ds_read_b64_tr_b16): lane (g, i) addresses row 16 s + 4 g + i / 4,
+  // columns 16 db + 4 (i % 4) .. + 3, i.e. piece 2 db + (i % 4) / 2 at
+  // element 4 (i % 2) of it.  Row offsets of 16 leave the swizzle unchanged.
+  unsigned kaddr[NKD], vaddr[NDB];
+  {
+    const int sk = swz<D>(c);
+    const int vrow = 4 * g + (c >> 2);
+    const int sv = swz<D>(vrow);
+    const int vpiece = (c & 3) >> 1;
+#pragma unroll
+    for (int kk = 0; kk < NKD; ++kk) kaddr[kk] = lds_addr(kring + c * D + 8 * ((4 * kk + g) ^ sk));
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+      vaddr[db] = lds_addr(vring + vrow * D + 4 * (c & 1) + 8 * ((2 * db + vpiece) ^ sv));
+  }
+
+  // O^T accumulators and per-query row sums (MFMA accumulators pinned in
+  // AGPRs), the reference maxima the probabilities are taken against.
+  f32x4 o[NDB][4], lsum[4];
+  float m_ref[4], m_seen[4], mt[4];
+#pragma unroll
+  for (int qb = 0; qb < 4; ++qb) {
+    // a wave without chunks merges as (kNegBig, 0, 0)
+    m_ref[qb] = kNegBig;
+    m_seen[qb] = kNegBig;
+  }
+  bool grew = false;
+  bf16x8 ones;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ones[e] = (bf16)1.0f;
+
+  // One iteration: chunk i's probabilities, row sums and PV (its scores in
+  // sc, its V in slot i & 1), chunk i + 1's scores and maxima (MORE: chunk
+  // i + 1 exists; its K is in the other slot), which replace sc.  MASK: chunk
+  // i + 1 may reach the diagonal (only a wave's last chunk can).  FETCH:
+  // chunk i + 2 exists; its K goes into K(i)'s slot at the start, its V into
+  // V(i)'s at the end.  On entry K(i + 1) and V(i) are in LDS or in flight.
+  f32x4 sc[2][4];
+  auto iteration = [&](int i, auto more, auto mask, auto fetch) {
+    constexpr bool MORE = decltype(more)::value;
+    constexpr bool MASK = decltype(mask)::value;
+    constexpr bool FETCH = decltype(fetch)::value;
+    if constexpr (MORE)
+      wait_vmcnt<NDMA / 2>();  // all but V(i + 1)'s DMA
+    else
+      wait_vmcnt<0>();
+    if (i < 6) GL_STAMP(kKernFwd, 4 + 2 * i);
+    if constexpr (FETCH) dma_k(i + 2);  // every read of K(i) completed last iteration
+    // K fragments of chunk i + 1, then the V^T fragments of chunk i (two
+    // transposing reads per 16-row block), all issued before any is used.
+    const unsigned vslot = (i & 1) * SLOT, kslot = SLOT - vslot;
+    bf16x8 kf[NKD][2];
+    if constexpr (MORE) {
+#pragma unroll
+      for (int kk = 0; kk < NKD; ++kk) {
+        kf[kk][0] = read_b128_async<0>(kaddr[kk] + kslot);
+        kf[kk][1] = read_b128_async<32 * D>(kaddr[kk] + kslot);
+      }
+    }
+    bf16x4 vt[2 * NDB];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      vt[2 * db] = read_tr_async<0>(vaddr[db] + vslot);
+      vt[2 * db + 1] = read_tr_async<32 * D>(vaddr[db] + vslot);
+    }
+    f32x4 sn[2][4];
+    if constexpr (MORE) {
+      wait_kfrags<(2 * NDB < 15 ? 2 * NDB : 15)>(kf);
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int qb = 0; qb < 4; ++qb) sn[kb][qb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int kk = 0; kk < NKD; ++kk)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int qb = 0; qb < 4; ++qb) sn[kb][qb] = M::mma(kf[kk][kb], qf[qb][kk], sn[kb][qb]);
+    }
+    bf16x8 pb[4];
+#pragma unroll
+    for (int qb = 0; qb < 4; ++qb)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          pb[qb][4 * kb + r] =
+              (bf16)__builtin_amdgcn_exp2f(__builtin_fmaf(sc[kb][qb][r], scale_log2, -m_ref[qb]));
+    wait_tr(vt);
+#pragma unroll
+    for (int qb = 0; qb < 4; ++qb) mma_acc(lsum[qb], ones, pb[qb]);
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      bf16x8 a;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        a[r] = vt[2 * db][r];
+        a[4 + r] = vt[2 * db + 1][r];
+      }
+#pragma unroll
+      for (int qb = 0; qb < 4; ++qb) mma_acc(o[db][qb], a, pb[qb]);
+    }
+    if constexpr (MORE) {
+      // maxima of chunk i + 1 in log2 units, keys after a query set to -inf
+      // first when the chunk may reach the diagonal
+      const int koff = kChunk * (w + kFwdWaves * (i + 1)) - q0;  // its key 0, from query 0
+#pragma unroll
+      for (int qb = 0; qb < 4; ++qb) {
+        float mloc = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            if (MASK)
+              sn[kb][qb][r] = (koff + 16 * kb + 4 * g + r <= 16 * qb + c) ? sn[kb][qb][r] : -INFINITY;
+            mloc = fmaxf(mloc, sn[kb][qb][r]);
+          }
+        mt[qb] = col_max_swap(mloc) * scale_log2;
+        grew = grew || (mt[qb] > m_ref[qb] + kRescale);
+        m_seen[qb] = fmaxf(m_seen[qb], mt[qb]);
+      }
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int qb = 0; qb < 4; ++qb) sc[kb][qb] = sn[kb][qb];
+    }
+    if constexpr (FETCH) {
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): every read of V(i) is complete
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      dma_v(i + 2);
+    }
+  };
+
+  // Pass 0 takes each column's reference maximum from the wave's first
+  // chunk; no rescaling ever happens inside the loop.  If a later chunk's
+  // maximum exceeds it by more than 2^16 (rare: probabilities stay finite up
+  // to 2^128, and the results are exact either way), the wave runs its
+  // chunks again with the maxima it saw as references (pass 1 cannot grow).
+#pragma clang loop unroll(disable)
+  for (int pass = 0; pass < 2; ++pass) {
+    if (pass > 0) {
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the last chunk's reads are complete
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      if (nit > 0) {
+        dma_k(0);
+        dma_v(0);
+      }
+      if (nit > 1) {
+        dma_k(1);
+        dma_v(1);
+      }
+    }
+#pragma unroll
+    for (int qb = 0; qb < 4; ++qb) {
+      lsum[qb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) o[db][qb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    grew = false;
+    if (nit > 0) {
+      // chunk 0: K(1)'s DMA (issued after K(0), V(0)) may still be in flight
+      if (nit > 1)
+        wait_vmcnt<NDMA / 2 * 3>();
+      else
+        wait_vmcnt<NDMA / 2>();
+      bf16x8 kf[NKD][2];
+#pragma unroll
+      for (int kk = 0; kk < NKD; ++kk) {
+        kf[kk][0] = read_b128_async<0>(kaddr[kk]);
+        kf[kk][1] = read_b128_async<32 * D>(kaddr[kk]);
+      }
+      wait_kfrags<0>(kf);
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int qb = 0; qb < 4; ++qb) sc[kb][qb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int kk = 0; kk < NKD; ++kk)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int qb = 0; qb < 4; ++qb) sc[kb][qb] = M::mma(kf[kk][kb], qf[qb][kk], sc[kb][qb]);
+      const int koff = kChunk * w - q0;
+#pragma unroll
+      for (int qb = 0; qb < 4; ++qb) {
+        float mloc = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            sc[kb][qb][r] = (koff + 16 * kb + 4 * g + r <= 16 * qb + c) ? sc[kb][qb][r] : -INFINITY;
+            mloc = fmaxf(mloc, sc[kb][qb][r]);
+          }
+        // a column the chunk masks entirely keeps kNegBig: that chunk is the
+        // wave's last, and its probabilities are exactly 0
+        const float m0 = fmaxf(col_max_swap(mloc) * scale_log2, kNegBig);
+        if (pass == 0) m_ref[qb] = m0;
+        m_seen[qb] = m0;
+      }
+    }
+    if (pass == 0 && q_rot != nullptr) {
+      // q_rot as whole rows, issued after chunk 0's wait so that it does not
+      // wait for these stores
+#pragma unroll
+      for (int n = 0; n < QI; ++n) {
+        const int idx = tid + n * NT;
+        const int r = idx / PPR, j = idx % PPR;
+        if (r < nq) {
+          const long gq = ((qrow0 + r) * n_heads_q + h) * D + 8 * j;
+          store8(q_rot + gq, qy[n][0]);
+          store8(q_rot + gq + H, qy[n][1]);
+        }
+      }
+    }
+    GL_STAMP(kKernFwd, 3);
+    int i = 0;
+    for (; i + 2 < nit; ++i) {
+      iteration(i, std::true_type{}, std::false_type{}, std::true_type{});
+      if (i < 6) GL_STAMP(kKernFwd, 5 + 2 * i);
+    }
+    if (i + 1 < nit) {
+      iteration(i, std::true_type{}, std::true_type{}, std::false_type{});
+      ++i;
+    }
+    GL_STAMP(kKernFwd, 16);
+    if (i < nit) iteration(i, std::false_type{}, std::false_type{}, std::false_type{});
+    fence_acc(o, lsum);
+    GL_STAMP(kKernFwd, 17);
+    if (__builtin_amdgcn_ballot_w64(grew) == 0) break;
+#pragma unroll
+    for (int qb = 0; qb < 4; ++qb) m_ref[qb] = m_seen[qb];
+  }
+  GL_STAMP(kKernFwd, 20);
+
+  // Merge.  Wave w owns query block w.  Each wave writes its raw partial
+  // O^T of the three other blocks and its (maximum, sum) per query into its
+  // own ring region (free once its loop is done, so no wave waits for the
+  // others first), straight from the AGPRs.  After one barrier the owner
+  // weighs the four partials by exp2(m_u - M) / L (M = max of the maxima,
+  // L = sum of exp2(m_u - M) l_u, both in wave order), adds them in wave
+  // order (its own from registers) and stores its 16 rows.
+  static_assert(3 * 16 * F::OS + 2 * kTile <= F::WAVE / 2, "merge data exceeds a wave's region");
+  float* const mine = reinterpret_cast<float*>(kring);  // [3 blocks][16][OS], maxima, sums
+  constexpr int MOFF = 3 * 16 * F::OS;                   // maxima, then sums (floats)
+  if (g == 0) {
+#pragma unroll
+    for (int qb = 0; qb < 4; ++qb) {
+      mine[MOFF + 16 * qb + c] = m_ref[qb];
+      mine[MOFF + kTile + 16 * qb + c] = lsum[qb][0];
+    }
+  }
+#pragma unroll
+  for (int qb = 0; qb < 4; ++qb) {
+    if (qb == w) continue;
+    const unsigned a = lds_addr(reinterpret_cast<const bf16*>(mine + ((qb - (qb > w)) * 16 + c) * F::OS + 4 * g));
+    write_acc_block(a, o, qb, std::make_integer_sequence<int, NDB>{});
+  }
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the merge writes are complete
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  GL_STAMP(kKernFwd, 24);
+  __syncthreads();
+  GL_STAMP(kKernFwd, 25);
+  {
+    const int qi = 16 * w + c;
+    const float* region[kFwdWaves];
+#pragma unroll
+    for (int u = 0; u < kFwdWaves; ++u) region[u] = reinterpret_cast<const float*>(lds + u * F::WAVE);
+    float mw[kFwdWaves], lw[kFwdWaves];
+    float m_all = kNegBig;
+#pragma unroll
+    for (int u = 0; u < kFwdWaves; ++u) {
+      mw[u] = region[u][MOFF + qi];
+      lw[u] = region[u][MOFF + kTile + qi];
+      m_all = fmaxf(m_all, mw[u]);
+    }
+    float l_all = 0.0f;
+#pragma unroll
+    for (int u = 0; u < kFwdWaves; ++u) {
+      mw[u] = __builtin_amdgcn_exp2f(mw[u] - m_all);
+      l_all += lw[u] * mw[u];
+    }
+    const float inv = 1.0f / l_all;
+    if (g == 0 && lse != nullptr && qi < nq)
+      lse[(long)h * total_tokens + td.tok0 + q0 + qi] = (m_all + log2f(l_all)) * kLn2;
+    f32x4 acc[NDB];
+    // QB: the owner's block as a constant (one branch on the wave index)
+    auto sum_block = [&](auto qbc) {
+      constexpr int QB = decltype(qbc)::value;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) acc[db] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int u = 0; u < kFwdWaves; ++u) {
+        const float f = mw[u] * inv;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+          const f32x4 x =
+              u == QB ? o[db][QB]
+                      : *reinterpret_cast<const f32x4*>(region[u] + ((QB - (QB > u)) * 16 + c) * F::OS +
+                                                        16 * db + 4 * g);
+          acc[db] += x * f;
+        }
+      }
+    };
+    if (w == 0)
+      sum_block(std::integral_constant<int, 0>{});
+    else if (w == 1)
+      sum_block(std::integral_constant<int, 1>{});
+    else if (w == 2)
+      sum_block(std::integral_constant<int, 2>{});
+    else
+      sum_block(std::integral_constant<int, 3>{});
+    GL_STAMP(kKernFwd, 28);
+    // rows of the block: lane (g, c) holds d = 16 db + 4 g .. + 3 of query qi
+    if (qi < nq) {
+      IO* const orow = out + ((qrow0 + qi) * n_heads_q + h) * D + 4 * g;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) store4(orow + 16 * db, acc[db]);
+    }
+  }
+  GL_STAMP(kKernFwd, 21);
+}
+
+}  // namespace
+
+template <typename IO, int D>
+hipError_t launch_fwd_bf16(const FwdLaunch& a, hipStream_t st, KernelTimer* tm) {
+  auto fn = a.single_seq ? attn_fwd_kernel_ks<IO, D, false> : attn_fwd_kernel_ks<IO, D, true>;
+  constexpr size_t lds = FwdLayout<D>::BYTES;
+  GL_CHECK(allow_lds(fn, lds));
+  LaunchTiming t(tm, kKernFwd);
+  hipExtLaunchKernelGGL(fn, dim3(a.n_heads_q / a.n_heads_kv, a.n_heads_kv, a.n_tiles),
+                        dim3(kFwdWaves * 64), lds, st, t.start(), t.stop(), 0,
+                        static_cast<const IO*>(a.q), static_cast<const bf16*>(a.kc),
+                        static_cast<const bf16*>(a.vc != nullptr ? a.vc : a.v),
+                        static_cast<IO*>(a.out), a.lse, static_cast<IO*>(a.q_rot), a.tiles_fwd,
+                        a.n_tiles, a.total_tokens, a.scale_log2, a.cos_t, a.sin_t);
+  GL_CHECK(hipGetLastError());
+  t.launched();
+  return hipSuccess;
+}
+
+template hipError_t launch_fwd_bf16<bf16, 64>(const FwdLaunch&, hipStream_t, KernelTimer*);
+template hipError_t launch_fwd_bf16<bf16, 128>(const FwdLaunch&, hipStream_t, KernelTimer*);
+template hipError_t launch_fwd_bf16<float, 64>(const FwdLaunch&, hipStream_t, KernelTimer*);
+template hipError_t launch_fwd_bf16<float, 128>(const FwdLaunch&, hipStream_t, KernelTimer*);
+
+}  // namespace glacier
+
+#ifdef GLACIER_PHASE_STAMPS
+// Profiling builds only: copies this file's phase stamps (the forward's) to
+// host memory.
+extern "C" int glacier_attn_debug_stamps_fwd(void* host, size_t bytes) {
+  return static_cast<int>(hipMemcpyFromSymbol(host, HIP_SYMBOL(glacier::glacier_stamps), bytes));
+}
+#endif

@@ -3,14 +3,11 @@
 // Forward  (GpuLoraEngine.Forward.cs:401-465 rope_batch + tune_attn_causal_gqa_fwd):
 //   rope_k    K -> RoPE -> k_rot (caller dtype) and/or a compute-dtype copy
 //             (plus a bf16 copy of V when fp32 tensors feed bf16 matrix cores).
-//   attn_fwd  one workgroup = 64 queries of one head, two groups of 4 waves
-//             (16 queries per wave) splitting the key tiles.  Q is rotated in
-//             registers on load (q_rot written if asked); rotated-K and V
-//             tiles of 64 keys are staged row-major in LDS (double-buffered,
-//             later tiles' global loads in flight meanwhile) and shared by the
-//             group's 4 waves; online softmax in fp32 (exp2 domain, lazy
-//             rescaling); O and the row log-sum-exp are written at the end.
-//             No [S,S] matrix exists.
+//   attn_fwd  fp32 mode: one workgroup = 64 queries of one head (this file);
+//             bf16 mode: attn_fwd.hip (key-split waves, LDS DMA).  Q is
+//             rotated on load (q_rot written if asked); online softmax in
+//             fp32 (exp2 domain); O and the row log-sum-exp are written at
+//             the end.  No [S,S] matrix exists.
 // Backward (GpuLoraEngine.Backward.cs:354-412 dq_ds + dk_dv, :452 inverse rope):
 //   attn_bwd  one launch with two kinds of workgroup.  dK/dV tiles: 64 keys of
 //             one query head; dV_h = P^T dO and dK_h = scale dS^T Q accumulated
@@ -32,29 +29,6 @@
 #include <type_traits>
 
 namespace glacier {
-
-#ifdef GLACIER_PHASE_STAMPS
-__device__ unsigned long long glacier_stamps[kStampKernels][kStampBlocks][kStampSlots];
-#endif
-
-// ---------------------------------------------------------------------------
-// RoPE, written without contraction so that q_rot/k_rot are the exact fp32
-// results of RoPEKernel.cs:84-85 (v0*c - v1*s, v0*s + v1*c) given the same
-// cos/sin table.
-// ---------------------------------------------------------------------------
-__device__ inline void rope_fwd(float x0, float x1, float c, float s, float& y0,
-                                float& y1) {
-#pragma clang fp contract(off)
-  y0 = x0 * c - x1 * s;
-  y1 = x0 * s + x1 * c;
-}
-// inverse rotation (sin negated, RoPEKernel.cs:60)
-__device__ inline void rope_inv(float x0, float x1, float c, float s, float& y0,
-                                float& y1) {
-#pragma clang fp contract(off)
-  y0 = x0 * c + x1 * s;
-  y1 = x1 * c - x0 * s;
-}
 
 // ---------------------------------------------------------------------------
 // rope_k: one thread per (token, kv head, 8 rotation pairs).  Writes the
@@ -339,280 +313,6 @@ __global__ __launch_bounds__(kThreads * fwd_groups<T>()) void attn_fwd_kernel(
     if (lse != nullptr && g == 0)
       lse[(long)h * total_tokens + td.tok0 + qrow] = (m_run + log2f(l_tot)) * kLn2;
   }
-}
-
-// ---------------------------------------------------------------------------
-// attn_fwd, bf16 matrix cores: grid (Hq/Hkv, Hkv, ntiles), 512 threads = 2
-// key groups x 4 waves x 16 queries.  Group grp takes the key tiles grp,
-// grp + 2, ... of the query tile and keeps two of them resident in LDS, so
-// the scores of its next tile are multiplied on the matrix cores while the
-// softmax of the current one runs on the vector ALUs (the next-next tile's
-// global loads are in registers meanwhile).  Group 0 rotates Q and hands the
-// fragments to group 1 through LDS; the two partial (max, sum, O) are merged
-// in group order at the end.
-// ---------------------------------------------------------------------------
-constexpr int kFwdGroups = 2;
-constexpr int kFwdThreads = 512;
-
-template <int D>
-constexpr size_t fwd_bf16_lds() {
-  // two K + V tiles per group, then group 0's Q fragments (64 queries x D)
-  return sizeof(bf16) * (4 * kFwdGroups * Lds<bf16, D>::TILE + kTile * D);
-}
-
-template <typename IO, int D, bool VARLEN>
-__global__ __launch_bounds__(kFwdThreads) void attn_fwd_bf16_kernel(
-    const IO* __restrict__ q, const bf16* __restrict__ kc, const bf16* __restrict__ v,
-    IO* __restrict__ out, float* __restrict__ lse, IO* __restrict__ q_rot,
-    const TileDesc* __restrict__ tiles, int n_tiles, int total_tokens,
-    float scale_log2, const float* __restrict__ cos_t, const float* __restrict__ sin_t) {
-  using M = Mfma<bf16>;
-  using L = Lds<bf16, D>;
-  using Frag = M::Frag;
-  constexpr int G = kFwdGroups;
-  constexpr int GT = kFwdThreads / G;  // threads per group (4 waves)
-  constexpr int NKD = D / M::KSTEP;
-  constexpr int H = D / 2;
-  extern __shared__ __align__(16) unsigned char smem_raw[];
-  bf16* const lds = reinterpret_cast<bf16*>(smem_raw);  // [G][2][K tile, V tile], Q frags
-
-  // grid (query heads per KV head, KV heads, tiles): no integer division
-  const int n_heads_kv = gridDim.y, n_heads_q = gridDim.x * gridDim.y;
-  const int kvh = blockIdx.y, h = kvh * gridDim.x + blockIdx.x;
-  const TileDesc td = VARLEN ? tiles[blockIdx.z]
-                             : TileDesc{0, total_tokens, n_tiles - 1 - (int)blockIdx.z, 0};
-  const int tid = threadIdx.x, w = wave_id(), lane = tid & 63;
-  GL_STAMP(kKernFwd, 0);
-  GL_STAMP_VALUE(kKernFwd, 31, td.tile);
-  const int grp = w >> 2, wq = w & 3, gtid = tid & (GT - 1);
-  const int g = lane >> 4, c = lane & 15;
-  const int qrow = kTile * td.tile + 16 * wq + c;
-  const bool qvalid = qrow < td.len;
-  bf16* const glds = lds + grp * 4 * L::TILE;  // buffer b: glds + b * 2 * TILE
-
-  const long kvstride = (long)n_heads_kv * D;
-  const bf16* kbase = kc + ((long)td.tok0 * n_heads_kv + kvh) * D;
-  const bf16* vbase = v + ((long)td.tok0 * n_heads_kv + kvh) * D;
-  // Two register sets for K/V tiles between their global loads and LDS
-  // stores, so each tile's loads are issued two iterations before its LDS
-  // store (a round trip under load outlasts one iteration's arithmetic).
-  using Regs = TileRegs<bf16, D, GT>;
-  Regs kA, vA, kB, vB;
-  auto load_into = [&](Regs& kr, Regs& vr, int kt) {
-    const long roff = (long)kTile * kt * kvstride;
-    kr.load(kbase + roff, kvstride, td.len - kTile * kt, gtid);
-    vr.load(vbase + roff, kvstride, td.len - kTile * kt, gtid);
-  };
-  auto store_from = [&](const Regs& kr, const Regs& vr, int buf) {
-    kr.store(glds + buf * 2 * L::TILE, gtid);
-    vr.store(glds + buf * 2 * L::TILE + L::TILE, gtid);
-  };
-  if (grp <= td.tile) load_into(kA, vA, grp);
-  if (grp + G <= td.tile) load_into(kB, vB, grp + G);
-
-  // Q: the tile's rows are loaded by all threads (coalesced, 8 rotation pairs
-  // per thread), rotated in fp32 (rope_fwd) and rounded to bf16, written to
-  // q_rot as whole rows and to LDS, from where every wave reads its operand
-  // fragments.  The LDS copy is unpadded ([64][D]) with its 16-byte chunks
-  // XOR-swizzled by row (chunk ch of row r at ch ^ (r mod CPR)), so that the
-  // 16 rows of a fragment read fall in distinct banks.
-  constexpr int QCPR = D / 8;  // 16-byte bf16 chunks per row
-  bf16* const qst = lds + 4 * G * L::TILE;
-  {
-    constexpr int PPR = H / 8;  // 8-pair chunks per row
-    const long qrow0 = (long)td.tok0 + kTile * td.tile;
-    const int nv = td.len - kTile * td.tile;
-    for (int idx = tid; idx < kTile * PPR; idx += kFwdThreads) {
-      const int r = idx / PPR, j = idx % PPR;
-      const bool valid = r < nv;
-      const long gq = ((qrow0 + (valid ? r : 0)) * n_heads_q + h) * D + 8 * j;
-      float x0[8], x1[8], cs[8], sn[8], y0[8], y1[8];
-      load8(q + gq, x0);
-      load8(q + gq + H, x1);
-      const long ti = (long)(kTile * td.tile + (valid ? r : 0)) * H + 8 * j;
-      load8(cos_t + ti, cs);
-      load8(sin_t + ti, sn);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        rope_fwd(valid ? x0[e] : 0.0f, valid ? x1[e] : 0.0f, cs[e], sn[e], y0[e], y1[e]);
-      }
-      if (q_rot != nullptr && valid) {
-        store8(q_rot + gq, y0);
-        store8(q_rot + gq + H, y1);
-      }
-      const int sw = r & (QCPR - 1);
-      store8(qst + r * D + 8 * (j ^ sw), y0);
-      store8(qst + r * D + 8 * ((PPR + j) ^ sw), y1);
-    }
-  }
-  GL_STAMP(kKernFwd, 1);
-  Frag qf[NKD];
-
-  // The group's first two tiles into its two buffers; the third tile's loads
-  // go out once everything before them has completed, and stay in flight
-  // through the first iteration.
-  if (grp <= td.tile) store_from(kA, vA, 0);
-  if (grp + G <= td.tile) store_from(kB, vB, 1);
-  GL_STAMP(kKernFwd, 22);
-  wait_vmem_all();
-  if (grp + 2 * G <= td.tile) load_into(kA, vA, grp + 2 * G);
-  GL_STAMP(kKernFwd, 23);
-  __syncthreads();
-  GL_STAMP(kKernFwd, 2);
-  {
-    const int row = 16 * wq + c;
-#pragma unroll
-    for (int kk = 0; kk < NKD; ++kk) {
-      const int ch = (kk * M::KSTEP + M::KPL * g) / 8;  // logical chunk of the fragment
-      qf[kk] = *reinterpret_cast<const bf16x8*>(qst + row * D + 8 * (ch ^ (row & (QCPR - 1))));
-    }
-  }
-
-  f32x4 o[D / 16];
-#pragma unroll
-  for (int db = 0; db < D / 16; ++db) o[db] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  float m_run = kNegBig, l_lane = 0.0f;
-
-  // Raw scores S^T = K Q^T of one resident key tile (all four key blocks).
-  auto scores = [&](const bf16* ks, float (&sc)[4][4]) {
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-      for (int kk = 0; kk < NKD; ++kk)
-        acc = M::mma(frag_rm<bf16, D>(ks, 16 * b + c, kk, g), qf[kk], acc);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) sc[b][r] = acc[r];
-    }
-  };
-
-  float sc[4][4];
-  if (grp <= td.tile) scores(glds, sc);
-  GL_STAMP(kKernFwd, 3);
-
-  // Softmax of the current tile's scores (masked on the diagonal tile),
-  // interleaved with the next tile's scores, then O^T += V^T P^T.
-  auto step = [&](const bf16* vcur, const bf16* knext, float (&scn)[4][4], auto diag) {
-    constexpr bool DIAG = decltype(diag)::value;
-    float mloc = -INFINITY;
-#pragma unroll
-    for (int b = 0; b < 4; ++b)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        if (DIAG) sc[b][r] = (16 * b + 4 * g + r <= 16 * wq + c) ? sc[b][r] : -INFINITY;
-        mloc = fmaxf(mloc, sc[b][r]);
-      }
-    const float m_tile = col_max(mloc) * scale_log2;
-    if (__builtin_amdgcn_ballot_w64(m_tile > m_run + kRescaleTau) != 0) {
-      const float m_new = fmaxf(m_run, m_tile);
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-      l_lane *= alpha;
-#pragma unroll
-      for (int db = 0; db < D / 16; ++db) o[db] *= alpha;
-      m_run = m_new;
-    }
-    float p[4][4];
-    float psum = 0.0f;
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-      for (int kk = 0; kk < NKD; ++kk)
-        acc = M::mma(frag_rm<bf16, D>(knext, 16 * b + c, kk, g), qf[kk], acc);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        scn[b][r] = acc[r];
-        p[b][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[b][r], scale_log2, -m_run));
-        psum += p[b][r];
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < 4 * NKD; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // four VALU
-    }
-    l_lane += psum;
-    acc_rows<bf16, D>(o, vcur, p, DIAG ? wq + 1 : 4, lane);
-  };
-
-  // Iteration it: buffer it&1 holds tile kt (its V multiplies now), the other
-  // buffer tile kt + G (its K gives the next scores).  (kl, vl) receive tile
-  // kt + 3G; (ks, vs) hold tile kt + 2G, stored into buffer it&1 at the end.
-  const int nit = (td.tile + G) / G;  // iterations of group 0 (the most)
-  auto iter = [&](int it, Regs& kl, Regs& vl, const Regs& ks, const Regs& vs) {
-    const int kt = grp + G * it;
-    const int cur = it & 1;
-    if (kt + 3 * G <= td.tile) load_into(kl, vl, kt + 3 * G);
-    float scn[4][4];
-    const bf16* vcur = glds + cur * 2 * L::TILE + L::TILE;
-    const bf16* knext = glds + (cur ^ 1) * 2 * L::TILE;
-    if (kt < td.tile)
-      step(vcur, knext, scn, std::false_type{});
-    else if (kt == td.tile)
-      step(vcur, knext, scn, std::true_type{});
-    if (it < 8) GL_STAMP(kKernFwd, 4 + 2 * it);
-    if (it + 1 < nit) {
-      __syncthreads();
-      if (kt + 2 * G <= td.tile) store_from(ks, vs, cur);
-      __syncthreads();
-    }
-    if (it < 8) GL_STAMP(kKernFwd, 5 + 2 * it);
-#pragma unroll
-    for (int b = 0; b < 4; ++b)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) sc[b][r] = scn[b][r];
-  };
-  for (int it = 0; it < nit; it += 2) {
-    iter(it, kB, vB, kA, vA);
-    if (it + 1 < nit) iter(it + 1, kA, vA, kB, vB);
-  }
-
-  GL_STAMP(kKernFwd, 20);
-  // Merge group 1 into group 0 (lane for lane: waves wq and wq + 4 own the
-  // same queries); 16-byte LDS accesses: (max, sum), then O.  Then O goes
-  // through LDS (row-major, output dtype, in group 1's region) so that all
-  // eight waves store whole 256-byte rows.
-  constexpr int NS = 1 + D / 16;
-  __syncthreads();
-  f32x4* const cmb = reinterpret_cast<f32x4*>(smem_raw) + wq * NS * 64 + lane;
-  if (grp != 0) {
-    cmb[0] = f32x4{m_run, l_lane, 0.0f, 0.0f};
-#pragma unroll
-    for (int db = 0; db < D / 16; ++db) cmb[(1 + db) * 64] = o[db];
-  }
-  __syncthreads();
-  IO* const ot = reinterpret_cast<IO*>(lds + 4 * L::TILE);
-  constexpr int OS = D + 16 / sizeof(IO);  // padded row stride
-  if (grp == 0) {
-    const f32x4 ml = cmb[0];
-    const float m_new = fmaxf(m_run, ml[0]);
-    const float a0 = __builtin_amdgcn_exp2f(m_run - m_new);
-    const float a1 = __builtin_amdgcn_exp2f(ml[0] - m_new);
-    l_lane = l_lane * a0 + ml[1] * a1;
-#pragma unroll
-    for (int db = 0; db < D / 16; ++db) o[db] = o[db] * a0 + cmb[(1 + db) * 64] * a1;
-    m_run = m_new;
-    const float l_tot = col_sum(l_lane);
-    const float inv = 1.0f / l_tot;
-    if (lse != nullptr && qvalid && g == 0)
-      lse[(long)h * total_tokens + td.tok0 + qrow] = (m_run + log2f(l_tot)) * kLn2;
-#pragma unroll
-    for (int db = 0; db < D / 16; ++db)
-      store4(ot + (16 * wq + c) * OS + 16 * db + 4 * g, o[db] * inv);
-  }
-  __syncthreads();
-  constexpr int CPR = D * sizeof(IO) / 16;  // 16-byte chunks per row
-  const long orow0 = (long)td.tok0 + kTile * td.tile;
-#pragma unroll
-  for (int i = 0; i < kTile * CPR / kFwdThreads; ++i) {
-    const int idx = tid + i * kFwdThreads;
-    const int r = idx / CPR, ch = idx % CPR;
-    if (kTile * td.tile + r < td.len)
-      *reinterpret_cast<uint4*>(out + ((orow0 + r) * n_heads_q + h) * D + ch * (16 / sizeof(IO))) =
-          *reinterpret_cast<const uint4*>(ot + r * OS + ch * (16 / sizeof(IO)));
-  }
-  GL_STAMP(kKernFwd, 21);
 }
 
 // ---------------------------------------------------------------------------
@@ -1154,20 +854,6 @@ constexpr size_t bwd_lds() {
   return dq > dkdv ? dq : dkdv;
 }
 
-template <typename F>
-hipError_t allow_lds(F* fn, size_t bytes) {
-  if (bytes <= 65536) return hipSuccess;
-  return hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
-                             hipFuncAttributeMaxDynamicSharedMemorySize,
-                             static_cast<int>(bytes));
-}
-
-#define GL_CHECK(expr)                       \
-  do {                                       \
-    hipError_t e_ = (expr);                  \
-    if (e_ != hipSuccess) return e_;         \
-  } while (0)
-
 template <typename IO, typename T, int D>
 hipError_t forward_impl(const FwdLaunch& a, hipStream_t st, KernelTimer* tm) {
   const dim3 blk(kThreads);
@@ -1186,18 +872,7 @@ hipError_t forward_impl(const FwdLaunch& a, hipStream_t st, KernelTimer* tm) {
     t.launched();
   }
   if constexpr (sizeof(T) == 2) {
-    auto fn = a.single_seq ? attn_fwd_bf16_kernel<IO, D, false> : attn_fwd_bf16_kernel<IO, D, true>;
-    constexpr size_t lds = fwd_bf16_lds<D>();
-    GL_CHECK(allow_lds(fn, lds));
-    LaunchTiming t(tm, kKernFwd);
-    hipExtLaunchKernelGGL(fn, dim3(a.n_heads_q / a.n_heads_kv, a.n_heads_kv, a.n_tiles),
-                          dim3(kFwdThreads), lds, st, t.start(), t.stop(), 0,
-                          static_cast<const IO*>(a.q), static_cast<const bf16*>(a.kc),
-                          static_cast<const bf16*>(a.vc != nullptr ? a.vc : a.v),
-                          static_cast<IO*>(a.out), a.lse, static_cast<IO*>(a.q_rot), a.tiles_fwd,
-                          a.n_tiles, a.total_tokens, a.scale_log2, a.cos_t, a.sin_t);
-    GL_CHECK(hipGetLastError());
-    t.launched();
+    GL_CHECK((launch_fwd_bf16<IO, D>(a, st, tm)));
   } else {
     auto fn = attn_fwd_kernel<IO, T, D>;
     constexpr size_t lds = fwd_lds<T, D>();

@@ -154,4 +154,25 @@ hipError_t launch_forward(const FwdLaunch& a, hipStream_t st, KernelTimer* tm);
 hipError_t launch_backward(const BwdLaunch& a, hipStream_t st, KernelTimer* tm);
 size_t compute_elem_size(int precision, bool io_bf16);
 
+// The bf16-MFMA attention forward (attn_fwd.hip), after rope_k has written
+// the rotated K (and bf16 V) it reads.  IO: the dtype of q, out and q_rot
+// (__bf16 or float); D: 64 or 128.
+template <typename IO, int D>
+hipError_t launch_fwd_bf16(const FwdLaunch& a, hipStream_t st, KernelTimer* tm);
+
+// Kernels whose dynamic LDS exceeds 64 KB must say so before their launch.
+template <typename F>
+hipError_t allow_lds(F* fn, size_t bytes) {
+  if (bytes <= 65536) return hipSuccess;
+  return hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                             static_cast<int>(bytes));
+}
+
+#define GL_CHECK(expr)               \
+  do {                               \
+    hipError_t e_ = (expr);          \
+    if (e_ != hipSuccess) return e_; \
+  } while (0)
+
 }  // namespace glacier
