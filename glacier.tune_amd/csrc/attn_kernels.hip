@@ -33,7 +33,8 @@ namespace glacier {
 // ---------------------------------------------------------------------------
 // rope_k: one thread per (token, kv head, 8 rotation pairs).  Writes the
 // rotated K to k_rot (caller dtype) and/or kc (compute dtype), and, when vc
-// is given, a compute-dtype copy of V.
+// is given, a compute-dtype copy of V.  pos_of == nullptr: one sequence, the
+// token index is the position (no table load before the cos/sin loads).
 // ---------------------------------------------------------------------------
 template <typename IO, typename T, int D>
 __global__ __launch_bounds__(kThreads) void rope_k_kernel(
@@ -49,7 +50,7 @@ __global__ __launch_bounds__(kThreads) void rope_k_kernel(
   const long th = idx / CH;  // token * Hkv + head
   const long tok = th / n_heads_kv;
   const long base = th * D + p0;
-  const long ti = (long)pos_of[tok] * H + p0;
+  const long ti = (pos_of != nullptr ? (long)pos_of[tok] : tok) * H + p0;
   float x0[8], x1[8], c[8], s[8], y0[8], y1[8];
   load8(k + base, x0);
   load8(k + base + H, x1);
@@ -866,8 +867,9 @@ hipError_t forward_impl(const FwdLaunch& a, hipStream_t st, KernelTimer* tm) {
     hipExtLaunchKernelGGL((rope_k_kernel<IO, T, D>), dim3(grid), blk, 0, st, t.start(), t.stop(), 0,
                           static_cast<const IO*>(a.k), k_rot,
                           (static_cast<void*>(kc) == static_cast<void*>(k_rot)) ? nullptr : kc,
-                          static_cast<const IO*>(a.v), static_cast<T*>(a.vc), a.pos_of,
-                          a.total_tokens, a.n_heads_kv, a.cos_t, a.sin_t);
+                          static_cast<const IO*>(a.v), static_cast<T*>(a.vc),
+                          a.single_seq ? nullptr : a.pos_of, a.total_tokens, a.n_heads_kv,
+                          a.cos_t, a.sin_t);
     GL_CHECK(hipGetLastError());
     t.launched();
   }
