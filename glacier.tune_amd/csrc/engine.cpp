@@ -21,7 +21,9 @@
 #include <vector>
 
 #include "../../include/glacier_attn.h"
+#include "../../include/glacier_qkv.h"
 #include "attn_launch.hpp"
+#include "proj_launch.hpp"
 
 namespace glacier {
 
@@ -109,10 +111,13 @@ class GpuAttentionEngine {
 
   ~GpuAttentionEngine() {
     (void)hipSetDevice(device_);
-    if (own_stream_ != nullptr) {
-      (void)hipStreamSynchronize(own_stream_);
-      (void)hipStreamDestroy(own_stream_);
+    if (own_stream_ != nullptr) (void)hipStreamSynchronize(own_stream_);
+    if (blas_ != nullptr) {
+      // GEMMs may still run on a caller's stream with the handle's workspace
+      (void)hipDeviceSynchronize();
+      destroy_blas_handle(blas_);
     }
+    if (own_stream_ != nullptr) (void)hipStreamDestroy(own_stream_);
   }
 
   // GpuLoraEngine.SupportsAttention (GpuLoraEngine.cs:111-112): the shapes
@@ -200,6 +205,22 @@ class GpuAttentionEngine {
     a.cos_t = static_cast<const float*>(rope_cos_.ptr);
     a.sin_t = static_cast<const float*>(rope_sin_.ptr);
     check_hip(launch_backward(a, stream(), &timer_), "attention backward launch");
+  }
+
+  // ---- projection with LoRA adapters (glacier_qkv.h) --------------------
+  // GpuLoraEngine.ForwardQKV (GpuLoraEngine.Forward.cs:205-245) with the
+  // LoRA deltas added on the device instead of AddLoraDeltaHost (:366-399).
+  void ProjForward(ProjLaunch& a) {
+    if (a.T == 0) return;
+    ProjScratch(a, false);
+    check_hip(launch_proj_forward(a, stream(), blas()), "projection forward launch");
+  }
+
+  // The block's LoraAdapter.Backward calls (LoraAdapter.cs:190-247).
+  void ProjBackward(ProjLaunch& a) {
+    if (a.T == 0) return;
+    ProjScratch(a, true);
+    check_hip(launch_proj_backward(a, stream(), blas()), "projection backward launch");
   }
 
   // ---- host entry points (fp32 host tensors) ----------------------------
@@ -352,6 +373,30 @@ class GpuAttentionEngine {
     return ref;
   }
 
+  void* blas() {
+    if (blas_ == nullptr) {
+      blas_ = create_blas_handle();
+      if (blas_ == nullptr) fail(GLACIER_ATTN_ERR_DEVICE, "rocblas_create_handle failed");
+    }
+    return blas_;
+  }
+
+  void ProjScratch(ProjLaunch& a, bool backward) {
+    int max_out = 0;
+    for (int p = 0; p < a.n_proj; ++p) max_out = std::max(max_out, a.p[p].out);
+    const size_t T = a.T, r = std::max(a.rank, 1);
+    if (!backward) {
+      a.yf = static_cast<float*>(yf_.ensure(T * max_out * sizeof(float), "projection scratch"));
+    } else {
+      a.dxf = static_cast<float*>(dxf_.ensure(T * a.in * sizeof(float), "dX scratch"));
+      a.dl = static_cast<float*>(dl_.ensure(a.n_proj * T * r * sizeof(float), "dL scratch"));
+      const size_t nblk = (T + 255) / 256;
+      a.part = static_cast<float*>(
+          part_.ensure(nblk * r * std::max(a.in, max_out) * sizeof(float), "gradient partials"));
+    }
+    a.lr = static_cast<float*>(lr_.ensure(T * r * sizeof(float), "low-rank scratch"));
+  }
+
   int device_;
   int precision_;
   hipStream_t own_stream_ = nullptr;
@@ -365,6 +410,9 @@ class GpuAttentionEngine {
   float rope_base_ = 0.0f;
   // device-path scratch
   DeviceBuffer kc_, vc_, wk_, wv_;
+  // projection scratch and the rocBLAS handle (created on first use)
+  DeviceBuffer yf_, lr_, dl_, dxf_, part_;
+  void* blas_ = nullptr;
   // host-path device copies
   DeviceBuffer h_q_, h_k_, h_v_, h_out_, h_lse_, h_qr_, h_kr_, h_dout_, h_dq_, h_dk_, h_dv_;
 };
@@ -435,6 +483,65 @@ Shape shape_of(const glacier_attn_desc* desc) {
   return make_shape(desc->total_tokens, desc->n_seqs, desc->cu_seqlens, desc->n_heads_q,
                     desc->n_heads_kv, desc->head_dim, desc->rope_freq_base,
                     desc->precision, desc->io_dtype);
+}
+
+// Validates a projection call and fills the launch (pointers only).
+ProjLaunch proj_launch_of(const glacier_proj_desc* desc, const void* x, const glacier_lora_proj* proj,
+                          int n_proj, bool backward) {
+  if (desc == nullptr) fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, "desc is NULL");
+  const glacier_proj_desc& d = *desc;
+  if (d.total_tokens < 0) fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, "total_tokens must be >= 0");
+  if (d.in_features <= 0) fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, "in_features must be positive");
+  if (d.precision != GLACIER_ATTN_PREC_FP32 && d.precision != GLACIER_ATTN_PREC_BF16)
+    fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, "unknown precision " + std::to_string(d.precision));
+  if (d.io_dtype != GLACIER_ATTN_IO_F32 && d.io_dtype != GLACIER_ATTN_IO_BF16)
+    fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, "unknown io dtype " + std::to_string(d.io_dtype));
+  if (d.io_dtype == GLACIER_ATTN_IO_BF16 && d.precision != GLACIER_ATTN_PREC_BF16)
+    fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, "bf16 device tensors need GLACIER_ATTN_PREC_BF16");
+  if (proj == nullptr) fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, "proj is NULL");
+  if (n_proj < 1 || n_proj > GLACIER_PROJ_MAX_PROJ)
+    fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, "n_proj must be 1.." + std::to_string(GLACIER_PROJ_MAX_PROJ));
+  if (d.total_tokens > 0 && x == nullptr) fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, "x is NULL");
+  ProjLaunch a{};
+  a.T = d.total_tokens;
+  a.in = d.in_features;
+  a.rank = d.rank;
+  a.io_bf16 = d.io_dtype == GLACIER_ATTN_IO_BF16;
+  a.n_proj = n_proj;
+  a.x = x;
+  bool any_lora = false;
+  for (int p = 0; p < n_proj; ++p) {
+    const glacier_lora_proj& g = proj[p];
+    const std::string at = "proj[" + std::to_string(p) + "]";
+    if (g.out_features <= 0) fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, at + ".out_features must be positive");
+    if (d.total_tokens > 0) {
+      if (g.w == nullptr) fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, at + ".w is NULL");
+      if (!backward && g.y == nullptr) fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, at + ".y is NULL");
+      if (backward && g.dy == nullptr) fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, at + ".dy is NULL");
+    }
+    if (g.lora_a != nullptr) {
+      any_lora = true;
+      if (g.lora_b == nullptr) fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, at + ".lora_b is NULL");
+      if (!std::isfinite(g.scaling)) fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, at + ".scaling is not finite");
+    }
+    a.p[p] = ProjSpec{g.w, g.bias, g.lora_a, g.lora_b, g.scaling, g.out_features,
+                      g.y, g.dy, g.grad_a, g.grad_b};
+  }
+  if (any_lora && (d.rank < 1 || d.rank > GLACIER_PROJ_MAX_RANK))
+    fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT,
+         "rank must be 1.." + std::to_string(GLACIER_PROJ_MAX_RANK) + " when an adapter is given");
+  if (d.in_features % 4 != 0)
+    fail(GLACIER_ATTN_ERR_UNSUPPORTED, "in_features must be a multiple of 4");
+  for (int p = 0; p < n_proj; ++p)
+    if (proj[p].out_features % 4 != 0)
+      fail(GLACIER_ATTN_ERR_UNSUPPORTED, "out_features must be a multiple of 4");
+  if ((long long)d.total_tokens * std::max(d.in_features, 1) >= (1LL << 31))
+    fail(GLACIER_ATTN_ERR_UNSUPPORTED, "tensor too large");
+  for (int p = 0; p < n_proj; ++p)
+    if ((long long)d.total_tokens * proj[p].out_features >= (1LL << 31) ||
+        (long long)proj[p].out_features * d.in_features >= (1LL << 31))
+      fail(GLACIER_ATTN_ERR_UNSUPPORTED, "tensor too large");
+  return a;
 }
 
 void need(const void* p, const char* name) {
@@ -619,6 +726,30 @@ int glacier_attn_kernel_time(glacier_attn_ctx* ctx, int id, double* total_ms, in
     glacier::check_hip(ctx->eng->timer().collect(), "kernel timing");
     *total_ms = ctx->eng->timer().total_ms(id);
     *launches = ctx->eng->timer().launches(id);
+  });
+}
+
+int glacier_proj_forward(glacier_attn_ctx* ctx, const glacier_proj_desc* desc, const void* x,
+                         const glacier_lora_proj* proj, int n_proj) {
+  return guarded([&] {
+    glacier::ProjLaunch a = glacier::proj_launch_of(desc, x, proj, n_proj, false);
+    need(ctx, "ctx");
+    std::lock_guard<std::mutex> g(ctx->eng->lock());
+    ctx->eng->activate();
+    ctx->eng->ProjForward(a);
+  });
+}
+
+int glacier_proj_backward(glacier_attn_ctx* ctx, const glacier_proj_desc* desc, const void* x,
+                          const glacier_lora_proj* proj, int n_proj, void* dx) {
+  return guarded([&] {
+    glacier::ProjLaunch a = glacier::proj_launch_of(desc, x, proj, n_proj, true);
+    need(ctx, "ctx");
+    if (desc->total_tokens > 0) need(dx, "dx");
+    a.dx = dx;
+    std::lock_guard<std::mutex> g(ctx->eng->lock());
+    ctx->eng->activate();
+    ctx->eng->ProjBackward(a);
   });
 }
 

@@ -10,7 +10,9 @@ GpuLoraEngine with the same names and argument meaning:
 
 on host float32 numpy arrays, plus `forward` / `backward` on device-resident
 torch tensors (passed to the library as raw pointers, enqueued on torch's
-current stream).  Errors raise: InvalidArgument (a ValueError, where the C#
+current stream), and `proj_forward` / `proj_backward`: the q/k/v projections
+with LoRA adapters on the device (include/glacier_qkv.h; GpuLoraEngine.ForwardQKV,
+GpuLoraEngine.Forward.cs:205-245, and LoraAdapter.Backward, LoraAdapter.cs:190-247).  Errors raise: InvalidArgument (a ValueError, where the C#
 engine throws ArgumentOutOfRangeException), Unsupported (the shape stays on
 the CPU path), DeviceError, OutOfMemory.  There is no fallback: if the
 library is missing or the device fails, the call raises.
@@ -25,7 +27,8 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libglacier_attn.so")
-HEADER = os.path.join(os.path.dirname(HERE), "include", "glacier_attn.h")
+HEADERS = [os.path.join(os.path.dirname(HERE), "include", h)
+           for h in ("glacier_attn.h", "glacier_qkv.h")]
 
 OK, ERR_INVALID_ARGUMENT, ERR_UNSUPPORTED, ERR_DEVICE, ERR_OUT_OF_MEMORY = 0, 1, 2, 3, 4
 PREC_FP32, PREC_BF16 = 0, 1
@@ -72,14 +75,41 @@ class Desc(ctypes.Structure):
     ]
 
 
+class ProjDesc(ctypes.Structure):
+    _fields_ = [
+        ("total_tokens", ctypes.c_int32),
+        ("in_features", ctypes.c_int32),
+        ("rank", ctypes.c_int32),
+        ("precision", ctypes.c_int32),
+        ("io_dtype", ctypes.c_int32),
+    ]
+
+
+class LoraProj(ctypes.Structure):
+    _fields_ = [
+        ("w", ctypes.c_void_p),
+        ("bias", ctypes.c_void_p),
+        ("lora_a", ctypes.c_void_p),
+        ("lora_b", ctypes.c_void_p),
+        ("scaling", ctypes.c_float),
+        ("out_features", ctypes.c_int32),
+        ("y", ctypes.c_void_p),
+        ("dy", ctypes.c_void_p),
+        ("grad_a", ctypes.c_void_p),
+        ("grad_b", ctypes.c_void_p),
+    ]
+
+
 _lib = None
 
 
 def header_functions() -> list[str]:
-    """Names of every function include/glacier_attn.h declares."""
-    text = open(HEADER).read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(glacier_attn_[a-z_]+)\s*\(", text)))
+    """Names of every function the headers in include/ declare."""
+    names = set()
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
+        names |= set(re.findall(r"\b(glacier_(?:attn|proj)_[a-z_]+)\s*\(", text))
+    return sorted(names)
 
 
 def load():
@@ -112,6 +142,10 @@ def load():
     L.glacier_attn_kernel_name.argtypes = [c_int]
     L.glacier_attn_kernel_time.argtypes = [vp, c_int, ctypes.POINTER(ctypes.c_double),
                                            ctypes.POINTER(ctypes.c_int64)]
+    L.glacier_proj_forward.argtypes = [vp, ctypes.POINTER(ProjDesc), vp, ctypes.POINTER(LoraProj),
+                                       c_int]
+    L.glacier_proj_backward.argtypes = [vp, ctypes.POINTER(ProjDesc), vp,
+                                        ctypes.POINTER(LoraProj), c_int, vp]
     _lib = L
     return L
 
@@ -286,6 +320,80 @@ class GpuAttentionEngine:
                                             self._ptr(out), self._ptr(lse), self._ptr(dq),
                                             self._ptr(dk), self._ptr(dv)))
         return dq, dk, dv
+
+    # ---- projections with LoRA adapters (device tensors) ------------------
+    @staticmethod
+    def _proj_array(projs, x, rank, backward):
+        arr = (LoraProj * len(projs))()
+        p = GpuAttentionEngine._ptr
+        for i, pr in enumerate(projs):
+            w = pr["w"]
+            if not (w.is_cuda and w.is_contiguous() and w.dtype == x.dtype and w.dim() == 2
+                    and w.shape[1] == x.shape[1]):
+                raise TypeError("w must be a contiguous [out, in] GPU tensor of x's dtype")
+            for key in ("bias", "a", "b", "grad_a", "grad_b"):
+                t = pr.get(key)
+                if t is not None and not (t.is_cuda and t.is_contiguous() and t.dtype.is_floating_point
+                                          and t.element_size() == 4):
+                    raise TypeError(f"{key} must be a contiguous float32 GPU tensor")
+            e = arr[i]
+            e.w = p(w).value
+            e.bias = None if pr.get("bias") is None else p(pr["bias"]).value
+            e.lora_a = None if pr.get("a") is None else p(pr["a"]).value
+            e.lora_b = None if pr.get("b") is None else p(pr["b"]).value
+            e.scaling = float(pr.get("scaling", 0.0))
+            e.out_features = int(w.shape[0])
+            e.y = None if pr.get("y") is None else p(pr["y"]).value
+            e.dy = None if pr.get("dy") is None else p(pr["dy"]).value
+            e.grad_a = None if pr.get("grad_a") is None else p(pr["grad_a"]).value
+            e.grad_b = None if pr.get("grad_b") is None else p(pr["grad_b"]).value
+        return arr
+
+    def _proj_desc(self, x, rank, precision):
+        desc = ProjDesc()
+        desc.total_tokens, desc.in_features = int(x.shape[0]), int(x.shape[1])
+        desc.rank = int(rank)
+        desc.precision = int(self.precision if precision is None else precision)
+        desc.io_dtype = self._io_of(x)
+        return desc
+
+    def proj_forward(self, x, projs, rank=0, precision=None):
+        """x [T, in] (GPU, float32 or bfloat16).  projs: dicts with w [out, in]
+        (x's dtype), optional bias [out], a [in, rank], b [rank, out] (float32),
+        scaling, and optionally y [T, out] to write.  Returns the list of y."""
+        import torch
+
+        if not (x.is_cuda and x.is_contiguous() and x.dim() == 2):
+            raise TypeError("x must be a contiguous [T, in] GPU tensor")
+        for pr in projs:
+            if pr.get("y") is None:
+                pr["y"] = torch.empty((x.shape[0], pr["w"].shape[0]), dtype=x.dtype, device=x.device)
+        arr = self._proj_array(projs, x, rank, False)
+        desc = self._proj_desc(x, rank, precision)
+        self._bind_stream()
+        _check(load().glacier_proj_forward(self._h, ctypes.byref(desc), self._ptr(x), arr,
+                                           len(projs)))
+        return [pr["y"] for pr in projs]
+
+    def proj_backward(self, x, projs, rank=0, precision=None, dx=None):
+        """projs as for proj_forward with dy [T, out] (x's dtype) and optional
+        float32 grad_a [in, rank] / grad_b [rank, out] accumulators (added to).
+        Returns dx [T, in] (overwritten)."""
+        import torch
+
+        if not (x.is_cuda and x.is_contiguous() and x.dim() == 2):
+            raise TypeError("x must be a contiguous [T, in] GPU tensor")
+        for pr in projs:
+            dy = pr.get("dy")
+            if dy is None or not (dy.is_cuda and dy.is_contiguous() and dy.dtype == x.dtype):
+                raise TypeError("dy must be a contiguous GPU tensor of x's dtype")
+        dx = torch.empty_like(x) if dx is None else dx
+        arr = self._proj_array(projs, x, rank, True)
+        desc = self._proj_desc(x, rank, precision)
+        self._bind_stream()
+        _check(load().glacier_proj_backward(self._h, ctypes.byref(desc), self._ptr(x), arr,
+                                            len(projs), self._ptr(dx)))
+        return dx
 
     # ---- instrumentation ---------------------------------------------------
     def set_kernel_timing(self, enable: bool) -> None:

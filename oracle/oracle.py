@@ -1,4 +1,5 @@
-"""TEST INFRASTRUCTURE ONLY: ctypes front end of the C oracle (attn_oracle.c).
+"""TEST INFRASTRUCTURE ONLY: ctypes front end of the C oracle (attn_oracle.c,
+lora_oracle.c).
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import
 this module, always as the checker or the timed CPU baseline, never as part of
@@ -9,6 +10,7 @@ Functions that call into liboracle.so follow the reference loop for loop:
   attn_forward                  -> src/Glacier.Tune/Kernels/CausalAttentionKernel.cs:17-77
   attn_backward                 -> src/Glacier.Tune/Kernels/CausalAttentionKernel.cs:79-213
   layer_fwd_bwd                 -> the CPU branch of TransformerBlock.cs:444-485 and :731-741
+  proj_forward / proj_backward  -> LoraAdapter.Forward / Backward (lora_oracle.c)
 The *_fp64 functions are independent brute-force twins in float64 used to pin
 the C restatement (they are not a restatement of the reference's loops).
 """
@@ -54,6 +56,8 @@ def lib():
         L.oracle_layer_fwd_bwd_varlen.restype = i
         L.oracle_fill_normal.argtypes = [_f32p, ctypes.c_size_t, ctypes.c_uint64, f, f]
         L.oracle_num_threads.restype = i
+        L.oracle_proj_forward.argtypes = [_f32p, _f32p, vp, vp, vp, f, _f32p, i, i, i, i]
+        L.oracle_proj_backward.argtypes = [_f32p, _f32p, _f32p, vp, vp, f, vp, vp, vp, i, i, i, i]
         L.oracle_set_num_threads.argtypes = [i]
         _lib = L
     return _lib
@@ -224,6 +228,54 @@ def layer_fp64(q, k, v, dO, freq_base):
     res["dq"] = rope_fp64(res["dq"], freq_base, inverse=True)
     res["dk"] = rope_fp64(res["dk"], freq_base, inverse=True)
     return res
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data
+
+
+def proj_forward(x, w, bias=None, a=None, b=None, scaling=0.0):
+    """LoraAdapter.Forward: y = x W^T + bias + scaling (x A) B.
+
+    x [S,in], w [out,in], bias [out] or None, a [in,r], b [r,out] or None."""
+    x = _c(x); w = _c(w)
+    S, n_in = x.shape; n_out = w.shape[0]
+    bias = None if bias is None else _c(bias)
+    a = None if a is None else _c(a); b = None if b is None else _c(b)
+    rank = 0 if a is None else a.shape[1]
+    y = np.empty((S, n_out), np.float32)
+    lib().oracle_proj_forward(x, w, _ptr(bias), _ptr(a), _ptr(b), scaling, y, S, n_in, n_out, rank)
+    return y
+
+
+def proj_backward(x, dy, w, a=None, b=None, scaling=0.0, dx=None, grad_a=None, grad_b=None):
+    """LoraAdapter.Backward: dx += dy W + scaling (dy B^T) A^T, grad_a += scaling
+    x^T (dy B^T), grad_b += scaling (x A)^T dy.  The accumulators are updated in
+    place (zeros are made for those passed as None) and returned."""
+    x = _c(x); dy = _c(dy); w = _c(w)
+    S, n_in = x.shape; n_out = w.shape[0]
+    a = None if a is None else _c(a); b = None if b is None else _c(b)
+    rank = 0 if a is None else a.shape[1]
+    dx = np.zeros((S, n_in), np.float32) if dx is None else dx
+    if a is not None:
+        grad_a = np.zeros((n_in, rank), np.float32) if grad_a is None else grad_a
+        grad_b = np.zeros((rank, n_out), np.float32) if grad_b is None else grad_b
+    for t in (dx, grad_a, grad_b):
+        assert t is None or (t.dtype == np.float32 and t.flags["C_CONTIGUOUS"])
+    lib().oracle_proj_backward(x, dy, w, _ptr(a), _ptr(b), scaling, _ptr(dx), _ptr(grad_a),
+                               _ptr(grad_b), S, n_in, n_out, rank)
+    return dx, grad_a, grad_b
+
+
+def proj_fp64(x, w, bias=None, a=None, b=None, scaling=0.0):
+    """float64 twin of proj_forward (matrix products, not the reference's loops)."""
+    x = np.asarray(x, np.float64); w = np.asarray(w, np.float64)
+    y = x @ w.T
+    if bias is not None:
+        y = y + np.asarray(bias, np.float64)
+    if a is not None:
+        y = y + scaling * ((x @ np.asarray(a, np.float64)) @ np.asarray(b, np.float64))
+    return y
 
 
 def max_rel_err(x, ref) -> float:

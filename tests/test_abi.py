@@ -1,5 +1,5 @@
 """C-ABI checks that need no GPU: the library loads, exports every function
-include/glacier_attn.h declares, and rejects bad arguments before it touches
+include/glacier_attn.h and include/glacier_qkv.h declare, and rejects bad arguments before it touches
 a device (so these run on any CPU host).  No compute call is made here."""
 import ctypes
 import subprocess
@@ -20,8 +20,9 @@ def test_library_exports_every_header_function():
                          text=True, check=True).stdout
     exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
     assert set(declared) <= exported
-    # nothing else leaks into the ABI under the glacier_attn_ prefix
-    assert {e for e in exported if e.startswith("glacier_attn_")} == set(declared)
+    # nothing else leaks into the ABI under the library's prefixes
+    assert {e for e in exported if e.startswith(("glacier_attn_", "glacier_proj_"))} == set(declared)
+    assert {"glacier_proj_forward", "glacier_proj_backward"} <= set(declared)
 
 
 def test_supports_attention_gate():
@@ -100,3 +101,52 @@ def test_python_front_end_rejects_wrong_host_arrays():
         ga._host(np.zeros((2, 2), np.float64), "q")
     with pytest.raises(TypeError):
         ga._host(np.zeros((4, 4), np.float32)[:, ::2], "q")
+
+
+def _proj_rc(T=8, n_in=16, outs=(8,), rank=4, prec=ga.PREC_BF16, io=ga.IO_BF16, lora=True,
+             n_proj=None, backward=False):
+    L = ga.load()
+    desc = ga.ProjDesc(T, n_in, rank, prec, io)
+    arr = (ga.LoraProj * max(len(outs), 1))()
+    dummy = 16  # any non-null address: validation fails before it is used
+    for i, o in enumerate(outs):
+        arr[i].w = dummy
+        arr[i].out_features = o
+        arr[i].y = dummy
+        arr[i].dy = dummy
+        arr[i].scaling = 2.0
+        if lora:
+            arr[i].lora_a = dummy
+            arr[i].lora_b = dummy
+    n = len(outs) if n_proj is None else n_proj
+    if backward:
+        rc = L.glacier_proj_backward(None, ctypes.byref(desc), dummy, arr, n, dummy)
+    else:
+        rc = L.glacier_proj_forward(None, ctypes.byref(desc), dummy, arr, n)
+    return rc, L.glacier_attn_last_error().decode()
+
+
+def test_projection_argument_errors_come_before_any_device_work():
+    rc, msg = _proj_rc(rank=0)
+    assert rc == ga.ERR_INVALID_ARGUMENT and "rank" in msg
+    rc, msg = _proj_rc(rank=65)
+    assert rc == ga.ERR_INVALID_ARGUMENT and "rank" in msg
+    rc, msg = _proj_rc(prec=ga.PREC_FP32, io=ga.IO_BF16)
+    assert rc == ga.ERR_INVALID_ARGUMENT and "bf16" in msg
+    rc, msg = _proj_rc(outs=(8, 8, 8, 8, 8))
+    assert rc == ga.ERR_INVALID_ARGUMENT and "n_proj" in msg
+    rc, msg = _proj_rc(n_proj=0)
+    assert rc == ga.ERR_INVALID_ARGUMENT and "n_proj" in msg
+    rc, msg = _proj_rc(outs=(0,))
+    assert rc == ga.ERR_INVALID_ARGUMENT and "out_features" in msg
+    rc, msg = _proj_rc(outs=(10,))
+    assert rc == ga.ERR_UNSUPPORTED and "multiple of 4" in msg
+    rc, msg = _proj_rc(n_in=18)
+    assert rc == ga.ERR_UNSUPPORTED and "multiple of 4" in msg
+    rc, msg = _proj_rc(T=-1)
+    assert rc == ga.ERR_INVALID_ARGUMENT and "total_tokens" in msg
+    # no adapter: the rank is not checked; a valid call then needs the context
+    rc, msg = _proj_rc(rank=0, lora=False)
+    assert rc == ga.ERR_INVALID_ARGUMENT and "ctx" in msg
+    rc, msg = _proj_rc(backward=True)
+    assert rc == ga.ERR_INVALID_ARGUMENT and "ctx" in msg

@@ -293,3 +293,93 @@ def test_planted_mistakes_are_caught():
     r = Hq // Hkv
     dv_heads = np.einsum("hij,ihd->jhd", Pd, dO.astype(np.float64)).reshape(S, Hkv, r, D)
     assert oracle.max_rel_err(dv_heads[:, :, :-1].sum(2), ref["dv"]) > 1e-2
+
+
+# --------------------------------------------------------------------------
+# Projection + LoRA adapter (lora_oracle.c: LoraAdapter.Forward/Backward)
+# --------------------------------------------------------------------------
+
+def _proj_inputs(S, n_in, n_out, rank, seed=11):
+    rng = np.random.default_rng(seed)
+    f = lambda *shape: rng.standard_normal(shape).astype(np.float32)
+    return (f(S, n_in), f(n_out, n_in) / np.sqrt(n_in), f(n_out), f(n_in, rank) / np.sqrt(n_in),
+            f(rank, n_out), f(S, n_out))
+
+
+def test_proj_forward_matches_matrix_products():
+    """y = x W^T + bias + s (x A) B (LoraAdapter.cs:15) against numpy float64 products."""
+    x, w, bias, a, b, _ = _proj_inputs(9, 40, 24, 4)
+    ref = oracle.proj_fp64(x, w, bias, a, b, 2.0)
+    assert oracle.max_rel_err(oracle.proj_forward(x, w, bias, a, b, 2.0), ref) < 1e-6
+    # no adapter, no bias: the plain product
+    assert oracle.max_rel_err(oracle.proj_forward(x, w), x.astype(np.float64) @ w.T) < 1e-6
+
+
+def test_proj_forward_one_hot_rows_and_fresh_adapter():
+    """x = e_k picks column k of W; a fresh adapter (B = 0, LoraAdapter.cs:106) adds
+    nothing; a rank-1 adapter adds s A[k,0] B[0,:] to row e_k."""
+    n_in, n_out = 12, 7
+    _, w, bias, a, b, _ = _proj_inputs(1, n_in, n_out, 1)
+    x = np.eye(n_in, dtype=np.float32)
+    y = oracle.proj_forward(x, w, bias, a, b, 3.0)
+    expect = w.T.astype(np.float64) + bias + 3.0 * a.astype(np.float64) @ b.astype(np.float64)
+    assert oracle.max_rel_err(y, expect) < 1e-6
+    y0 = oracle.proj_forward(x, w, bias, a, np.zeros_like(b), 3.0)
+    assert np.array_equal(y0, oracle.proj_forward(x, w, bias))
+
+
+def test_proj_backward_is_the_gradient_of_the_forward():
+    """Central differences (float64) of L = sum dy * y w.r.t. x, A and B."""
+    S, n_in, n_out, rank, s = 5, 8, 6, 3, 1.5
+    x, w, bias, a, b, dy = _proj_inputs(S, n_in, n_out, rank, seed=3)
+    dx, ga, gb = oracle.proj_backward(x, dy, w, a, b, s)
+    X, A, B, DY = (t.astype(np.float64) for t in (x, a, b, dy))
+    loss = lambda X_, A_, B_: float(np.sum(DY * oracle.proj_fp64(X_, w, bias, A_, B_, s)))
+    eps = 1e-4
+    for got, base, which in ((dx, X, 0), (ga, A, 1), (gb, B, 2)):
+        num = np.zeros_like(base)
+        for idx in np.ndindex(base.shape):
+            hi = [X.copy(), A.copy(), B.copy()]
+            lo = [X.copy(), A.copy(), B.copy()]
+            hi[which][idx] += eps
+            lo[which][idx] -= eps
+            num[idx] = (loss(*hi) - loss(*lo)) / (2 * eps)
+        assert oracle.max_rel_err(got, num) < 1e-5, which
+
+
+def test_proj_backward_accumulates():
+    """dx, grad_a and grad_b are added to (the reference's Grad tensors and dXInput)."""
+    x, w, _, a, b, dy = _proj_inputs(6, 10, 8, 2)
+    dx, ga, gb = oracle.proj_backward(x, dy, w, a, b, 0.5)
+    dx2, ga2, gb2 = oracle.proj_backward(x, dy, w, a, b, 0.5, dx.copy(), ga.copy(), gb.copy())
+    for one, two in ((dx, dx2), (ga, ga2), (gb, gb2)):
+        assert oracle.max_rel_err(two, 2.0 * one) < 1e-6
+    # without an adapter only the base gradient dy W is formed
+    dxb, ga0, gb0 = oracle.proj_backward(x, dy, w)
+    assert ga0 is None and gb0 is None
+    assert oracle.max_rel_err(dxb, dy.astype(np.float64) @ w) < 1e-6
+
+
+def test_proj_planted_mistakes_are_caught():
+    """Each plausible slip in the projection math changes the result beyond the
+    parity tolerances, so the checks above would catch it."""
+    S, n_in, n_out, rank, s = 7, 16, 16, 4, 2.0
+    x, w, bias, a, b, dy = _proj_inputs(S, n_in, n_out, rank, seed=5)
+    y = oracle.proj_forward(x, w, bias, a, b, s)
+    slips = {
+        "W not transposed": oracle.proj_fp64(x, w.T, bias, a, b, s),
+        "bias dropped": oracle.proj_fp64(x, w, None, a, b, s),
+        "scaling dropped": oracle.proj_fp64(x, w, bias, a, b, 1.0),
+        "A, B swapped roles": oracle.proj_fp64(x, w, bias, b.T, a.T, s),
+    }
+    for name, bad in slips.items():
+        assert oracle.max_rel_err(bad, y) > 1e-2, name
+    dx, ga, gb = oracle.proj_backward(x, dy, w, a, b, s)
+    X, A, B, DY = (t.astype(np.float64) for t in (x, a, b, dy))
+    grad_slips = {
+        "dx with W^T": (dx, DY @ w.T + s * (DY @ B.T) @ A.T),
+        "grad_a without scaling": (ga, X.T @ (DY @ B.T)),
+        "grad_b with the output index reversed": (gb, s * (X @ A).T @ DY[:, ::-1]),
+    }
+    for name, (got, bad) in grad_slips.items():
+        assert oracle.max_rel_err(got, bad) > 1e-2, name

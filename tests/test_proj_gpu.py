@@ -1,0 +1,191 @@
+"""Parity of the projection step with LoRA adapters (glacier_proj_forward /
+glacier_proj_backward, include/glacier_qkv.h) against the CPU oracle
+(oracle/lora_oracle.c: LoraAdapter.Forward/Backward, LoraKernels.cs), through
+the C ABI on device tensors.
+
+Gates (the north star's): fp32 mode max-rel-err <= 1e-4, bf16 mode <= 2e-2,
+normwise (max|x - ref| / max|ref|) per tensor.  In the bf16 mode x and W are
+bf16 tensors; the oracle runs on the same bf16-rounded values in fp32.  At the
+Qwen2.5-7B shape (too slow for the loop-for-loop oracle in a test) the
+reference is torch float64 matrix products on the GPU.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import glacier_attn as ga
+import oracle
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+FP32_GATE, BF16_GATE = 1e-4, 2e-2
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def engines():
+    assert torch.cuda.is_available(), "GPU tests need a ROCm GPU"
+    e = {ga.PREC_FP32: ga.GpuAttentionEngine(0, ga.PREC_FP32),
+         ga.PREC_BF16: ga.GpuAttentionEngine(0, ga.PREC_BF16)}
+    yield e
+    for eng in e.values():
+        eng.close()
+
+
+def _problem(T, n_in, outs, rank, seed, adapters=(True, False, True)):
+    """Seeded fp32 host arrays: x, and per projection w, bias, a, b, dy."""
+    rng = np.random.default_rng(seed)
+    f = lambda *s: rng.standard_normal(s).astype(np.float32)
+    x = f(T, n_in)
+    projs = []
+    for o, lora in zip(outs, adapters):
+        p = {"w": f(o, n_in) / np.sqrt(n_in), "bias": 0.1 * f(o), "dy": 0.01 * f(T, o),
+             "scaling": 2.0}
+        if lora:
+            p["a"] = f(n_in, rank) / np.sqrt(n_in)
+            p["b"] = 0.1 * f(rank, o)  # a trained adapter: B no longer zero
+        projs.append(p)
+    return x, projs
+
+
+def _to_dev(x, projs, io_dtype, dev):
+    def d(a, dt=torch.float32):
+        return torch.from_numpy(np.ascontiguousarray(a)).to(dev, dt).contiguous()
+    xd = d(x, io_dtype)
+    dprojs = []
+    for p in projs:
+        q = {"w": d(p["w"], io_dtype), "bias": d(p["bias"]), "scaling": p["scaling"],
+             "dy": d(p["dy"], io_dtype)}
+        if "a" in p:
+            q["a"], q["b"] = d(p["a"]), d(p["b"])
+            q["grad_a"] = torch.zeros_like(q["a"])
+            q["grad_b"] = torch.zeros_like(q["b"])
+        dprojs.append(q)
+    return xd, dprojs
+
+
+def _rounded(x, projs, bf16):
+    """The operands the library sees, as fp32 host arrays (bf16-rounded in the
+    bf16 mode; bias and adapters stay fp32)."""
+    if not bf16:
+        return x, projs
+    r = oracle.round_bf16
+    return r(x), [dict(p, w=r(p["w"]), dy=r(p["dy"])) for p in projs]
+
+
+def _oracle(x, projs, rank):
+    ys, dx = [], np.zeros_like(x)
+    grads = []
+    for p in projs:
+        ys.append(oracle.proj_forward(x, p["w"], p["bias"], p.get("a"), p.get("b"), p["scaling"]))
+        _, ga_, gb_ = oracle.proj_backward(x, p["dy"], p["w"], p.get("a"), p.get("b"), p["scaling"],
+                                           dx=dx)
+        grads.append((ga_, gb_))
+    return ys, dx, grads
+
+
+SHAPES = {  # T, in, (q, k, v outs), rank
+    "qwen05b_t256": (256, 896, (896, 128, 128), 8),
+    "ragged_t37": (37, 96, (64, 32, 32), 4),
+}
+
+
+@pytest.mark.parametrize("shape", sorted(SHAPES))
+@pytest.mark.parametrize("prec", [ga.PREC_FP32, ga.PREC_BF16], ids=["fp32", "bf16"])
+def test_projection_matches_oracle(engines, prec, shape):
+    T, n_in, outs, rank = SHAPES[shape]
+    bf16 = prec == ga.PREC_BF16
+    _say(f"[proj] prec={'bf16' if bf16 else 'fp32'} shape={shape} T={T} in={n_in} outs={outs} r={rank}")
+    x, projs = _problem(T, n_in, outs, rank, seed=7)
+    dev = torch.device("cuda:0")
+    io = torch.bfloat16 if bf16 else torch.float32
+    xd, dprojs = _to_dev(x, projs, io, dev)
+    eng = engines[prec]
+    ys = eng.proj_forward(xd, dprojs, rank)
+    dx = eng.proj_backward(xd, dprojs, rank)
+    torch.cuda.synchronize()
+    xr, pr = _rounded(x, projs, bf16)
+    ys_ref, dx_ref, grads_ref = _oracle(xr, pr, rank)
+    gate = BF16_GATE if bf16 else FP32_GATE
+    errs = {}
+    for i, (y, yr) in enumerate(zip(ys, ys_ref)):
+        errs[f"y{i}"] = oracle.max_rel_err(y.float().cpu().numpy(), yr)
+    errs["dx"] = oracle.max_rel_err(dx.float().cpu().numpy(), dx_ref)
+    for i, (p, (gar, gbr)) in enumerate(zip(dprojs, grads_ref)):
+        if "a" in p:
+            errs[f"grad_a{i}"] = oracle.max_rel_err(p["grad_a"].cpu().numpy(), gar)
+            errs[f"grad_b{i}"] = oracle.max_rel_err(p["grad_b"].cpu().numpy(), gbr)
+    _say("  " + " ".join(f"{k}={v:.2e}" for k, v in errs.items()) + f" (gate {gate:g})")
+    for k, v in errs.items():
+        assert v <= gate, k
+
+
+@pytest.mark.parametrize("prec", [ga.PREC_FP32, ga.PREC_BF16], ids=["fp32", "bf16"])
+def test_projection_at_qwen7b_shape_vs_fp64(engines, prec):
+    """T=512, hidden 3584 -> q 3584, k/v 512, rank 16 (alpha 32): against torch
+    float64 products on the GPU of the same (rounded) operands."""
+    T, n_in, outs, rank = 512, 3584, (3584, 512, 512), 16
+    bf16 = prec == ga.PREC_BF16
+    _say(f"[proj] qwen7b shape prec={'bf16' if bf16 else 'fp32'}")
+    x, projs = _problem(T, n_in, outs, rank, seed=3, adapters=(True, True, True))
+    dev = torch.device("cuda:0")
+    io = torch.bfloat16 if bf16 else torch.float32
+    xd, dprojs = _to_dev(x, projs, io, dev)
+    eng = engines[prec]
+    ys = eng.proj_forward(xd, dprojs, rank)
+    dx = eng.proj_backward(xd, dprojs, rank)
+    torch.cuda.synchronize()
+    X = xd.double()
+    gate = BF16_GATE if bf16 else FP32_GATE
+    dX = torch.zeros_like(X)
+    for i, p in enumerate(dprojs):
+        W, A, B, dY = p["w"].double(), p["a"].double(), p["b"].double(), p["dy"].double()
+        s = p["scaling"]
+        y_ref = X @ W.T + p["bias"].double() + s * (X @ A) @ B
+        e = (ys[i].double() - y_ref).abs().max() / y_ref.abs().max()
+        dL = dY @ B.T
+        ga_ref, gb_ref = s * X.T @ dL, s * (X @ A).T @ dY
+        e_a = (p["grad_a"].double() - ga_ref).abs().max() / ga_ref.abs().max()
+        e_b = (p["grad_b"].double() - gb_ref).abs().max() / gb_ref.abs().max()
+        dX += dY @ W + s * dL @ A.T
+        _say(f"  p{i}: y {e.item():.2e} grad_a {e_a.item():.2e} grad_b {e_b.item():.2e}")
+        assert e.item() <= gate and e_a.item() <= gate and e_b.item() <= gate
+    e = (dx.double() - dX).abs().max() / dX.abs().max()
+    _say(f"  dx {e.item():.2e} (gate {gate:g})")
+    assert e.item() <= gate
+
+
+def test_projection_repeatable_accumulating_and_empty(engines):
+    """Bitwise repeatable; grad_a/grad_b accumulate; no adapter gives x W^T + b;
+    T = 0 is a no-op."""
+    eng = engines[ga.PREC_BF16]
+    T, n_in, outs, rank = 64, 128, (64, 32, 32), 8
+    x, projs = _problem(T, n_in, outs, rank, seed=9)
+    dev = torch.device("cuda:0")
+    xd, dprojs = _to_dev(x, projs, torch.bfloat16, dev)
+    y1 = [y.clone() for y in eng.proj_forward(xd, dprojs, rank)]
+    y2 = eng.proj_forward(xd, dprojs, rank)
+    assert all(torch.equal(a, b) for a, b in zip(y1, y2))
+    dx1 = eng.proj_backward(xd, dprojs, rank).clone()
+    g1 = [(p["grad_a"].clone(), p["grad_b"].clone()) for p in dprojs if "a" in p]
+    dx2 = eng.proj_backward(xd, dprojs, rank)
+    torch.cuda.synchronize()
+    assert torch.equal(dx1, dx2)
+    for (a1, b1), p in zip(g1, [p for p in dprojs if "a" in p]):
+        assert torch.allclose(p["grad_a"], 2 * a1, rtol=1e-6, atol=0)
+        assert torch.allclose(p["grad_b"], 2 * b1, rtol=1e-6, atol=0)
+    # the k projection has no adapter: plain x W^T + bias
+    yk = y1[1].double().cpu().numpy()
+    xr = oracle.round_bf16(x).astype(np.float64)
+    ref = xr @ oracle.round_bf16(projs[1]["w"]).astype(np.float64).T + projs[1]["bias"]
+    assert oracle.max_rel_err(yk, ref) <= BF16_GATE
+    # empty call
+    x0 = torch.empty((0, n_in), dtype=torch.bfloat16, device=dev)
+    ys0 = eng.proj_forward(x0, [{"w": dprojs[0]["w"]}], rank=0)
+    assert ys0[0].shape == (0, outs[0])
