@@ -151,3 +151,116 @@ def test_lora_loss_drift(engines, prec, layout):
     assert np.all(np.isfinite(got))
     assert ref[-1] < ref[0], "the harness must actually train (loss falls)"
     assert drift.max() <= DRIFT_GATE
+
+
+# --------------------------------------------------------------------------
+# The whole block on the device: q/k/v projections with their LoRA adapters
+# through glacier_proj_forward/backward (the device replacement of
+# GpuLoraEngine.ForwardQKV + AddLoraDeltaHost and LoraAdapter.Backward),
+# attention through the library, loss and AdamW in torch on the GPU; Q, K, V
+# and their gradients never leave HBM.  Compared with the same CPU fp32 run as
+# above (torch projections, oracle attention).
+# --------------------------------------------------------------------------
+
+class LibraryProjQKV(torch.autograd.Function):
+    """q = x Wq^T + (x Aq) Bq, k = x Wk^T, v = x Wv^T + (x Av) Bv (scaling 1)."""
+
+    @staticmethod
+    def forward(ctx, x, Aq, Bq, Av, Bv, eng, io_dtype, w):
+        xd = x.detach().to(io_dtype).contiguous()
+        projs = [{"w": w["q"], "a": Aq.detach().contiguous(), "b": Bq.detach().contiguous(),
+                  "scaling": 1.0},
+                 {"w": w["k"]},
+                 {"w": w["v"], "a": Av.detach().contiguous(), "b": Bv.detach().contiguous(),
+                  "scaling": 1.0}]
+        q, k, v = eng.proj_forward(xd, projs, RANK)
+        ctx.xd, ctx.projs, ctx.eng, ctx.io_dtype = xd, projs, eng, io_dtype
+        return q.float(), k.float(), v.float()
+
+    @staticmethod
+    def backward(ctx, dq, dk, dv):
+        projs = ctx.projs
+        for p, g in zip(projs, (dq, dk, dv)):
+            p["dy"] = g.to(ctx.io_dtype).contiguous()
+            if "a" in p:
+                p["grad_a"] = torch.zeros_like(p["a"])
+                p["grad_b"] = torch.zeros_like(p["b"])
+        ctx.eng.proj_backward(ctx.xd, projs, RANK)
+        return (None, projs[0]["grad_a"], projs[0]["grad_b"], projs[2]["grad_a"],
+                projs[2]["grad_b"], None, None, None)
+
+
+class LibraryAttentionDevice(torch.autograd.Function):
+    """LibraryAttention with device tensors in and out."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, cu, eng, io_dtype):
+        T = q.shape[0]
+        qd = q.detach().reshape(T, HQ, D).to(io_dtype).contiguous()
+        kd = k.detach().reshape(T, HKV, D).to(io_dtype).contiguous()
+        vd = v.detach().reshape(T, HKV, D).to(io_dtype).contiguous()
+        out, lse, q_rot, k_rot = eng.forward(qd, kd, vd, THETA, cu_seqlens=cu, save=True)
+        ctx.saved = (q_rot, k_rot, vd, out, lse)
+        ctx.cu, ctx.eng, ctx.io_dtype = cu, eng, io_dtype
+        return out.float().reshape(T, HQ * D)
+
+    @staticmethod
+    def backward(ctx, d_out):
+        q_rot, k_rot, vd, out, lse = ctx.saved
+        T = q_rot.shape[0]
+        dO = d_out.reshape(T, HQ, D).to(ctx.io_dtype).contiguous()
+        dq, dk, dv = ctx.eng.backward(dO, q_rot, k_rot, vd, out, lse, THETA, cu_seqlens=ctx.cu)
+        return (dq.float().reshape(T, -1), dk.float().reshape(T, -1), dv.float().reshape(T, -1),
+                None, None, None)
+
+
+def train_device(eng, io_dtype, cu, T, seed=0):
+    """train() with every tensor on the GPU and the block through the library."""
+    dev = torch.device("cuda:0")
+    gen = torch.Generator().manual_seed(seed)
+    x = torch.randn(T, HIDDEN, generator=gen)
+    Wq = torch.randn(HIDDEN, HQ * D, generator=gen) / HIDDEN ** 0.5
+    Wk = torch.randn(HIDDEN, HKV * D, generator=gen) / HIDDEN ** 0.5
+    Wv = torch.randn(HIDDEN, HKV * D, generator=gen) / HIDDEN ** 0.5
+    Wo = torch.randn(HQ * D, HIDDEN, generator=gen) / (HQ * D) ** 0.5
+    target = torch.randn(T, HIDDEN, generator=gen)
+    Aq = torch.randn(HIDDEN, RANK, generator=gen) / HIDDEN ** 0.5
+    Av = torch.randn(HIDDEN, RANK, generator=gen) / HIDDEN ** 0.5
+    x, Wo, target = x.to(dev), Wo.to(dev), target.to(dev)
+    # base weights as the GGUF row order [out][in], in the engine's I/O type
+    w = {n: W.T.contiguous().to(dev, io_dtype) for n, W in (("q", Wq), ("k", Wk), ("v", Wv))}
+    Aq = Aq.to(dev).requires_grad_()
+    Av = Av.to(dev).requires_grad_()
+    Bq = torch.zeros(RANK, HQ * D, device=dev, requires_grad=True)
+    Bv = torch.zeros(RANK, HKV * D, device=dev, requires_grad=True)
+    opt = torch.optim.AdamW([Aq, Bq, Av, Bv], lr=1e-2, weight_decay=0.01)
+    losses = []
+    for _ in range(STEPS):
+        q, k, v = LibraryProjQKV.apply(x, Aq, Bq, Av, Bv, eng, io_dtype, w)
+        o = LibraryAttentionDevice.apply(q, k, v, cu, eng, io_dtype)
+        loss = ((o @ Wo - target) ** 2).mean()
+        opt.zero_grad()
+        loss.backward()
+        opt.step()
+        losses.append(loss.item())
+    return np.array(losses)
+
+
+@pytest.mark.parametrize("layout", sorted(LAYOUTS))
+@pytest.mark.parametrize("prec", [ga.PREC_BF16, ga.PREC_FP32], ids=["bf16", "fp32"])
+def test_lora_block_on_device_loss_drift(engines, prec, layout):
+    lengths = LAYOUTS[layout]
+    T = sum(lengths)
+    cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+    cu_lib = None if len(lengths) == 1 else cu
+    io_dtype = torch.bfloat16 if prec == ga.PREC_BF16 else torch.float32
+    _say(f"[lora-drift device block] prec={'bf16' if prec == ga.PREC_BF16 else 'fp32'} "
+         f"layout={layout} T={T} steps={STEPS}")
+    ref = train(lambda q, k, v: OracleAttention.apply(q, k, v, cu), T)
+    got = train_device(engines[prec], io_dtype, cu_lib, T)
+    drift = np.abs(got - ref)
+    _say(f"  cpu path     losses {np.array2string(ref, precision=6)}")
+    _say(f"  device block losses {np.array2string(got, precision=6)}")
+    _say(f"  max drift {drift.max():.3e} (gate {DRIFT_GATE:g})")
+    assert np.all(np.isfinite(got))
+    assert drift.max() <= DRIFT_GATE
