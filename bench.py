@@ -2,6 +2,7 @@
 """Benchmark: causal GQA attention forward + backward on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config qwen7b_s512]
+    python bench.py --component proj      # the q/k/v projections with LoRA adapters
 
 One step = the attention layer's forward (RoPE, QK^T, causal softmax, PV,
 saving the row log-sum-exp) followed by its backward (dP, softmax gradient,
@@ -20,6 +21,11 @@ roofline = the dominant kernel (largest share of device time), its average
          (profiles/attn_kernels_qwen7b_s512_pmc.md).
 cpu_baseline = the C restatement of the reference CPU path (oracle/), fp32,
          on this host's cores, over a bounded sample.
+
+--component proj measures the projection step instead (include/glacier_qkv.h):
+one step = glacier_proj_forward + glacier_proj_backward of the q, k and v
+projections of Qwen2.5-7B (T=512, hidden 3584 -> 3584, 512, 512, with bias)
+with rank-16 LoRA adapters (alpha 32) on all three, bf16 tensors.
 """
 import argparse
 import json
@@ -106,6 +112,130 @@ def cpu_baseline(lengths, Hq, Hkv, D, theta, budget_s=12.0):
     }
 
 
+PROJ_SHAPE = (512, 3584, (3584, 512, 512), 16, 2.0)  # T, hidden, q/k/v outs, rank, alpha/rank
+
+
+def proj_flops(T, n_in, outs, rank):
+    """Algorithmic FLOPs of one projection forward + backward: the base
+    products X W^T and dY W, and per adapter X A, (XA) B, dY B^T, (XA)^T dY,
+    X^T dL and dL A^T (2 flop per multiply-add; no credit for recomputing X A)."""
+    base = 2 * 2.0 * T * n_in * sum(outs)
+    lora = sum(2.0 * T * rank * (3 * n_in + 3 * o) for o in outs)
+    return base + lora
+
+
+def cpu_proj_baseline(T, n_in, outs, rank, s, budget_s=20.0):
+    """Times oracle.proj_forward + proj_backward for the three projections."""
+    import numpy as np
+
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+
+    threads = max(1, min(16, os.cpu_count() or 1))
+    oracle.set_threads(threads)
+    x = oracle.fill_normal((T, n_in), 1)
+    projs = []
+    for i, o in enumerate(outs):
+        projs.append((oracle.fill_normal((o, n_in), 10 + i, 0.0, n_in ** -0.5),
+                      oracle.fill_normal((o,), 20 + i, 0.0, 0.1),
+                      oracle.fill_normal((n_in, rank), 30 + i, 0.0, n_in ** -0.5),
+                      oracle.fill_normal((rank, o), 40 + i, 0.0, 0.1),
+                      oracle.fill_normal((T, o), 50 + i, 0.0, 0.01)))
+
+    def one():
+        dx = np.zeros((T, n_in), np.float32)
+        for w, b, a, bb, dy in projs:
+            oracle.proj_forward(x, w, b, a, bb, s)
+            oracle.proj_backward(x, dy, w, a, bb, s, dx=dx)
+
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 3 and (not times or time.perf_counter() < t_end):
+        t0 = time.perf_counter()
+        one()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    return {
+        "value": round(proj_flops(T, n_in, outs, rank) / med / 1e12, 6),
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"median of {len(times)} full q/k/v projection fwd+bwd passes "
+                   f"(LoraAdapter.Forward/Backward restated, fp32) at T={T}, hidden={n_in}, "
+                   f"outs={list(outs)}, rank={rank}; {med * 1e3:.0f} ms each; OpenMP over rows"),
+    }
+
+
+def run_proj(args):
+    import torch
+
+    import glacier_attn as ga
+
+    T, n_in, outs, rank, s = PROJ_SHAPE
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+    rnd = lambda *shape: torch.randn(*shape, device=dev, generator=g)
+    x = rnd(T, n_in).bfloat16()
+    projs = []
+    for o in outs:
+        projs.append({"w": (rnd(o, n_in) / n_in ** 0.5).bfloat16(), "bias": 0.1 * rnd(o),
+                      "a": rnd(n_in, rank) / n_in ** 0.5, "b": 0.1 * rnd(rank, o), "scaling": s,
+                      "y": torch.empty(T, o, device=dev, dtype=torch.bfloat16),
+                      "dy": (0.01 * rnd(T, o)).bfloat16(),
+                      "grad_a": torch.zeros(n_in, rank, device=dev),
+                      "grad_b": torch.zeros(rank, o, device=dev)})
+    dx = torch.empty_like(x)
+    eng = ga.GpuAttentionEngine(0, ga.PREC_BF16)
+
+    def step():
+        eng.proj_forward(x, projs, rank)
+        eng.proj_backward(x, projs, rank, dx=dx)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(args.steps):
+        step()
+    stop.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(stop) / args.steps
+    flops = proj_flops(T, n_in, outs, rank)
+    tflops = flops / (ms * 1e-3) / 1e12
+    cpu = None if args.no_cpu else cpu_proj_baseline(T, n_in, outs, rank, s)
+    res = {
+        "metric": "q/k/v projection + LoRA fwd+bwd TFLOP/s + % bf16 MFMA peak, Qwen2.5-7B shape T=512",
+        "value": round(tflops, 3),
+        "unit": "TFLOP/s",
+        "pct_bf16_peak": round(100.0 * tflops / PEAK_BF16_TFLOPS, 3),
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded normal x, W, bias, adapters, dY; device-resident)",
+        "config": {
+            "workload": "qkv_proj_qwen7b_t512: q/k/v projections with bias and rank-16 LoRA, fwd+bwd",
+            "tokens": T, "hidden": n_in, "out_features": list(outs), "lora_rank": rank,
+            "lora_scaling": s, "io": "bf16 x/W/y/dY/dX, fp32 bias/adapters/gradients",
+            "parallelism": "1 GPU", "algorithmic_gflop_per_step": round(flops / 1e9, 4),
+        },
+        "roofline": {"bound": "mfma", "kernel": "whole step (rocBLAS base GEMMs + HIP low-rank "
+                     "kernels)", "achieved": round(tflops, 3), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 5),
+                     "traffic": None},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(res), flush=True)
+    eng.close()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -113,6 +243,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="qwen7b_s512", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--component", default="attention", choices=["attention", "proj"],
+                    help="attention (the headline) or the q/k/v projections with LoRA adapters")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run 5 plain device copies of MIB MiB (a known-size kernel that "
                          "calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE counters)")
@@ -121,6 +253,9 @@ def main():
         print(json.dumps({"error": "this build runs on one GPU only; use --gpus 1 "
                                    "(the path shards by KV-head group, see DESIGN.md)"}))
         sys.exit(2)
+    if args.component == "proj":
+        run_proj(args)
+        return
 
     import numpy as np
     import torch

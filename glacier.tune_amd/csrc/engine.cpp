@@ -382,19 +382,14 @@ class GpuAttentionEngine {
   }
 
   void ProjScratch(ProjLaunch& a, bool backward) {
-    int max_out = 0;
-    for (int p = 0; p < a.n_proj; ++p) max_out = std::max(max_out, a.p[p].out);
-    const size_t T = a.T, r = std::max(a.rank, 1);
-    if (!backward) {
-      a.yf = static_cast<float*>(yf_.ensure(T * max_out * sizeof(float), "projection scratch"));
-    } else {
-      a.dxf = static_cast<float*>(dxf_.ensure(T * a.in * sizeof(float), "dX scratch"));
-      a.dl = static_cast<float*>(dl_.ensure(a.n_proj * T * r * sizeof(float), "dL scratch"));
-      const size_t nblk = (T + 255) / 256;
-      a.part = static_cast<float*>(
-          part_.ensure(nblk * r * std::max(a.in, max_out) * sizeof(float), "gradient partials"));
-    }
-    a.lr = static_cast<float*>(lr_.ensure(T * r * sizeof(float), "low-rank scratch"));
+    const ProjScratchNeed need = proj_scratch_need(a, backward);
+    auto get = [](DeviceBuffer& buf, long floats, const char* what) {
+      return floats > 0 ? static_cast<float*>(buf.ensure(floats * sizeof(float), what)) : nullptr;
+    };
+    a.yf = get(yf_, need.yf, "projection scratch");
+    a.dxf = get(dxf_, need.dxf, "dX scratch");
+    a.lowrank = get(lowrank_, need.lowrank, "low-rank scratch");
+    a.part = get(part_, need.part, "low-rank split sums");
   }
 
   int device_;
@@ -411,7 +406,7 @@ class GpuAttentionEngine {
   // device-path scratch
   DeviceBuffer kc_, vc_, wk_, wv_;
   // projection scratch and the rocBLAS handle (created on first use)
-  DeviceBuffer yf_, lr_, dl_, dxf_, part_;
+  DeviceBuffer yf_, dxf_, lowrank_, part_;
   void* blas_ = nullptr;
   // host-path device copies
   DeviceBuffer h_q_, h_k_, h_v_, h_out_, h_lse_, h_qr_, h_kr_, h_dout_, h_dq_, h_dk_, h_dv_;
@@ -486,6 +481,8 @@ Shape shape_of(const glacier_attn_desc* desc) {
 }
 
 // Validates a projection call and fills the launch (pointers only).
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
 ProjLaunch proj_launch_of(const glacier_proj_desc* desc, const void* x, const glacier_lora_proj* proj,
                           int n_proj, bool backward) {
   if (desc == nullptr) fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, "desc is NULL");
@@ -535,6 +532,13 @@ ProjLaunch proj_launch_of(const glacier_proj_desc* desc, const void* x, const gl
   for (int p = 0; p < n_proj; ++p)
     if (proj[p].out_features % 4 != 0)
       fail(GLACIER_ATTN_ERR_UNSUPPORTED, "out_features must be a multiple of 4");
+  // the kernels move 4 consecutive elements of x, y, dy, dx and lora_b at once
+  if (!aligned16(x)) fail(GLACIER_ATTN_ERR_UNSUPPORTED, "x must be 16-byte aligned");
+  for (int p = 0; p < n_proj; ++p)
+    if (!aligned16(backward ? proj[p].dy : proj[p].y) || !aligned16(proj[p].lora_b))
+      fail(GLACIER_ATTN_ERR_UNSUPPORTED,
+           "proj[" + std::to_string(p) + "]." + (backward ? "dy" : "y") +
+               " and .lora_b must be 16-byte aligned");
   if ((long long)d.total_tokens * std::max(d.in_features, 1) >= (1LL << 31))
     fail(GLACIER_ATTN_ERR_UNSUPPORTED, "tensor too large");
   for (int p = 0; p < n_proj; ++p)
@@ -746,6 +750,7 @@ int glacier_proj_backward(glacier_attn_ctx* ctx, const glacier_proj_desc* desc, 
     glacier::ProjLaunch a = glacier::proj_launch_of(desc, x, proj, n_proj, true);
     need(ctx, "ctx");
     if (desc->total_tokens > 0) need(dx, "dx");
+    if (!glacier::aligned16(dx)) glacier::fail(GLACIER_ATTN_ERR_UNSUPPORTED, "dx must be 16-byte aligned");
     a.dx = dx;
     std::lock_guard<std::mutex> g(ctx->eng->lock());
     ctx->eng->activate();

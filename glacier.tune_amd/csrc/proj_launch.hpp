@@ -6,7 +6,7 @@
 
 namespace glacier {
 
-constexpr int kMaxRank = 64;  // LoRA ranks the kernels take (1..64)
+constexpr int kMaxRank = 64;  // largest LoRA rank taken
 constexpr int kMaxProj = 4;   // projections of one input per call
 
 // One projection p of the input: W [out][in] (io dtype), bias [out] fp32 or
@@ -33,21 +33,18 @@ struct ProjLaunch {
   ProjSpec p[kMaxProj];
   const void* x;  // [T][in]
   void* dx;       // [T][in] (backward; overwritten)
-  // scratch
-  float* yf;    // [T][max out] base product
-  float* lr;    // [T][r] X A
-  float* dl;    // [n_proj][T][r] dY B^T
-  float* dxf;   // [T][in] sum of the base gradients
-  float* part;  // [ceil(T/256)][r][max(in, out)] partial gradient sums
+  // scratch (fp32), sized by proj_scratch_need
+  float* yf;       // forward: [T][out_p] base products, one after another
+  float* dxf;      // backward: [T][in] sum_p dY_p W_p
+  float* lowrank;  // [slot][T][r] X A_p and dY_p B_p^T
+  float* part;     // split sums of those products
 };
 
-// The adapter terms of dX for the epilogue (by value, a kernel argument).
-struct DxTerms {
-  int n;
-  const float* dl[kMaxProj];
-  const float* a[kMaxProj];
-  float scaling[kMaxProj];
+// Floats of each ProjLaunch scratch buffer for a forward or backward call.
+struct ProjScratchNeed {
+  long yf, dxf, lowrank, part;
 };
+ProjScratchNeed proj_scratch_need(const ProjLaunch& a, bool backward);
 
 // Enqueue on st; blas is a rocBLAS handle from create_blas_handle().
 hipError_t launch_proj_forward(const ProjLaunch& a, hipStream_t st, void* blas);

@@ -9,17 +9,23 @@
 //   forward   Y_p  = X W_p^T + bias_p + s_p (X A_p) B_p
 //   backward  dX   = sum_p dY_p W_p + s_p (dY_p B_p^T) A_p^T
 //             dA_p += s_p X^T (dY_p B_p^T),  dB_p += s_p (X A_p)^T dY_p
-// The base products (the only large ones) are rocBLAS GEMMs with fp32
-// results in scratch; everything of rank r is done here, fused into the
-// epilogues that add the deltas and write the caller's dtype:
-//   lora_down      L = X A             one wave per row, lanes over in
-//   proj_epilogue  Y = io(Yf + bias + s L B)
-//   lora_dl        dL = dY B^T         one wave per row, lanes over out
-//   lora_grad      partial column sums of X^T dL or L^T dY over token blocks
-//   lora_grad_sum  grad += s * (sum of the partials in block order)
-//   dx_epilogue    dX = io(dXf + sum_p s_p dL_p A_p^T)
-// Every sum has a fixed order (rocBLAS runs with atomics disallowed), so
-// results are bitwise repeatable.
+//
+// The base products X W_p^T and dY_p W_p are rocBLAS GEMMs with fp32
+// results.  Everything low-rank is here, each kernel taking every
+// projection of the call in one launch:
+//   lowrank_rows    L = X A_p and dL = dY_p B_p^T (output r columns wide,
+//                   reduction over in / out): 16-row slabs, the reduction
+//                   split over workgroups and over their 8 waves, fp32 MFMAs
+//   lowrank_reduce  adds the workgroups' split sums in split order
+//   lowrank_cols    grad_A += s X^T dL, grad_B += s L^T dY (reduction over
+//                   the tokens): 64-column slabs, tokens split over 8 waves
+//   lowrank_out     Y_p = io(Yf_p + bias_p + (s L) B_p) and dX = io(dXf +
+//                   sum_p (s dL_p) A_p^T): 16 x 256 tiles, the rank-r
+//                   product on MFMAs, fused with the dtype conversion
+// The adapters, the low-rank activations and the gradients stay fp32, as in
+// the reference (LoraAdapter.cs:23-24); bf16 tensors round only the base
+// operands and the outputs.  rocBLAS runs with atomics disallowed and every
+// reduction here has a fixed order, so every result is bitwise repeatable.
 #include "attn_common.hpp"
 #include "proj_launch.hpp"
 
@@ -28,264 +34,508 @@
 namespace glacier {
 namespace {
 
-constexpr int kProjThreads = 256;
-constexpr int kGradRows = 256;  // tokens per partial sum of the adapter gradients
+constexpr int kLrWaves = 8;  // waves of a rows/cols workgroup, splitting the reduction
+constexpr int kLrThreads = 64 * kLrWaves;
+constexpr int kOutThreads = 256;  // lowrank_out: 4 waves of 16 x 64
+constexpr int kMaxJobs = 2 * kMaxProj;
 
-template <typename IO>
-__device__ inline float ld(const IO* p) {
-  return to_f32(*p);
+__device__ inline void load4(const float* p, float (&x)[4]) {
+  const float4 a = *reinterpret_cast<const float4*>(p);
+  x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+}
+__device__ inline void load4(const bf16* p, float (&x)[4]) {
+  const bf16x4 v = *reinterpret_cast<const bf16x4*>(p);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) x[e] = (float)v[e];
 }
 
-// Sum over the 64 lanes of a wave in a fixed order (every lane gets it).
-__device__ inline float wave_sum(float x) {
-  x = lanes_sum<32>(x);
-  return x + __shfl_xor(x, 32);
+__device__ inline f32x4 mma_f32(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-// L[t][j] = sum_k X[t][k] A[k][j]; grid.x = rows / 4, 4 waves per block.
-// Lane l takes k = l, l + 64, ... in ascending order.
-template <typename IO>
-__global__ __launch_bounds__(kProjThreads) void lora_down_kernel(const IO* __restrict__ x,
-                                                                 const float* __restrict__ a,
-                                                                 float* __restrict__ lr, int T,
-                                                                 int in, int rank) {
-  const int t = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-  if (t >= T) return;
-  float acc[kMaxRank];
+// The [lo, hi) share of part p of n of a range [0, len), cut at multiples of g.
+__device__ inline void share(int len, int n, int p, int g, int& lo, int& hi) {
+  const int per = (len + n * g - 1) / (n * g) * g;
+  lo = min(len, p * per);
+  hi = min(len, lo + per);
+}
+
+// One product Out [T][r] = U [T][K] V of lowrank_rows: V = A [K][r] (vt 0)
+// or B^T with B [r][K] (vt 1); U in the call's dtype.
+struct RowsJob {
+  const void* u;
+  const float* v;
+  int K;
+  int vt;
+};
+struct RowsJobs {
+  RowsJob j[kMaxJobs];
+};
+
+// Workgroup (x, y, z): rows 16x.. of job z, split y of its K; wave w reduces
+// a contiguous slice of that split in steps of 16.  In a step lane (i = lane
+// % 16, q = lane / 16) loads U[row i][k0 + 4q .. +4] and, for MFMA e of the
+// step, supplies U[i][k0 + 4q + e] and V(k0 + 4q + e, 16 jt + i): each
+// MFMA's reduction index q maps to one k for both operands.  Lanes of rows
+// >= T or columns >= r read 0.  The workgroup's sums (waves added in order
+// through LDS) go to part[z][y][x][16][16 NT].
+template <typename IO, int NT>
+__global__ __launch_bounds__(kLrThreads) void lowrank_rows_kernel(RowsJobs jobs, int rows, int rank,
+                                                                  float* __restrict__ part) {
+  constexpr int CH = NT <= 2 ? 8 : 4;  // steps whose loads are issued together
+  constexpr int kOut = 16 * NT * 16;   // outputs of the workgroup
+  __shared__ float red[kLrWaves * kOut];
+  const RowsJob& job = jobs.j[blockIdx.z];
+  const IO* u = static_cast<const IO*>(job.u);
+  const float* v = job.v;
+  const int K = job.K;
+  const bool vt = job.vt != 0;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int i = lane & 15, q = lane >> 4;
+  const int t0 = blockIdx.x * 16;
+  const bool row_ok = t0 + i < rows;
+  const IO* urow = u + (long)(row_ok ? t0 + i : 0) * K;
+  int k_lo, k_hi, kb, ke;
+  share(K, gridDim.y, blockIdx.y, 16, k_lo, k_hi);
+  share(k_hi - k_lo, kLrWaves, wave, 16, kb, ke);
+  kb += k_lo;
+  ke += k_lo;
+  f32x4 acc[NT];
 #pragma unroll
-  for (int j = 0; j < kMaxRank; ++j) acc[j] = 0.0f;
-  const IO* row = x + (long)t * in;
-  for (int k = lane; k < in; k += 64) {
-    const float xv = ld(row + k);
-    const float* ar = a + (long)k * rank;
+  for (int jt = 0; jt < NT; ++jt) acc[jt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int k0 = kb; k0 < ke; k0 += 16 * CH) {
+    float x[CH][4], w[CH][NT][4];
 #pragma unroll
-    for (int j = 0; j < kMaxRank; ++j)
-      if (j < rank) acc[j] += xv * ar[j];
-  }
+    for (int s = 0; s < CH; ++s) {
+      const int k = k0 + 16 * s + 4 * q;  // K % 4 == 0: a 4-chunk is all in or all out
+      const bool k_ok = k < ke;
 #pragma unroll
-  for (int j = 0; j < kMaxRank; ++j) {
-    if (j < rank) {
-      const float v = wave_sum(acc[j]);
-      if (lane == 0) lr[(long)t * rank + j] = v;
+      for (int e = 0; e < 4; ++e) x[s][e] = 0.0f;
+      if (k_ok && row_ok) load4(urow + k, x[s]);
+#pragma unroll
+      for (int jt = 0; jt < NT; ++jt) {
+        const int j = 16 * jt + i;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w[s][jt][e] = 0.0f;
+        if (k_ok && j < rank) {
+          if (vt) {
+            load4(v + (long)j * K + k, w[s][jt]);
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) w[s][jt][e] = v[(long)(k + e) * rank + j];
+          }
+        }
+      }
     }
+#pragma unroll
+    for (int s = 0; s < CH; ++s)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int jt = 0; jt < NT; ++jt) acc[jt] = mma_f32(x[s][e], w[s][jt][e], acc[jt]);
+  }
+  // D of tile jt: lane (i, q), register c holds row 4q + c, column 16 jt + i.
+#pragma unroll
+  for (int jt = 0; jt < NT; ++jt)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) red[wave * kOut + (4 * q + c) * (16 * NT) + 16 * jt + i] = acc[jt][c];
+  __syncthreads();
+  float* mine = part + (((long)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * kOut;
+  for (int idx = threadIdx.x; idx < kOut; idx += kLrThreads) {
+    float sum = 0.0f;
+#pragma unroll
+    for (int wv = 0; wv < kLrWaves; ++wv) sum += red[wv * kOut + idx];
+    mine[idx] = sum;
   }
 }
 
-// dL[t][j] = sum_n dY[t][n] B[j][n]; lane l takes n = l, l + 64, ...
-template <typename IO>
-__global__ __launch_bounds__(kProjThreads) void lora_dl_kernel(const IO* __restrict__ dy,
-                                                               const float* __restrict__ b,
-                                                               float* __restrict__ dl, int T,
-                                                               int out, int rank) {
-  const int t = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-  if (t >= T) return;
-  float acc[kMaxRank];
-#pragma unroll
-  for (int j = 0; j < kMaxRank; ++j) acc[j] = 0.0f;
-  const IO* row = dy + (long)t * out;
-  for (int n = lane; n < out; n += 64) {
-    const float g = ld(row + n);
-#pragma unroll
-    for (int j = 0; j < kMaxRank; ++j)
-      if (j < rank) acc[j] += g * b[(long)j * out + n];
-  }
-#pragma unroll
-  for (int j = 0; j < kMaxRank; ++j) {
-    if (j < rank) {
-      const float v = wave_sum(acc[j]);
-      if (lane == 0) dl[(long)t * rank + j] = v;
-    }
-  }
-}
-
-// Y[t][n] = io(Yf[t][n] + bias[n] + sum_j (s L[t][j]) B[j][n]), 4 columns
-// per thread (out % 4 == 0), the terms added in the reference's order
-// (LoraAdapter.cs:141-150, LoraKernels.cs:103-112).
-template <typename IO>
-__global__ __launch_bounds__(kProjThreads) void proj_epilogue_kernel(
-    const float* __restrict__ yf, const float* __restrict__ bias, const float* __restrict__ lr,
-    const float* __restrict__ b, float scaling, IO* __restrict__ y, int T, int out, int rank) {
-  const long idx = (long)blockIdx.x * kProjThreads + threadIdx.x;
-  const int q4 = out / 4;
-  if (idx >= (long)T * q4) return;
-  const int t = (int)(idx / q4), n = 4 * (int)(idx % q4);
-  f32x4 v = *reinterpret_cast<const f32x4*>(yf + (long)t * out + n);
-  if (bias != nullptr) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] += bias[n + e];
-  }
-  if (lr != nullptr) {
-    for (int j = 0; j < rank; ++j) {
-      const float s = lr[(long)t * rank + j] * scaling;
-      const f32x4 bj = *reinterpret_cast<const f32x4*>(b + (long)j * out + n);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] += s * bj[e];
-    }
-  }
-  store4(y + (long)t * out + n, v);
-}
-
-// Partial sums P[c][j][col] = sum_{t in block c} U[t][col] V[t][j] over a
-// block of kGradRows tokens (ascending), for the adapter gradients:
-// grad_a: U = X [T][in],  V = dL [T][r];  grad_b: U = dY [T][out], V = L [T][r].
-// grid (ceil(cols / 256), blocks of tokens); one column per thread.
-template <typename IO>
-__global__ __launch_bounds__(kProjThreads) void lora_grad_kernel(const IO* __restrict__ u,
-                                                                 const float* __restrict__ v,
-                                                                 float* __restrict__ part, int T,
-                                                                 int cols, int rank) {
-  const int col = blockIdx.x * kProjThreads + threadIdx.x;
-  const int t0 = blockIdx.y * kGradRows, t1 = min(T, t0 + kGradRows);
-  if (col >= cols) return;
-  float acc[kMaxRank];
-#pragma unroll
-  for (int j = 0; j < kMaxRank; ++j) acc[j] = 0.0f;
-  for (int t = t0; t < t1; ++t) {
-    const float uv = ld(u + (long)t * cols + col);
-    const float* vr = v + (long)t * rank;
-#pragma unroll
-    for (int j = 0; j < kMaxRank; ++j)
-      if (j < rank) acc[j] += uv * vr[j];
-  }
-  float* pr = part + (long)blockIdx.y * rank * cols;
-#pragma unroll
-  for (int j = 0; j < kMaxRank; ++j)
-    if (j < rank) pr[(long)j * cols + col] = acc[j];
-}
-
-// grad[col][j] (transposed: grad_a is [in][r]) or grad[j][col] (grad_b is
-// [r][out]) += s * sum_c P[c][j][col], blocks in ascending order.
-__global__ __launch_bounds__(kProjThreads) void lora_grad_sum_kernel(
-    const float* __restrict__ part, int nblk, int cols, int rank, float scaling,
-    float* __restrict__ grad, int transposed) {
-  const long idx = (long)blockIdx.x * kProjThreads + threadIdx.x;
-  if (idx >= (long)cols * rank) return;
-  const int j = (int)(idx / cols), col = (int)(idx % cols);
+// dense[z][t][j] = sum over the splits s (ascending) of part[z][s][t / 16]
+// [t % 16][j], for every job z of a lowrank_rows launch.
+__global__ __launch_bounds__(256) void lowrank_reduce_kernel(const float* __restrict__ part,
+                                                             float* __restrict__ dense, int n_jobs,
+                                                             int splits, int slabs, int width,
+                                                             int T, int rank) {
+  const long idx = (long)blockIdx.x * 256 + threadIdx.x;
+  const long per_job = (long)T * rank;
+  if (idx >= n_jobs * per_job) return;
+  const int z = (int)(idx / per_job), t = (int)(idx % per_job / rank), j = (int)(idx % rank);
+  const long slab_floats = 16L * width;
+  const float* p = part + ((long)z * splits * slabs + t / 16) * slab_floats + (t % 16) * width + j;
   float sum = 0.0f;
-  for (int c = 0; c < nblk; ++c) sum += part[((long)c * rank + j) * cols + col];
-  float* g = transposed ? grad + (long)col * rank + j : grad + (long)j * cols + col;
-  *g += sum * scaling;
+  for (int s = 0; s < splits; ++s) sum += p[(long)s * slabs * slab_floats];
+  dense[idx] = sum;
 }
 
-// dX[t][k] = io(dXf[t][k] + sum_p s_p sum_j dL_p[t][j] A_p[k][j]), 4
-// columns per thread (in % 4 == 0), projections in order.
-template <typename IO>
-__global__ __launch_bounds__(kProjThreads) void dx_epilogue_kernel(const float* __restrict__ dxf,
-                                                                   DxTerms terms,
-                                                                   IO* __restrict__ dx, int T,
-                                                                   int in, int rank) {
-  const long idx = (long)blockIdx.x * kProjThreads + threadIdx.x;
-  const int q4 = in / 4;
-  if (idx >= (long)T * q4) return;
-  const int t = (int)(idx / q4), k = 4 * (int)(idx % q4);
-  f32x4 v = *reinterpret_cast<const f32x4*>(dxf + (long)t * in + k);
-  for (int p = 0; p < terms.n; ++p) {
-    const float* dl = terms.dl[p] + (long)t * rank;
-    const float* a = terms.a[p];
-    f32x4 dot = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int j = 0; j < rank; ++j) {
-      const float d = dl[j];
+// One product Out (+)= alpha U^T W of lowrank_cols: U [T][cols] in the call's
+// dtype, W [T][r] fp32; Out [cols][r] or, transposed, [r][cols];
+// workgroups first .. first + ceil(cols / 64) - 1.
+struct ColsJob {
+  const void* u;
+  const float* w;
+  float* out;
+  int cols;
+  float alpha;
+  int transposed;
+  int first;
+};
+struct ColsJobs {
+  ColsJob j[kMaxJobs];
+  int n;
+};
+
+// Workgroup: 64 columns of one job; wave w reduces a contiguous slice of the
+// tokens in steps of 4.  Lane (i, q) loads U[t0 + q][c0 + 4i .. +4]: element
+// e feeds tile e, whose row i is column c0 + 4i + e, with W[t0 + q][16 jt +
+// i] as the other operand.  The waves' sums are added in order through LDS.
+template <typename IO, int NT>
+__global__ __launch_bounds__(kLrThreads) void lowrank_cols_kernel(ColsJobs jobs, int T, int rank) {
+  constexpr int CH = 8;
+  constexpr int kPad = 17;  // LDS row stride: the 4 lane groups fall in different banks
+  __shared__ float red[kLrWaves * 64 * kPad];
+  int z = 0;
+  while (z + 1 < jobs.n && (int)blockIdx.x >= jobs.j[z + 1].first) ++z;
+  const ColsJob& job = jobs.j[z];
+  const IO* u = static_cast<const IO*>(job.u);
+  const float* w = job.w;
+  const int cols = job.cols;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int i = lane & 15, q = lane >> 4;
+  const int c0 = ((int)blockIdx.x - job.first) * 64;
+  const bool col_ok = c0 + 4 * i < cols;  // cols % 4 == 0
+  int tb, te;
+  share(T, kLrWaves, wave, 4, tb, te);
+  f32x4 acc[4][NT];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) dot[e] += d * a[(long)(k + e) * rank + j];
+  for (int e = 0; e < 4; ++e)
+#pragma unroll
+    for (int jt = 0; jt < NT; ++jt) acc[e][jt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int t0 = tb; t0 < te; t0 += 4 * CH) {
+    float x[CH][4], wv[CH][NT];
+#pragma unroll
+    for (int s = 0; s < CH; ++s) {
+      const int t = t0 + 4 * s + q;
+      const bool t_ok = t < te;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x[s][e] = 0.0f;
+      if (t_ok && col_ok) load4(u + (long)t * cols + c0 + 4 * i, x[s]);
+#pragma unroll
+      for (int jt = 0; jt < NT; ++jt) {
+        const int j = 16 * jt + i;
+        wv[s][jt] = t_ok && j < rank ? w[(long)t * rank + j] : 0.0f;
+      }
     }
 #pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] += dot[e] * terms.scaling[p];
+    for (int s = 0; s < CH; ++s)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int jt = 0; jt < NT; ++jt) acc[e][jt] = mma_f32(x[s][e], wv[s][jt], acc[e][jt]);
   }
-  store4(dx + (long)t * in + k, v);
+  // D of tile (e, jt): lane (i, q), register c holds column c0 + 4 (4q + c) +
+  // e, rank 16 jt + i.  One rank tile at a time through LDS.
+#pragma unroll
+  for (int jt = 0; jt < NT; ++jt) {
+    if (jt > 0) __syncthreads();
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) red[(wave * 64 + 4 * (4 * q + c) + e) * kPad + i] = acc[e][jt][c];
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < 64 * 16; idx += kLrThreads) {
+      // transposed output: consecutive threads take consecutive columns
+      const int cl = job.transposed ? idx % 64 : idx / 16, jl = job.transposed ? idx / 64 : idx % 16;
+      float sum = 0.0f;
+#pragma unroll
+      for (int wv2 = 0; wv2 < kLrWaves; ++wv2) sum += red[(wv2 * 64 + cl) * kPad + jl];
+      const int c = c0 + cl, j = 16 * jt + jl;
+      if (c < cols && j < rank) {
+        float* o = job.transposed ? job.out + (long)j * cols + c : job.out + (long)c * rank + j;
+        *o += job.alpha * sum;
+      }
+    }
+  }
+}
+
+// One output of lowrank_out: out [T][n] = io(base [T][n] + bias [n] + sum
+// over the terms of (s L [T][r]) V), V = B [r][n] (forward) or A^T with A
+// [n][r] (dX); workgroups first .. first + ceil(T / 16) ceil(n / 256) - 1.
+struct OutJob {
+  const float* base;
+  const float* bias;  // or null
+  void* out;
+  int n;
+  int n_terms;
+  int first;
+  const float* l[kMaxProj];
+  const float* v[kMaxProj];
+  float s[kMaxProj];
+};
+struct OutJobs {
+  OutJob j[kMaxProj];
+  int n;
+};
+
+// Workgroup: 16 tokens x 256 columns of one output, wave w the columns 64w..
+// of those.  Lane (i, q) owns columns col = n0 + 4i .. +4: tile e's column i
+// is n0 + 4i + e, so that register c of the 4 tiles holds out[t0 + 4q +
+// c][col .. col + 4], and the MFMA reduction index q is rank 4m + q.
+template <typename IO, bool AT>
+__global__ __launch_bounds__(kOutThreads) void lowrank_out_kernel(OutJobs jobs, int T, int rank) {
+  int z = 0;
+  while (z + 1 < jobs.n && (int)blockIdx.x >= jobs.j[z + 1].first) ++z;
+  const OutJob& job = jobs.j[z];
+  const int n = job.n;
+  const int b = (int)blockIdx.x - job.first, ncb = (n + 255) / 256;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int i = lane & 15, q = lane >> 4;
+  const int t0 = (b / ncb) * 16, col = (b % ncb) * 256 + 64 * wave + 4 * i;
+  const bool col_ok = col < n;  // n % 4 == 0
+  f32x4 base[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int t = t0 + 4 * q + c;
+    base[c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    if (t < T && col_ok) base[c] = *reinterpret_cast<const f32x4*>(job.base + (long)t * n + col);
+  }
+  f32x4 acc[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) acc[e] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  const bool row_ok = t0 + i < T;
+  for (int term = 0; term < job.n_terms; ++term) {
+    const float* L = job.l[term];
+    const float* V = job.v[term];
+    const float s = job.s[term];
+    for (int m0 = 0; m0 < rank; m0 += 16) {  // 4 MFMA steps of 4 ranks, loads first
+      float a[4], bv[4][4];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const int j = m0 + 4 * m + q;
+        a[m] = j < rank && row_ok ? s * L[(long)(t0 + i) * rank + j] : 0.0f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) bv[m][e] = 0.0f;
+        if (j < rank && col_ok) {
+          if constexpr (AT) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) bv[m][e] = V[(long)(col + e) * rank + j];
+          } else {
+            load4(V + (long)j * n + col, bv[m]);
+          }
+        }
+      }
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[e] = mma_f32(a[m], bv[m][e], acc[e]);
+    }
+  }
+  if (!col_ok) return;
+  f32x4 bias = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  if (job.bias != nullptr) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) bias[e] = job.bias[col + e];
+  }
+  IO* out = static_cast<IO*>(job.out);
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int t = t0 + 4 * q + c;
+    if (t >= T) continue;
+    f32x4 y;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) y[e] = base[c][e] + bias[e] + acc[e][c];
+    store4(out + (long)t * n + col, y);
+  }
 }
 
 unsigned blocks(long n, int per) { return static_cast<unsigned>((n + per - 1) / per); }
 
-rocblas_status gemm(rocblas_handle h, bool bf16, rocblas_operation ta, rocblas_operation tb, int m,
-                    int n, int k, const void* a, int lda, const void* b, int ldb, float beta,
-                    float* c, int ldc) {
-  const float alpha = 1.0f;
-  const rocblas_datatype in_t = bf16 ? rocblas_datatype_bf16_r : rocblas_datatype_f32_r;
-  return rocblas_gemm_ex(h, ta, tb, m, n, k, &alpha, a, in_t, lda, b, in_t, ldb, &beta, c,
-                         rocblas_datatype_f32_r, ldc, c, rocblas_datatype_f32_r, ldc,
-                         rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0,
-                         rocblas_gemm_flags_none);
+// Row-major C [M x N] = alpha op(A) [M x K] op(B) [K x N] + beta C, as the
+// column-major C^T = op(B)^T op(A)^T (leading dimensions are row strides).
+rocblas_status gemm_rm(rocblas_handle h, bool bf16_in, bool ta, bool tb, int M, int N, int K,
+                       float alpha, const void* A, int lda, const void* B, int ldb, float beta,
+                       float* C, int ldc) {
+  const rocblas_datatype in_t = bf16_in ? rocblas_datatype_bf16_r : rocblas_datatype_f32_r;
+  return rocblas_gemm_ex(h, tb ? rocblas_operation_transpose : rocblas_operation_none,
+                         ta ? rocblas_operation_transpose : rocblas_operation_none, N, M, K,
+                         &alpha, B, in_t, ldb, A, in_t, lda, &beta, C, rocblas_datatype_f32_r, ldc,
+                         C, rocblas_datatype_f32_r, ldc, rocblas_datatype_f32_r,
+                         rocblas_gemm_algo_standard, 0, rocblas_gemm_flags_none);
 }
 
-#define PROJ_CHECK_BLAS(expr)                                   \
-  do {                                                          \
+#define PROJ_CHECK_BLAS(expr)                                           \
+  do {                                                                  \
     if ((expr) != rocblas_status_success) return hipErrorLaunchFailure; \
   } while (0)
+
+// The low-rank products X A_p / dY_p B_p^T of a call: which are needed, and
+// where their results go (slot z of ProjLaunch::lowrank, [T][r] each).
+struct RowsPlan {
+  RowsJobs jobs{};
+  int n = 0, kmax = 0;
+  int slot_l[kMaxProj], slot_dl[kMaxProj];  // -1: not computed
+};
+
+RowsPlan rows_plan(const ProjLaunch& a, bool backward) {
+  RowsPlan plan;
+  for (int p = 0; p < a.n_proj; ++p) {
+    const ProjSpec& s = a.p[p];
+    plan.slot_l[p] = plan.slot_dl[p] = -1;
+    if (s.a == nullptr) continue;
+    if (backward) {
+      plan.slot_dl[p] = plan.n;
+      plan.jobs.j[plan.n++] = RowsJob{s.dy, s.b, s.out, 1};
+      plan.kmax = std::max(plan.kmax, s.out);
+    }
+    if (!backward || s.grad_b != nullptr) {
+      plan.slot_l[p] = plan.n;
+      plan.jobs.j[plan.n++] = RowsJob{a.x, s.a, a.in, 0};
+      plan.kmax = std::max(plan.kmax, a.in);
+    }
+  }
+  return plan;
+}
+
+// Workgroups splitting each reduction of lowrank_rows: about 512 workgroups
+// in all, at least 128 reduction elements per split.
+int rows_splits(const ProjLaunch& a, const RowsPlan& plan) {
+  const int slabs = (a.T + 15) / 16, per = std::max(1, slabs * plan.n);
+  return std::max(1, std::min({(512 + per - 1) / per, plan.kmax / 128, 16}));
+}
+
+template <typename IO>
+hipError_t run_rows(const ProjLaunch& a, const RowsPlan& plan, hipStream_t st) {
+  if (plan.n == 0) return hipSuccess;
+  const int slabs = (a.T + 15) / 16, splits = rows_splits(a, plan), nt = (a.rank + 15) / 16;
+  const dim3 grid(slabs, splits, plan.n), block(kLrThreads);
+  switch (nt) {
+#define GL_ROWS(NT) \
+  hipLaunchKernelGGL((lowrank_rows_kernel<IO, NT>), grid, block, 0, st, plan.jobs, a.T, a.rank, a.part)
+    case 1: GL_ROWS(1); break;
+    case 2: GL_ROWS(2); break;
+    case 3: GL_ROWS(3); break;
+    case 4: GL_ROWS(4); break;
+#undef GL_ROWS
+    default: return hipErrorInvalidValue;
+  }
+  GL_CHECK(hipGetLastError());
+  const long n = (long)plan.n * a.T * a.rank;
+  hipLaunchKernelGGL(lowrank_reduce_kernel, dim3(blocks(n, 256)), dim3(256), 0, st, a.part,
+                     a.lowrank, plan.n, splits, slabs, 16 * nt, a.T, a.rank);
+  return hipGetLastError();
+}
+
+template <typename IO, bool AT>
+hipError_t run_out(const ProjLaunch& a, OutJobs& jobs, hipStream_t st) {
+  int total = 0;
+  for (int z = 0; z < jobs.n; ++z) {
+    jobs.j[z].first = total;
+    total += ((a.T + 15) / 16) * ((jobs.j[z].n + 255) / 256);
+  }
+  hipLaunchKernelGGL((lowrank_out_kernel<IO, AT>), dim3(total), dim3(kOutThreads), 0, st, jobs, a.T,
+                     a.rank);
+  return hipGetLastError();
+}
+
+const float* slot(const ProjLaunch& a, int z) { return a.lowrank + (long)z * a.T * a.rank; }
 
 template <typename IO>
 hipError_t forward_impl(const ProjLaunch& a, hipStream_t st, rocblas_handle h) {
   constexpr bool BF = sizeof(IO) == 2;
-  const IO* x = static_cast<const IO*>(a.x);
+  long off = 0;
+  OutJobs out{};
+  out.n = a.n_proj;
   for (int p = 0; p < a.n_proj; ++p) {
     const ProjSpec& s = a.p[p];
-    // Yf = X W^T: column-major Yf^T [out x T] = W (W^T stored) x X^T
-    PROJ_CHECK_BLAS(gemm(h, BF, rocblas_operation_transpose, rocblas_operation_none, s.out, a.T,
-                         a.in, s.w, a.in, a.x, a.in, 0.0f, a.yf, s.out));
-    const bool lora = s.a != nullptr;
-    if (lora) {
-      hipLaunchKernelGGL(lora_down_kernel<IO>, dim3(blocks(a.T, 4)), dim3(kProjThreads), 0, st, x,
-                         s.a, a.lr, a.T, a.in, a.rank);
-      GL_CHECK(hipGetLastError());
-    }
-    hipLaunchKernelGGL(proj_epilogue_kernel<IO>, dim3(blocks((long)a.T * (s.out / 4), kProjThreads)),
-                       dim3(kProjThreads), 0, st, a.yf, s.bias, lora ? a.lr : nullptr, s.b,
-                       s.scaling, static_cast<IO*>(s.y), a.T, s.out, a.rank);
-    GL_CHECK(hipGetLastError());
+    // Yf_p = X W_p^T
+    PROJ_CHECK_BLAS(gemm_rm(h, BF, false, true, a.T, s.out, a.in, 1.0f, a.x, a.in, s.w, a.in,
+                            0.0f, a.yf + off, s.out));
+    out.j[p] = OutJob{a.yf + off, s.bias, s.y, s.out, 0, 0, {}, {}, {}};
+    off += (long)a.T * s.out;
   }
-  return hipSuccess;
+  const RowsPlan plan = rows_plan(a, false);
+  GL_CHECK(run_rows<IO>(a, plan, st));  // L_p = X A_p
+  for (int p = 0; p < a.n_proj; ++p) {
+    if (plan.slot_l[p] < 0) continue;
+    OutJob& o = out.j[p];
+    o.n_terms = 1;
+    o.l[0] = slot(a, plan.slot_l[p]);
+    o.v[0] = a.p[p].b;
+    o.s[0] = a.p[p].scaling;
+  }
+  return run_out<IO, false>(a, out, st);  // Y_p = io(Yf_p + bias_p + (s L_p) B_p)
 }
 
 template <typename IO>
 hipError_t backward_impl(const ProjLaunch& a, hipStream_t st, rocblas_handle h) {
   constexpr bool BF = sizeof(IO) == 2;
-  const IO* x = static_cast<const IO*>(a.x);
-  const int nblk = (a.T + kGradRows - 1) / kGradRows;
-  DxTerms terms{};
+  // dXf = sum_p dY_p W_p
   for (int p = 0; p < a.n_proj; ++p) {
     const ProjSpec& s = a.p[p];
-    // dXf (+)= dY W: column-major dXf^T [in x T] = W^T (W stored) x dY^T
-    PROJ_CHECK_BLAS(gemm(h, BF, rocblas_operation_none, rocblas_operation_none, a.in, a.T, s.out,
-                         s.w, a.in, s.dy, s.out, p == 0 ? 0.0f : 1.0f, a.dxf, a.in));
-    if (s.a == nullptr) continue;
-    const IO* dy = static_cast<const IO*>(s.dy);
-    float* dl = a.dl + (long)p * a.T * a.rank;
-    hipLaunchKernelGGL(lora_dl_kernel<IO>, dim3(blocks(a.T, 4)), dim3(kProjThreads), 0, st, dy, s.b,
-                       dl, a.T, s.out, a.rank);
-    GL_CHECK(hipGetLastError());
-    if (s.grad_b != nullptr) {
-      hipLaunchKernelGGL(lora_down_kernel<IO>, dim3(blocks(a.T, 4)), dim3(kProjThreads), 0, st, x,
-                         s.a, a.lr, a.T, a.in, a.rank);
-      GL_CHECK(hipGetLastError());
-      hipLaunchKernelGGL(lora_grad_kernel<IO>, dim3(blocks(s.out, kProjThreads), nblk),
-                         dim3(kProjThreads), 0, st, dy, a.lr, a.part, a.T, s.out, a.rank);
-      GL_CHECK(hipGetLastError());
-      hipLaunchKernelGGL(lora_grad_sum_kernel, dim3(blocks((long)s.out * a.rank, kProjThreads)),
-                         dim3(kProjThreads), 0, st, a.part, nblk, s.out, a.rank, s.scaling,
-                         s.grad_b, 0);
-      GL_CHECK(hipGetLastError());
-    }
-    if (s.grad_a != nullptr) {
-      hipLaunchKernelGGL(lora_grad_kernel<IO>, dim3(blocks(a.in, kProjThreads), nblk),
-                         dim3(kProjThreads), 0, st, x, dl, a.part, a.T, a.in, a.rank);
-      GL_CHECK(hipGetLastError());
-      hipLaunchKernelGGL(lora_grad_sum_kernel, dim3(blocks((long)a.in * a.rank, kProjThreads)),
-                         dim3(kProjThreads), 0, st, a.part, nblk, a.in, a.rank, s.scaling,
-                         s.grad_a, 1);
-      GL_CHECK(hipGetLastError());
-    }
-    terms.dl[terms.n] = dl;
-    terms.a[terms.n] = s.a;
-    terms.scaling[terms.n] = s.scaling;
-    ++terms.n;
+    PROJ_CHECK_BLAS(gemm_rm(h, BF, false, false, a.T, a.in, s.out, 1.0f, s.dy, s.out, s.w, a.in,
+                            p == 0 ? 0.0f : 1.0f, a.dxf, a.in));
   }
-  hipLaunchKernelGGL(dx_epilogue_kernel<IO>, dim3(blocks((long)a.T * (a.in / 4), kProjThreads)),
-                     dim3(kProjThreads), 0, st, a.dxf, terms, static_cast<IO*>(a.dx), a.T, a.in,
-                     a.rank);
-  GL_CHECK(hipGetLastError());
-  return hipSuccess;
+  // dL_p = dY_p B_p^T, and L_p = X A_p where grad_B_p is wanted
+  const RowsPlan plan = rows_plan(a, true);
+  GL_CHECK(run_rows<IO>(a, plan, st));
+  // grad_A_p += s X^T dL_p;  grad_B_p += s L_p^T dY_p
+  ColsJobs cj{};
+  int total = 0;
+  for (int p = 0; p < a.n_proj; ++p) {
+    const ProjSpec& s = a.p[p];
+    if (s.a == nullptr) continue;
+    if (s.grad_a != nullptr) {
+      cj.j[cj.n++] = ColsJob{a.x, slot(a, plan.slot_dl[p]), s.grad_a, a.in, s.scaling, 0, total};
+      total += (a.in + 63) / 64;
+    }
+    if (s.grad_b != nullptr) {
+      cj.j[cj.n++] = ColsJob{s.dy, slot(a, plan.slot_l[p]), s.grad_b, s.out, s.scaling, 1, total};
+      total += (s.out + 63) / 64;
+    }
+  }
+  if (cj.n > 0) {
+    switch ((a.rank + 15) / 16) {
+#define GL_COLS(NT) \
+  hipLaunchKernelGGL((lowrank_cols_kernel<IO, NT>), dim3(total), dim3(kLrThreads), 0, st, cj, a.T, a.rank)
+      case 1: GL_COLS(1); break;
+      case 2: GL_COLS(2); break;
+      case 3: GL_COLS(3); break;
+      case 4: GL_COLS(4); break;
+#undef GL_COLS
+      default: return hipErrorInvalidValue;
+    }
+    GL_CHECK(hipGetLastError());
+  }
+  // dX = io(dXf + sum_p (s dL_p) A_p^T)
+  OutJobs out{};
+  out.n = 1;
+  OutJob& o = out.j[0];
+  o = OutJob{a.dxf, nullptr, a.dx, a.in, 0, 0, {}, {}, {}};
+  for (int p = 0; p < a.n_proj; ++p) {
+    if (plan.slot_dl[p] < 0) continue;
+    o.l[o.n_terms] = slot(a, plan.slot_dl[p]);
+    o.v[o.n_terms] = a.p[p].a;
+    o.s[o.n_terms] = a.p[p].scaling;
+    ++o.n_terms;
+  }
+  return run_out<IO, true>(a, out, st);
 }
 
 }  // namespace
+
+ProjScratchNeed proj_scratch_need(const ProjLaunch& a, bool backward) {
+  ProjScratchNeed need{};
+  if (backward) {
+    need.dxf = (long)a.T * a.in;
+  } else {
+    for (int p = 0; p < a.n_proj; ++p) need.yf += (long)a.T * a.p[p].out;
+  }
+  const RowsPlan plan = rows_plan(a, backward);
+  if (plan.n > 0) {
+    const long slabs = (a.T + 15) / 16, nt = (a.rank + 15) / 16;
+    need.lowrank = (long)plan.n * a.T * a.rank;
+    need.part = (long)plan.n * rows_splits(a, plan) * slabs * 256 * nt;
+  }
+  return need;
+}
 
 hipError_t launch_proj_forward(const ProjLaunch& a, hipStream_t st, void* blas) {
   auto h = static_cast<rocblas_handle>(blas);

@@ -104,25 +104,27 @@ def test_python_front_end_rejects_wrong_host_arrays():
 
 
 def _proj_rc(T=8, n_in=16, outs=(8,), rank=4, prec=ga.PREC_BF16, io=ga.IO_BF16, lora=True,
-             n_proj=None, backward=False):
+             n_proj=None, backward=False, misaligned=()):
     L = ga.load()
     desc = ga.ProjDesc(T, n_in, rank, prec, io)
     arr = (ga.LoraProj * max(len(outs), 1))()
-    dummy = 16  # any non-null address: validation fails before it is used
+    # any non-null address: validation fails before it is used (8 for the
+    # tensors named in misaligned)
+    addr = lambda name: 8 if name in misaligned else 16
     for i, o in enumerate(outs):
-        arr[i].w = dummy
+        arr[i].w = addr("w")
         arr[i].out_features = o
-        arr[i].y = dummy
-        arr[i].dy = dummy
+        arr[i].y = addr("y")
+        arr[i].dy = addr("dy")
         arr[i].scaling = 2.0
         if lora:
-            arr[i].lora_a = dummy
-            arr[i].lora_b = dummy
+            arr[i].lora_a = addr("lora_a")
+            arr[i].lora_b = addr("lora_b")
     n = len(outs) if n_proj is None else n_proj
     if backward:
-        rc = L.glacier_proj_backward(None, ctypes.byref(desc), dummy, arr, n, dummy)
+        rc = L.glacier_proj_backward(None, ctypes.byref(desc), addr("x"), arr, n, addr("dx"))
     else:
-        rc = L.glacier_proj_forward(None, ctypes.byref(desc), dummy, arr, n)
+        rc = L.glacier_proj_forward(None, ctypes.byref(desc), addr("x"), arr, n)
     return rc, L.glacier_attn_last_error().decode()
 
 
@@ -145,6 +147,12 @@ def test_projection_argument_errors_come_before_any_device_work():
     assert rc == ga.ERR_UNSUPPORTED and "multiple of 4" in msg
     rc, msg = _proj_rc(T=-1)
     assert rc == ga.ERR_INVALID_ARGUMENT and "total_tokens" in msg
+    for name, backward in (("x", False), ("y", False), ("lora_b", False), ("dy", True)):
+        rc, msg = _proj_rc(misaligned=(name,), backward=backward)
+        assert rc == ga.ERR_UNSUPPORTED and "16-byte aligned" in msg and name in msg, name
+    # unused by the call: not checked
+    rc, msg = _proj_rc(misaligned=("dy",))
+    assert rc == ga.ERR_INVALID_ARGUMENT and "ctx" in msg
     # no adapter: the rank is not checked; a valid call then needs the context
     rc, msg = _proj_rc(rank=0, lora=False)
     assert rc == ga.ERR_INVALID_ARGUMENT and "ctx" in msg

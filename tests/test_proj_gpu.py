@@ -93,6 +93,8 @@ def _oracle(x, projs, rank):
 SHAPES = {  # T, in, (q, k, v outs), rank
     "qwen05b_t256": (256, 896, (896, 128, 128), 8),
     "ragged_t37": (37, 96, (64, 32, 32), 4),
+    "r40_t70": (70, 192, (128, 64, 64), 40),  # 3 rank tiles, the last one partial
+    "r64_t50": (50, 256, (64, 32, 128), 64),  # the largest rank
 }
 
 
