@@ -532,13 +532,14 @@ ProjLaunch proj_launch_of(const glacier_proj_desc* desc, const void* x, const gl
   for (int p = 0; p < n_proj; ++p)
     if (proj[p].out_features % 4 != 0)
       fail(GLACIER_ATTN_ERR_UNSUPPORTED, "out_features must be a multiple of 4");
-  // the kernels move 4 consecutive elements of x, y, dy, dx and lora_b at once
+  // the kernels move 4 consecutive elements of x, y, dy, dx and the adapters at once
   if (!aligned16(x)) fail(GLACIER_ATTN_ERR_UNSUPPORTED, "x must be 16-byte aligned");
   for (int p = 0; p < n_proj; ++p)
-    if (!aligned16(backward ? proj[p].dy : proj[p].y) || !aligned16(proj[p].lora_b))
+    if (!aligned16(backward ? proj[p].dy : proj[p].y) || !aligned16(proj[p].lora_a) ||
+        !aligned16(proj[p].lora_b))
       fail(GLACIER_ATTN_ERR_UNSUPPORTED,
            "proj[" + std::to_string(p) + "]." + (backward ? "dy" : "y") +
-               " and .lora_b must be 16-byte aligned");
+               ", .lora_a and .lora_b must be 16-byte aligned");
   if ((long long)d.total_tokens * std::max(d.in_features, 1) >= (1LL << 31))
     fail(GLACIER_ATTN_ERR_UNSUPPORTED, "tensor too large");
   for (int p = 0; p < n_proj; ++p)

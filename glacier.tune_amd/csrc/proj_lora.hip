@@ -43,10 +43,37 @@ __device__ inline void load4(const float* p, float (&x)[4]) {
   const float4 a = *reinterpret_cast<const float4*>(p);
   x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
 }
-__device__ inline void load4(const bf16* p, float (&x)[4]) {
-  const bf16x4 v = *reinterpret_cast<const bf16x4*>(p);
+
+// 4 consecutive elements as loaded, converted (or zeroed) only when used:
+// every load of a step is issued at an in-bounds (clamped) address before any
+// value is used, and out-of-range values of ONE operand of each product are
+// zeroed afterwards; the other operand's clamped values then meet zeros, or
+// reach only outputs that are not stored.  (A load under a condition makes
+// the wave wait for each load in turn; so would a select on both operands,
+// which the compiler turns back into conditional loads.)
+template <typename IO>
+struct Raw4;
+template <>
+struct Raw4<float> {
+  using T = float4;
+};
+template <>
+struct Raw4<bf16> {
+  using T = bf16x4;
+};
+template <typename IO>
+__device__ inline typename Raw4<IO>::T ld_raw4(const IO* p) {
+  return *reinterpret_cast<const typename Raw4<IO>::T*>(p);
+}
+__device__ inline void sel4(float4 r, bool ok, float (&x)[4]) {
+  x[0] = ok ? r.x : 0.0f;
+  x[1] = ok ? r.y : 0.0f;
+  x[2] = ok ? r.z : 0.0f;
+  x[3] = ok ? r.w : 0.0f;
+}
+__device__ inline void sel4(bf16x4 r, bool ok, float (&x)[4]) {
 #pragma unroll
-  for (int e = 0; e < 4; ++e) x[e] = (float)v[e];
+  for (int e = 0; e < 4; ++e) x[e] = ok ? (float)r[e] : 0.0f;
 }
 
 __device__ inline f32x4 mma_f32(float a, float b, f32x4 c) {
@@ -72,68 +99,76 @@ struct RowsJobs {
   RowsJob j[kMaxJobs];
 };
 
-// Workgroup (x, y, z): rows 16x.. of job z, split y of its K; wave w reduces
-// a contiguous slice of that split in steps of 16.  In a step lane (i = lane
-// % 16, q = lane / 16) loads U[row i][k0 + 4q .. +4] and, for MFMA e of the
-// step, supplies U[i][k0 + 4q + e] and V(k0 + 4q + e, 16 jt + i): each
-// MFMA's reduction index q maps to one k for both operands.  Lanes of rows
-// >= T or columns >= r read 0.  The workgroup's sums (waves added in order
-// through LDS) go to part[z][y][x][16][16 NT].
-template <typename IO, int NT>
-__global__ __launch_bounds__(kLrThreads) void lowrank_rows_kernel(RowsJobs jobs, int rows, int rank,
-                                                                  float* __restrict__ part) {
+// The k range [kb, ke) of one wave of lowrank_rows_kernel, added into acc.
+// In a step of 16 lane (i = lane % 16, q = lane / 16) loads U[row i][k0 + 4q
+// .. +4] and, for MFMA e of the step, supplies U[i][k0 + 4q + e] and V(k0 +
+// 4q + e, 16 jt + i): each MFMA's reduction index q maps to one k for both
+// operands.  U is zeroed for k past the slice and for rows >= T.
+template <typename IO, int NT, bool VT>
+__device__ inline void rows_accumulate(const IO* __restrict__ urow, bool row_ok,
+                                       const float* __restrict__ v, int K, int rank, int kb, int ke,
+                                       f32x4 (&acc)[NT]) {
   constexpr int CH = NT <= 2 ? 8 : 4;  // steps whose loads are issued together
-  constexpr int kOut = 16 * NT * 16;   // outputs of the workgroup
-  __shared__ float red[kLrWaves * kOut];
-  const RowsJob& job = jobs.j[blockIdx.z];
-  const IO* u = static_cast<const IO*>(job.u);
-  const float* v = job.v;
-  const int K = job.K;
-  const bool vt = job.vt != 0;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int i = lane & 15, q = lane >> 4;
-  const int t0 = blockIdx.x * 16;
-  const bool row_ok = t0 + i < rows;
-  const IO* urow = u + (long)(row_ok ? t0 + i : 0) * K;
-  int k_lo, k_hi, kb, ke;
-  share(K, gridDim.y, blockIdx.y, 16, k_lo, k_hi);
-  share(k_hi - k_lo, kLrWaves, wave, 16, kb, ke);
-  kb += k_lo;
-  ke += k_lo;
-  f32x4 acc[NT];
-#pragma unroll
-  for (int jt = 0; jt < NT; ++jt) acc[jt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  const int lane = threadIdx.x & 63, i = lane & 15, q = lane >> 4;
   for (int k0 = kb; k0 < ke; k0 += 16 * CH) {
-    float x[CH][4], w[CH][NT][4];
+    typename Raw4<IO>::T xr[CH];
+    float w[CH][NT][4];
 #pragma unroll
     for (int s = 0; s < CH; ++s) {
-      const int k = k0 + 16 * s + 4 * q;  // K % 4 == 0: a 4-chunk is all in or all out
-      const bool k_ok = k < ke;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) x[s][e] = 0.0f;
-      if (k_ok && row_ok) load4(urow + k, x[s]);
+      if (k0 + 16 * s >= ke) break;  // the wave's slice ends (uniform)
+      const int kc = min(k0 + 16 * s + 4 * q, K - 4);  // K % 4 == 0
+      xr[s] = ld_raw4(urow + kc);
 #pragma unroll
       for (int jt = 0; jt < NT; ++jt) {
-        const int j = 16 * jt + i;
+        const int jc = min(16 * jt + i, rank - 1);
+        if constexpr (VT) {
+          const float4 r = *reinterpret_cast<const float4*>(v + (long)jc * K + kc);
+          w[s][jt][0] = r.x; w[s][jt][1] = r.y; w[s][jt][2] = r.z; w[s][jt][3] = r.w;
+        } else {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) w[s][jt][e] = 0.0f;
-        if (k_ok && j < rank) {
-          if (vt) {
-            load4(v + (long)j * K + k, w[s][jt]);
-          } else {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) w[s][jt][e] = v[(long)(k + e) * rank + j];
-          }
+          for (int e = 0; e < 4; ++e) w[s][jt][e] = v[(long)(kc + e) * rank + jc];
         }
       }
     }
 #pragma unroll
-    for (int s = 0; s < CH; ++s)
+    for (int s = 0; s < CH; ++s) {
+      if (k0 + 16 * s >= ke) break;
+      const bool k_ok = k0 + 16 * s + 4 * q < ke;  // a 4-chunk is all in or all out
+      float x[4];
+      sel4(xr[s], k_ok && row_ok, x);
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
+      for (int jt = 0; jt < NT; ++jt)
 #pragma unroll
-        for (int jt = 0; jt < NT; ++jt) acc[jt] = mma_f32(x[s][e], w[s][jt][e], acc[jt]);
+        for (int e = 0; e < 4; ++e) acc[jt] = mma_f32(x[e], w[s][jt][e], acc[jt]);
+    }
   }
+}
+
+// Workgroup (x, y, z): rows 16x.. of job z, split y of its K; wave w reduces
+// a contiguous slice of that split (rows_accumulate).  The workgroup's sums
+// (waves added in order through LDS) go to part[z][y][x][16][16 NT].
+template <typename IO, int NT>
+__global__ __launch_bounds__(kLrThreads) void lowrank_rows_kernel(RowsJobs jobs, int rows, int rank,
+                                                                  float* __restrict__ part) {
+  constexpr int kOut = 16 * NT * 16;  // outputs of the workgroup
+  __shared__ float red[kLrWaves * kOut];
+  const RowsJob& job = jobs.j[blockIdx.z];
+  const int K = job.K;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int i = lane & 15, q = lane >> 4;
+  const int t0 = blockIdx.x * 16;
+  const bool row_ok = t0 + i < rows;
+  const IO* urow = static_cast<const IO*>(job.u) + (long)(row_ok ? t0 + i : 0) * K;
+  int k_lo, k_hi, kb, ke;
+  share(K, gridDim.y, blockIdx.y, 16, k_lo, k_hi);
+  share(k_hi - k_lo, kLrWaves, wave, 16, kb, ke);
+  f32x4 acc[NT];
+#pragma unroll
+  for (int jt = 0; jt < NT; ++jt) acc[jt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  if (job.vt)
+    rows_accumulate<IO, NT, true>(urow, row_ok, job.v, K, rank, k_lo + kb, k_lo + ke, acc);
+  else
+    rows_accumulate<IO, NT, false>(urow, row_ok, job.v, K, rank, k_lo + kb, k_lo + ke, acc);
   // D of tile jt: lane (i, q), register c holds row 4q + c, column 16 jt + i.
 #pragma unroll
   for (int jt = 0; jt < NT; ++jt)
@@ -198,7 +233,7 @@ __global__ __launch_bounds__(kLrThreads) void lowrank_cols_kernel(ColsJobs jobs,
   const IO* u = static_cast<const IO*>(job.u);
   const float* w = job.w;
   const int cols = job.cols;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int i = lane & 15, q = lane >> 4;
   const int c0 = ((int)blockIdx.x - job.first) * 64;
   const bool col_ok = c0 + 4 * i < cols;  // cols % 4 == 0
@@ -209,27 +244,29 @@ __global__ __launch_bounds__(kLrThreads) void lowrank_cols_kernel(ColsJobs jobs,
   for (int e = 0; e < 4; ++e)
 #pragma unroll
     for (int jt = 0; jt < NT; ++jt) acc[e][jt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  const IO* ucol = u + min(c0 + 4 * i, cols - 4);
   for (int t0 = tb; t0 < te; t0 += 4 * CH) {
-    float x[CH][4], wv[CH][NT];
+    typename Raw4<IO>::T xr[CH];
+    float wv[CH][NT];
 #pragma unroll
     for (int s = 0; s < CH; ++s) {
-      const int t = t0 + 4 * s + q;
-      const bool t_ok = t < te;
+      if (t0 + 4 * s >= te) break;  // the wave's slice ends (uniform)
+      const int tc = min(t0 + 4 * s + q, T - 1);
+      xr[s] = ld_raw4(ucol + (long)tc * cols);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) x[s][e] = 0.0f;
-      if (t_ok && col_ok) load4(u + (long)t * cols + c0 + 4 * i, x[s]);
-#pragma unroll
-      for (int jt = 0; jt < NT; ++jt) {
-        const int j = 16 * jt + i;
-        wv[s][jt] = t_ok && j < rank ? w[(long)t * rank + j] : 0.0f;
-      }
+      for (int jt = 0; jt < NT; ++jt) wv[s][jt] = w[(long)tc * rank + min(16 * jt + i, rank - 1)];
     }
 #pragma unroll
-    for (int s = 0; s < CH; ++s)
+    for (int s = 0; s < CH; ++s) {
+      if (t0 + 4 * s >= te) break;
+      const bool t_ok = t0 + 4 * s + q < te;
+      float x[4];
+      sel4(xr[s], t_ok && col_ok, x);
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
+      for (int jt = 0; jt < NT; ++jt)
 #pragma unroll
-        for (int jt = 0; jt < NT; ++jt) acc[e][jt] = mma_f32(x[s][e], wv[s][jt], acc[e][jt]);
+        for (int e = 0; e < 4; ++e) acc[e][jt] = mma_f32(x[e], wv[s][jt], acc[e][jt]);
+    }
   }
   // D of tile (e, jt): lane (i, q), register c holds column c0 + 4 (4q + c) +
   // e, rank 16 jt + i.  One rank tile at a time through LDS.
@@ -278,50 +315,63 @@ struct OutJobs {
 // Workgroup: 16 tokens x 256 columns of one output, wave w the columns 64w..
 // of those.  Lane (i, q) owns columns col = n0 + 4i .. +4: tile e's column i
 // is n0 + 4i + e, so that register c of the 4 tiles holds out[t0 + 4q +
-// c][col .. col + 4], and the MFMA reduction index q is rank 4m + q.
-template <typename IO, bool AT>
+// c][col .. col + 4].  In MFMA step m of a group of 16 ranks m0.., the
+// reduction index q is rank m0 + 4q + m: a lane's 4 ranks are consecutive,
+// one 16-byte load of L, and of A (dX) or of each row of B (forward), when
+// r % 4 == 0 (VEC).
+template <typename IO, bool AT, bool VEC>
 __global__ __launch_bounds__(kOutThreads) void lowrank_out_kernel(OutJobs jobs, int T, int rank) {
   int z = 0;
   while (z + 1 < jobs.n && (int)blockIdx.x >= jobs.j[z + 1].first) ++z;
   const OutJob& job = jobs.j[z];
   const int n = job.n;
   const int b = (int)blockIdx.x - job.first, ncb = (n + 255) / 256;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int i = lane & 15, q = lane >> 4;
   const int t0 = (b / ncb) * 16, col = (b % ncb) * 256 + 64 * wave + 4 * i;
   const bool col_ok = col < n;  // n % 4 == 0
+  const int colc = min(col, n - 4);
   f32x4 base[4];
 #pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    const int t = t0 + 4 * q + c;
-    base[c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    if (t < T && col_ok) base[c] = *reinterpret_cast<const f32x4*>(job.base + (long)t * n + col);
-  }
+  for (int c = 0; c < 4; ++c)
+    base[c] = *reinterpret_cast<const f32x4*>(job.base + (long)min(t0 + 4 * q + c, T - 1) * n + colc);
   f32x4 acc[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) acc[e] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   const bool row_ok = t0 + i < T;
   for (int term = 0; term < job.n_terms; ++term) {
-    const float* L = job.l[term];
+    const float* L = job.l[term] + (long)min(t0 + i, T - 1) * rank;
     const float* V = job.v[term];
     const float s = job.s[term];
-    for (int m0 = 0; m0 < rank; m0 += 16) {  // 4 MFMA steps of 4 ranks, loads first
-      float a[4], bv[4][4];
+    for (int m0 = 0; m0 < rank; m0 += 16) {
+      const int jb = m0 + 4 * q;  // this lane's ranks jb .. jb + 3
+      float a[4], bv[4][4];       // a[m] = L[t][jb + m], bv[m][e] = V(jb + m, col + e)
+      if constexpr (VEC) {  // r % 4 == 0
+        const int jc = min(jb, rank - 4);
+        load4(L + jc, a);
+        if constexpr (AT) {
 #pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        const int j = m0 + 4 * m + q;
-        a[m] = j < rank && row_ok ? s * L[(long)(t0 + i) * rank + j] : 0.0f;
+          for (int e = 0; e < 4; ++e) {
+            float r4[4];
+            load4(V + (long)(colc + e) * rank + jc, r4);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) bv[m][e] = 0.0f;
-        if (j < rank && col_ok) {
-          if constexpr (AT) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) bv[m][e] = V[(long)(col + e) * rank + j];
-          } else {
-            load4(V + (long)j * n + col, bv[m]);
+            for (int m = 0; m < 4; ++m) bv[m][e] = r4[m];
           }
+        } else {
+#pragma unroll
+          for (int m = 0; m < 4; ++m) load4(V + (long)(jc + m) * n + colc, bv[m]);
+        }
+      } else {
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          const int j = min(jb + m, rank - 1);
+          a[m] = L[j];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) bv[m][e] = AT ? V[(long)(colc + e) * rank + j] : V[(long)j * n + colc + e];
         }
       }
+#pragma unroll
+      for (int m = 0; m < 4; ++m) a[m] = jb + m < rank && row_ok ? s * a[m] : 0.0f;
 #pragma unroll
       for (int m = 0; m < 4; ++m)
 #pragma unroll
@@ -430,8 +480,12 @@ hipError_t run_out(const ProjLaunch& a, OutJobs& jobs, hipStream_t st) {
     jobs.j[z].first = total;
     total += ((a.T + 15) / 16) * ((jobs.j[z].n + 255) / 256);
   }
-  hipLaunchKernelGGL((lowrank_out_kernel<IO, AT>), dim3(total), dim3(kOutThreads), 0, st, jobs, a.T,
-                     a.rank);
+  if (a.rank % 4 == 0)
+    hipLaunchKernelGGL((lowrank_out_kernel<IO, AT, true>), dim3(total), dim3(kOutThreads), 0, st,
+                       jobs, a.T, a.rank);
+  else
+    hipLaunchKernelGGL((lowrank_out_kernel<IO, AT, false>), dim3(total), dim3(kOutThreads), 0, st,
+                       jobs, a.T, a.rank);
   return hipGetLastError();
 }
 

@@ -147,7 +147,8 @@ def test_projection_argument_errors_come_before_any_device_work():
     assert rc == ga.ERR_UNSUPPORTED and "multiple of 4" in msg
     rc, msg = _proj_rc(T=-1)
     assert rc == ga.ERR_INVALID_ARGUMENT and "total_tokens" in msg
-    for name, backward in (("x", False), ("y", False), ("lora_b", False), ("dy", True)):
+    for name, backward in (("x", False), ("y", False), ("lora_a", False), ("lora_b", False),
+                           ("dy", True)):
         rc, msg = _proj_rc(misaligned=(name,), backward=backward)
         assert rc == ga.ERR_UNSUPPORTED and "16-byte aligned" in msg and name in msg, name
     # unused by the call: not checked
