@@ -71,10 +71,10 @@ def build(verbose: bool = False, out: str = OUT, stamps: bool = False) -> str:
     with cf.ThreadPoolExecutor(max_workers=len(SOURCES)) as ex:
         objs = list(ex.map(lambda src: _compile(src, objdir, extra + SOURCES[src]), SOURCES))
     tmp = out + ".tmp"
-    # rocBLAS runs the base projections' GEMMs (proj_lora.hip)
+    # hipBLASLt runs the base projections' GEMMs (proj_lora.hip)
     rocm_lib = os.path.join(os.path.dirname(os.path.dirname(os.path.realpath(hipcc()))), "lib")
     cmd = [hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp,
-           "-L" + rocm_lib, "-Wl,-rpath," + rocm_lib, "-lrocblas"]
+           "-L" + rocm_lib, "-Wl,-rpath," + rocm_lib, "-lhipblaslt"]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError("link failed:\n" + res.stderr)

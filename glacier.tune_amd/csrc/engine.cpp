@@ -376,7 +376,7 @@ class GpuAttentionEngine {
   void* blas() {
     if (blas_ == nullptr) {
       blas_ = create_blas_handle();
-      if (blas_ == nullptr) fail(GLACIER_ATTN_ERR_DEVICE, "rocblas_create_handle failed");
+      if (blas_ == nullptr) fail(GLACIER_ATTN_ERR_DEVICE, "hipblasLtCreate failed");
     }
     return blas_;
   }
@@ -405,7 +405,7 @@ class GpuAttentionEngine {
   float rope_base_ = 0.0f;
   // device-path scratch
   DeviceBuffer kc_, vc_, wk_, wv_;
-  // projection scratch and the rocBLAS handle (created on first use)
+  // projection scratch and the hipBLASLt handle (created on first use)
   DeviceBuffer yf_, dxf_, lowrank_, part_;
   void* blas_ = nullptr;
   // host-path device copies
