@@ -32,6 +32,7 @@ SOURCES = {
     "attn_kernels.hip": (),
     "attn_fwd.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form"),
     "proj_lora.hip": (),
+    "rmsnorm.hip": (),
     "engine.cpp": (),
 }
 COMMON = [

@@ -21,8 +21,10 @@
 #include <vector>
 
 #include "../../include/glacier_attn.h"
+#include "../../include/glacier_norm.h"
 #include "../../include/glacier_qkv.h"
 #include "attn_launch.hpp"
+#include "norm_launch.hpp"
 #include "proj_launch.hpp"
 
 namespace glacier {
@@ -223,6 +225,23 @@ class GpuAttentionEngine {
     check_hip(launch_proj_backward(a, stream(), blas()), "projection backward launch");
   }
 
+  // ---- residual add and RMSNorm (glacier_norm.h) ------------------------
+  // ElementwiseKernels.RMSNorm and TensorOps.Add (TransformerBlock.cs:318,
+  // :505-506, :524, :579).
+  void NormForward(const NormFwd& a) {
+    if (a.rows == 0) return;
+    check_hip(launch_rmsnorm_forward(a, stream()), "rmsnorm forward launch");
+  }
+
+  // ElementwiseKernels.RMSNormBackward and the residual adds
+  // (TransformerBlock.cs:672-677, :827-836).
+  void NormBackward(NormBwd a) {
+    if (a.rows == 0) return;
+    if (a.d_weight != nullptr)
+      a.rstd = static_cast<float*>(rstd_.ensure(sizeof(float) * a.rows, "norm row scales"));
+    check_hip(launch_rmsnorm_backward(a, stream()), "rmsnorm backward launch");
+  }
+
   // ---- host entry points (fp32 host tensors) ----------------------------
   // GpuLoraEngine.ForwardAttention (GpuLoraEngine.Forward.cs:467-512).
   void ForwardAttention(int /*layerIndex*/, float* q, float* k, const float* v,
@@ -407,6 +426,7 @@ class GpuAttentionEngine {
   DeviceBuffer kc_, vc_, wk_, wv_;
   // projection scratch and the hipBLASLt handle (created on first use)
   DeviceBuffer yf_, dxf_, lowrank_, part_;
+  DeviceBuffer rstd_;  // RMSNorm backward row scales (weight gradient)
   void* blas_ = nullptr;
   // host-path device copies
   DeviceBuffer h_q_, h_k_, h_v_, h_out_, h_lse_, h_qr_, h_kr_, h_dout_, h_dq_, h_dk_, h_dv_;
@@ -547,6 +567,29 @@ ProjLaunch proj_launch_of(const glacier_proj_desc* desc, const void* x, const gl
         (long long)proj[p].out_features * d.in_features >= (1LL << 31))
       fail(GLACIER_ATTN_ERR_UNSUPPORTED, "tensor too large");
   return a;
+}
+
+// Checks a glacier_norm_desc before any device work.
+void norm_check(const glacier_norm_desc* desc) {
+  if (desc == nullptr) fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, "desc is NULL");
+  const glacier_norm_desc& d = *desc;
+  if (d.rows < 0) fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, "rows must be >= 0");
+  if (d.n <= 0) fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, "n must be positive");
+  if (d.io_dtype != GLACIER_ATTN_IO_F32 && d.io_dtype != GLACIER_ATTN_IO_BF16)
+    fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, "unknown io dtype " + std::to_string(d.io_dtype));
+  if (!std::isfinite(d.eps) || d.eps < 0.0f)
+    fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, "eps must be finite and >= 0");
+  if (d.n % 4 != 0) fail(GLACIER_ATTN_ERR_UNSUPPORTED, "n must be a multiple of 4");
+  if (d.n > GLACIER_NORM_MAX_N)
+    fail(GLACIER_ATTN_ERR_UNSUPPORTED, "n must be at most " + std::to_string(GLACIER_NORM_MAX_N));
+  if ((long long)d.rows * d.n >= (1LL << 31)) fail(GLACIER_ATTN_ERR_UNSUPPORTED, "tensor too large");
+}
+
+// Non-null (when the call has rows) and 16-byte aligned: the kernels move 4
+// consecutive elements at once.
+void need_row_tensor(const void* p, const char* name, bool has_rows) {
+  if (has_rows && p == nullptr) fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, std::string(name) + " is NULL");
+  if (!aligned16(p)) fail(GLACIER_ATTN_ERR_UNSUPPORTED, std::string(name) + " must be 16-byte aligned");
 }
 
 void need(const void* p, const char* name) {
@@ -756,6 +799,46 @@ int glacier_proj_backward(glacier_attn_ctx* ctx, const glacier_proj_desc* desc, 
     std::lock_guard<std::mutex> g(ctx->eng->lock());
     ctx->eng->activate();
     ctx->eng->ProjBackward(a);
+  });
+}
+
+int glacier_rmsnorm_forward(glacier_attn_ctx* ctx, const glacier_norm_desc* desc, const void* x,
+                            const void* delta, const float* weight, void* x1, void* y) {
+  return guarded([&] {
+    glacier::norm_check(desc);
+    const bool rows = desc->rows > 0;
+    glacier::need_row_tensor(x, "x", rows);
+    glacier::need_row_tensor(weight, "weight", rows);
+    glacier::need_row_tensor(y, "y", rows);
+    glacier::need_row_tensor(delta, "delta", false);
+    if (delta != nullptr) glacier::need_row_tensor(x1, "x1 (required with delta)", rows);
+    need(ctx, "ctx");
+    glacier::NormFwd a{desc->rows, desc->n, desc->eps, desc->io_dtype == GLACIER_ATTN_IO_BF16,
+                       x, delta, weight, delta != nullptr ? x1 : nullptr, y};
+    std::lock_guard<std::mutex> g(ctx->eng->lock());
+    ctx->eng->activate();
+    ctx->eng->NormForward(a);
+  });
+}
+
+int glacier_rmsnorm_backward(glacier_attn_ctx* ctx, const glacier_norm_desc* desc, const void* dy,
+                             const void* x, const float* weight, const void* d_residual, void* dx,
+                             float* d_weight) {
+  return guarded([&] {
+    glacier::norm_check(desc);
+    const bool rows = desc->rows > 0;
+    glacier::need_row_tensor(dy, "dy", rows);
+    glacier::need_row_tensor(x, "x", rows);
+    glacier::need_row_tensor(weight, "weight", rows);
+    glacier::need_row_tensor(dx, "dx", rows);
+    glacier::need_row_tensor(d_residual, "d_residual", false);
+    glacier::need_row_tensor(d_weight, "d_weight", false);
+    need(ctx, "ctx");
+    glacier::NormBwd a{desc->rows, desc->n, desc->eps, desc->io_dtype == GLACIER_ATTN_IO_BF16,
+                       dy, x, weight, d_residual, dx, d_weight, nullptr};
+    std::lock_guard<std::mutex> g(ctx->eng->lock());
+    ctx->eng->activate();
+    ctx->eng->NormBackward(a);
   });
 }
 

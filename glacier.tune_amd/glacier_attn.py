@@ -28,7 +28,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libglacier_attn.so")
 HEADERS = [os.path.join(os.path.dirname(HERE), "include", h)
-           for h in ("glacier_attn.h", "glacier_qkv.h")]
+           for h in ("glacier_attn.h", "glacier_qkv.h", "glacier_norm.h")]
 
 OK, ERR_INVALID_ARGUMENT, ERR_UNSUPPORTED, ERR_DEVICE, ERR_OUT_OF_MEMORY = 0, 1, 2, 3, 4
 PREC_FP32, PREC_BF16 = 0, 1
@@ -85,6 +85,16 @@ class ProjDesc(ctypes.Structure):
     ]
 
 
+class NormDesc(ctypes.Structure):
+    """glacier_norm_desc (include/glacier_norm.h)."""
+    _fields_ = [
+        ("rows", ctypes.c_int32),
+        ("n", ctypes.c_int32),
+        ("io_dtype", ctypes.c_int32),
+        ("eps", ctypes.c_float),
+    ]
+
+
 class LoraProj(ctypes.Structure):
     _fields_ = [
         ("w", ctypes.c_void_p),
@@ -108,7 +118,7 @@ def header_functions() -> list[str]:
     names = set()
     for h in HEADERS:
         text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
-        names |= set(re.findall(r"\b(glacier_(?:attn|proj)_[a-z_]+)\s*\(", text))
+        names |= set(re.findall(r"\b(glacier_(?:attn|proj|rmsnorm)_[a-z_]+)\s*\(", text))
     return sorted(names)
 
 
@@ -144,6 +154,8 @@ def load():
                                            ctypes.POINTER(ctypes.c_int64)]
     L.glacier_proj_forward.argtypes = [vp, ctypes.POINTER(ProjDesc), vp, ctypes.POINTER(LoraProj),
                                        c_int]
+    L.glacier_rmsnorm_forward.argtypes = [vp, ctypes.POINTER(NormDesc), vp, vp, vp, vp, vp]
+    L.glacier_rmsnorm_backward.argtypes = [vp, ctypes.POINTER(NormDesc), vp, vp, vp, vp, vp, vp]
     L.glacier_proj_backward.argtypes = [vp, ctypes.POINTER(ProjDesc), vp,
                                         ctypes.POINTER(LoraProj), c_int, vp]
     _lib = L
@@ -393,6 +405,57 @@ class GpuAttentionEngine:
         self._bind_stream()
         _check(load().glacier_proj_backward(self._h, ctypes.byref(desc), self._ptr(x), arr,
                                             len(projs), self._ptr(dx)))
+        return dx
+
+    # ---- residual add and RMSNorm (glacier_norm.h) -----------------------
+    def _norm_desc(self, x, eps):
+        if not (x.is_cuda and x.is_contiguous() and x.dim() == 2):
+            raise TypeError("x must be a contiguous [rows, n] GPU tensor")
+        desc = NormDesc()
+        desc.rows, desc.n = int(x.shape[0]), int(x.shape[1])
+        desc.io_dtype = self._io_of(x)
+        desc.eps = float(eps)
+        return desc
+
+    @staticmethod
+    def _like(t, ref, name):
+        if t is not None and not (t.is_cuda and t.is_contiguous() and t.shape == ref.shape
+                                  and t.dtype == ref.dtype):
+            raise TypeError(f"{name} must be a contiguous GPU tensor like x")
+
+    def rmsnorm_forward(self, x, weight, eps, delta=None, x1=None, y=None):
+        """x1 = x + delta, y = RMSNorm(x1) weight (delta None: y = RMSNorm(x)
+        weight and x1 is None).  x, delta [rows, n] float32 or bfloat16, weight
+        [n] float32.  Returns (x1, y)."""
+        import torch
+
+        desc = self._norm_desc(x, eps)
+        for t, name in ((delta, "delta"), (x1, "x1"), (y, "y")):
+            self._like(t, x, name)
+        y = torch.empty_like(x) if y is None else y
+        if delta is not None and x1 is None:
+            x1 = torch.empty_like(x)
+        self._bind_stream()
+        _check(load().glacier_rmsnorm_forward(self._h, ctypes.byref(desc), self._ptr(x),
+                                              self._ptr(delta), self._ptr(weight),
+                                              self._ptr(x1 if delta is not None else None),
+                                              self._ptr(y)))
+        return (x1 if delta is not None else None), y
+
+    def rmsnorm_backward(self, dy, x, weight, eps, d_residual=None, dx=None, d_weight=None):
+        """dx = RMSNormBackward(dy; x, weight) + d_residual; d_weight (float32
+        [n], optional) is accumulated.  Returns dx."""
+        import torch
+
+        desc = self._norm_desc(x, eps)
+        for t, name in ((dy, "dy"), (d_residual, "d_residual"), (dx, "dx")):
+            self._like(t, x, name)
+        dx = torch.empty_like(x) if dx is None else dx
+        self._bind_stream()
+        _check(load().glacier_rmsnorm_backward(self._h, ctypes.byref(desc), self._ptr(dy),
+                                               self._ptr(x), self._ptr(weight),
+                                               self._ptr(d_residual), self._ptr(dx),
+                                               self._ptr(d_weight)))
         return dx
 
     # ---- instrumentation ---------------------------------------------------

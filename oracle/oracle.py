@@ -58,6 +58,8 @@ def lib():
         L.oracle_num_threads.restype = i
         L.oracle_proj_forward.argtypes = [_f32p, _f32p, vp, vp, vp, f, _f32p, i, i, i, i]
         L.oracle_proj_backward.argtypes = [_f32p, _f32p, _f32p, vp, vp, f, vp, vp, vp, i, i, i, i]
+        L.oracle_rmsnorm_forward.argtypes = [_f32p, vp, _f32p, f, vp, _f32p, i, i]
+        L.oracle_rmsnorm_backward.argtypes = [_f32p, _f32p, _f32p, f, vp, _f32p, vp, i, i]
         L.oracle_set_num_threads.argtypes = [i]
         _lib = L
     return _lib
@@ -265,6 +267,30 @@ def proj_backward(x, dy, w, a=None, b=None, scaling=0.0, dx=None, grad_a=None, g
     lib().oracle_proj_backward(x, dy, w, _ptr(a), _ptr(b), scaling, _ptr(dx), _ptr(grad_a),
                                _ptr(grad_b), S, n_in, n_out, rank)
     return dx, grad_a, grad_b
+
+
+def rmsnorm_forward(x, w, eps, delta=None):
+    """x1 = x + delta (delta None: x1 = x); y = RMSNorm(x1) w.  x, delta [rows, n],
+    w [n].  Returns (x1, y)."""
+    x = _c(x); w = _c(w)
+    rows, n = x.shape
+    delta = None if delta is None else _c(delta)
+    x1 = np.empty_like(x)
+    y = np.empty_like(x)
+    lib().oracle_rmsnorm_forward(x, _ptr(delta), w, eps, _ptr(x1), y, rows, n)
+    return x1, y
+
+
+def rmsnorm_backward(dy, x, w, eps, d_residual=None, d_weight=None):
+    """dx = RMSNormBackward(dy; x, w) + d_residual; d_weight (if given) is
+    accumulated in place.  Returns dx."""
+    dy = _c(dy); x = _c(x); w = _c(w)
+    rows, n = x.shape
+    d_residual = None if d_residual is None else _c(d_residual)
+    assert d_weight is None or (d_weight.dtype == np.float32 and d_weight.flags["C_CONTIGUOUS"])
+    dx = np.empty_like(x)
+    lib().oracle_rmsnorm_backward(dy, x, w, eps, _ptr(d_residual), dx, _ptr(d_weight), rows, n)
+    return dx
 
 
 def proj_fp64(x, w, bias=None, a=None, b=None, scaling=0.0):

@@ -21,7 +21,8 @@ def test_library_exports_every_header_function():
     exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
     assert set(declared) <= exported
     # nothing else leaks into the ABI under the library's prefixes
-    assert {e for e in exported if e.startswith(("glacier_attn_", "glacier_proj_"))} == set(declared)
+    assert {e for e in exported
+            if e.startswith(("glacier_attn_", "glacier_proj_", "glacier_rmsnorm_"))} == set(declared)
     assert {"glacier_proj_forward", "glacier_proj_backward"} <= set(declared)
 
 
@@ -158,4 +159,48 @@ def test_projection_argument_errors_come_before_any_device_work():
     rc, msg = _proj_rc(rank=0, lora=False)
     assert rc == ga.ERR_INVALID_ARGUMENT and "ctx" in msg
     rc, msg = _proj_rc(backward=True)
+    assert rc == ga.ERR_INVALID_ARGUMENT and "ctx" in msg
+
+
+def _norm_rc(rows=8, n=64, io=ga.IO_BF16, eps=1e-6, backward=False, delta=True, x1=True,
+             misaligned=()):
+    L = ga.load()
+    desc = ga.NormDesc(rows, n, io, eps)
+    addr = lambda name: 8 if name in misaligned else 16  # validation fails before use
+    if backward:
+        rc = L.glacier_rmsnorm_backward(None, ctypes.byref(desc), addr("dy"), addr("x"),
+                                        addr("weight"), addr("d_residual"), addr("dx"), None)
+    else:
+        rc = L.glacier_rmsnorm_forward(None, ctypes.byref(desc), addr("x"),
+                                       addr("delta") if delta else None, addr("weight"),
+                                       addr("x1") if x1 else None, addr("y"))
+    return rc, L.glacier_attn_last_error().decode()
+
+
+def test_rmsnorm_argument_errors_come_before_any_device_work():
+    rc, msg = _norm_rc(rows=-1)
+    assert rc == ga.ERR_INVALID_ARGUMENT and "rows" in msg
+    rc, msg = _norm_rc(n=0)
+    assert rc == ga.ERR_INVALID_ARGUMENT and "n must" in msg
+    rc, msg = _norm_rc(io=7)
+    assert rc == ga.ERR_INVALID_ARGUMENT and "io dtype" in msg
+    for eps in (-1.0, float("nan"), float("inf")):
+        rc, msg = _norm_rc(eps=eps)
+        assert rc == ga.ERR_INVALID_ARGUMENT and "eps" in msg
+    rc, msg = _norm_rc(n=66)
+    assert rc == ga.ERR_UNSUPPORTED and "multiple of 4" in msg
+    rc, msg = _norm_rc(n=8196)
+    assert rc == ga.ERR_UNSUPPORTED and "at most" in msg
+    rc, msg = _norm_rc(x1=False)
+    assert rc == ga.ERR_INVALID_ARGUMENT and "x1" in msg
+    for name in ("x", "delta", "weight", "x1", "y"):
+        rc, msg = _norm_rc(misaligned=(name,))
+        assert rc == ga.ERR_UNSUPPORTED and "16-byte aligned" in msg and name in msg, name
+    for name in ("dy", "x", "weight", "d_residual", "dx"):
+        rc, msg = _norm_rc(misaligned=(name,), backward=True)
+        assert rc == ga.ERR_UNSUPPORTED and "16-byte aligned" in msg and name in msg, name
+    # valid calls then need the context; without delta x1 may be NULL
+    rc, msg = _norm_rc(delta=False, x1=False)
+    assert rc == ga.ERR_INVALID_ARGUMENT and "ctx" in msg
+    rc, msg = _norm_rc(backward=True)
     assert rc == ga.ERR_INVALID_ARGUMENT and "ctx" in msg

@@ -383,3 +383,116 @@ def test_proj_planted_mistakes_are_caught():
     }
     for name, (got, bad) in grad_slips.items():
         assert oracle.max_rel_err(got, bad) > 1e-2, name
+
+
+# --- residual + RMSNorm (oracle/norm_oracle.c) -------------------------------
+
+def _norm_inputs(rows, n, seed=0):
+    rng = np.random.default_rng(seed)
+    f = lambda *s: rng.standard_normal(s).astype(np.float32)
+    return f(rows, n), f(rows, n), (1.0 + 0.2 * f(n)).astype(np.float32), f(rows, n)
+
+
+def _rmsnorm_fp64(x, w, eps):
+    x = np.asarray(x, np.float64)
+    return x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps) * np.asarray(w, np.float64)
+
+
+def test_rmsnorm_forward_closed_forms():
+    """Constant rows, one-hot rows and the mean-square invariant."""
+    n, eps = 24, 1e-5
+    w = (1.0 + 0.3 * np.random.default_rng(1).standard_normal(n)).astype(np.float32)
+    c = np.array([[0.5], [-3.0], [1e-3]], np.float32)
+    x = np.repeat(c, n, axis=1)
+    _, y = oracle.rmsnorm_forward(x, w, eps)
+    want = c.astype(np.float64) / np.sqrt(c.astype(np.float64) ** 2 + eps) * w
+    assert oracle.max_rel_err(y, want) < 1e-6
+    # one-hot row: only element k is non-zero
+    x = np.zeros((1, n), np.float32); x[0, 7] = 2.5
+    _, y = oracle.rmsnorm_forward(x, w, eps)
+    r = 1.0 / np.sqrt(2.5 ** 2 / n + eps)
+    assert abs(y[0, 7] - 2.5 * r * w[7]) < 1e-6 * abs(y[0, 7]) and np.count_nonzero(y) == 1
+    # mean over i of (y_i / w_i)^2 = ms / (ms + eps)
+    x, _, w, _ = _norm_inputs(5, 64, seed=2)
+    _, y = oracle.rmsnorm_forward(x, w, eps)
+    ms = np.mean(x.astype(np.float64) ** 2, axis=1)
+    got = np.mean((y.astype(np.float64) / w) ** 2, axis=1)
+    assert np.max(np.abs(got - ms / (ms + eps))) < 1e-5
+
+
+def test_rmsnorm_forward_scale_invariance_and_residual():
+    """With eps = 0, RMSNorm(a x) = sign(a) RMSNorm(x); the residual form is
+    RMSNorm(x + delta) with x1 = x + delta exactly."""
+    x, delta, w, _ = _norm_inputs(6, 40, seed=3)
+    _, y = oracle.rmsnorm_forward(x, w, 0.0)
+    for a in (4.0, -0.25):
+        _, ya = oracle.rmsnorm_forward((a * x).astype(np.float32), w, 0.0)
+        assert oracle.max_rel_err(ya, np.sign(a) * y) < 1e-6
+    x1, y1 = oracle.rmsnorm_forward(x, w, 1e-6, delta=delta)
+    assert np.array_equal(x1, x + delta)
+    _, y2 = oracle.rmsnorm_forward(x + delta, w, 1e-6)
+    assert np.array_equal(y1, y2)
+    assert oracle.max_rel_err(y1, _rmsnorm_fp64(x + delta, w, 1e-6)) < 1e-6
+
+
+def test_rmsnorm_backward_is_the_gradient_of_the_forward():
+    """Central differences (float64) of L = sum g * RMSNorm(x) w.r.t. x and w;
+    d_residual is added to dx and d_weight accumulates."""
+    rows, n, eps = 3, 12, 1e-3
+    x, dres, w, g = _norm_inputs(rows, n, seed=4)
+    dw = np.zeros(n, np.float32)
+    dx = oracle.rmsnorm_backward(g, x, w, eps, d_residual=dres, d_weight=dw)
+    X, W, G = x.astype(np.float64), w.astype(np.float64), g.astype(np.float64)
+    loss = lambda X_, W_: float(np.sum(G * _rmsnorm_fp64(X_, W_, eps)))
+    h = 1e-5
+    num_x = np.zeros_like(X)
+    for idx in np.ndindex(X.shape):
+        hi, lo = X.copy(), X.copy()
+        hi[idx] += h; lo[idx] -= h
+        num_x[idx] = (loss(hi, W) - loss(lo, W)) / (2 * h)
+    num_w = np.zeros_like(W)
+    for i in range(n):
+        hi, lo = W.copy(), W.copy()
+        hi[i] += h; lo[i] -= h
+        num_w[i] = (loss(X, hi) - loss(X, lo)) / (2 * h)
+    assert oracle.max_rel_err(dx - dres, num_x) < 1e-5
+    assert oracle.max_rel_err(dw, num_w) < 1e-5
+    dx2 = oracle.rmsnorm_backward(g, x, w, eps, d_weight=dw)
+    assert np.array_equal(dx2 + dres, dx) or oracle.max_rel_err(dx2 + dres, dx) < 1e-7
+    assert oracle.max_rel_err(dw, 2.0 * num_w) < 1e-5
+
+
+def test_rmsnorm_backward_is_orthogonal_to_x_without_eps():
+    """With eps = 0 the norm is scale-invariant, so sum_i x_i dx_i = 0."""
+    x, _, w, g = _norm_inputs(4, 96, seed=5)
+    dx = oracle.rmsnorm_backward(g, x, w, 0.0)
+    dots = np.sum(x.astype(np.float64) * dx, axis=1)
+    scale = np.linalg.norm(x, axis=1) * np.linalg.norm(dx, axis=1)
+    assert np.max(np.abs(dots) / scale) < 1e-5
+
+
+def test_rmsnorm_planted_mistakes_are_caught():
+    """Each plausible slip changes the result beyond the parity tolerances."""
+    rows, n, eps = 5, 32, 0.05
+    x, _, w, g = _norm_inputs(rows, n, seed=6)
+    X, W, G = x.astype(np.float64), w.astype(np.float64), g.astype(np.float64)
+    _, y = oracle.rmsnorm_forward(x, w, eps)
+    ms = np.mean(X * X, axis=1, keepdims=True)
+    fwd_slips = {
+        "eps outside the root": X / (np.sqrt(ms) + eps) * W,
+        "sum instead of mean": X / np.sqrt(ms * n + eps) * W,
+        "weight dropped": _rmsnorm_fp64(X, np.ones(n), eps),
+    }
+    for name, bad in fwd_slips.items():
+        assert oracle.max_rel_err(y, bad) > 1e-3, name
+    dx = oracle.rmsnorm_backward(g, x, w, eps)
+    r = 1.0 / np.sqrt(ms + eps)
+    c = np.sum(G * W * X, axis=1, keepdims=True)
+    bwd_slips = {
+        "r instead of r^3": r * G * W - r / n * c * X,
+        "weight missing in the sum": r * G * W - r ** 3 / n * np.sum(G * X, axis=1, keepdims=True) * X,
+        "second term sign": r * G * W + r ** 3 / n * c * X,
+        "weight missing in the first term": r * G - r ** 3 / n * c * X,
+    }
+    for name, bad in bwd_slips.items():
+        assert oracle.max_rel_err(dx, bad) > 1e-3, name
