@@ -3,6 +3,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config qwen7b_s512]
     python bench.py --component proj      # the q/k/v projections with LoRA adapters
+    python bench.py --component norm      # the residual add + RMSNorm
 
 One step = the attention layer's forward (RoPE, QK^T, causal softmax, PV,
 saving the row log-sum-exp) followed by its backward (dP, softmax gradient,
@@ -26,6 +27,12 @@ cpu_baseline = the C restatement of the reference CPU path (oracle/), fp32,
 one step = glacier_proj_forward + glacier_proj_backward of the q, k and v
 projections of Qwen2.5-7B (T=512, hidden 3584 -> 3584, 512, 512, with bias)
 with rank-16 LoRA adapters (alpha 32) on all three, bf16 tensors.
+
+--component norm measures the residual add + RMSNorm (include/glacier_norm.h):
+one step = glacier_rmsnorm_forward (x1 = x + delta, y = RMSNorm(x1) w) +
+glacier_rmsnorm_backward (dx = RMSNormBackward(dy; x1, w) + d_residual) at
+Qwen2.5-7B (T=512, hidden 3584, eps 1e-6), bf16 tensors; value = algorithmic
+HBM bytes (each input row read once, each output row written once) per second.
 """
 import argparse
 import json
@@ -236,6 +243,137 @@ def run_proj(args):
     eng.close()
 
 
+NORM_SHAPE = (512, 3584, 1.0e-6)  # Qwen2.5-7B: tokens, hidden, rms_norm_eps
+PEAK_HBM_GBS = 8000.0
+NORM_TRAFFIC_FILE = os.path.join(ROOT, "profiles", "rmsnorm_qwen7b_t512_pmc.md")
+
+
+def norm_bytes(T, n, esz):
+    """Algorithmic bytes per launch: forward reads x, delta and writes x1, y;
+    backward reads dy, x1, d_residual and writes dx; both read the weight."""
+    return {"rmsnorm_fwd": 4 * T * n * esz + 4 * n, "rmsnorm_bwd": 4 * T * n * esz + 4 * n}
+
+
+def norm_traffic(kernel):
+    if not os.path.exists(NORM_TRAFFIC_FILE):
+        return None
+    for line in open(NORM_TRAFFIC_FILE):
+        f = line.split()
+        if len(f) == 3 and f[0] == "traffic_bytes" and f[1] == kernel:
+            return int(f[2])
+    return None
+
+
+def cpu_norm_baseline(T, n, eps, nbytes, budget_s=15.0):
+    """Times oracle.rmsnorm_forward (with delta) + rmsnorm_backward (with
+    d_residual), fp32, OpenMP over rows; the rate is the bf16 step's
+    algorithmic bytes over the CPU time."""
+    import numpy as np
+
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+
+    threads = max(1, min(16, os.cpu_count() or 1))
+    oracle.set_threads(threads)
+    x, delta = oracle.fill_normal((T, n), 1), oracle.fill_normal((T, n), 2, 0.0, 0.5)
+    dy, dres = oracle.fill_normal((T, n), 3), oracle.fill_normal((T, n), 4, 0.0, 0.3)
+    w = oracle.fill_normal((n,), 5, 1.0, 0.2)
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 200 and (len(times) < 5 or time.perf_counter() < t_end):
+        t0 = time.perf_counter()
+        x1, _ = oracle.rmsnorm_forward(x, w, eps, delta=delta)
+        oracle.rmsnorm_backward(dy, x1, w, eps, d_residual=dres)
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": f"median of {len(times)} fwd+bwd passes (RMSNorm/RMSNormBackward and the "
+                      f"residual adds restated, fp32) at T={T}, hidden={n}; {med * 1e3:.2f} ms "
+                      "each; OpenMP over rows; rate = the bf16 step's algorithmic bytes / time"}
+
+
+def run_norm(args):
+    import torch
+
+    import glacier_attn as ga
+
+    T, n, eps = NORM_SHAPE
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+    rnd = lambda *shape: torch.randn(*shape, device=dev, generator=g)
+    x, delta = rnd(T, n).bfloat16(), (0.5 * rnd(T, n)).bfloat16()
+    dy, dres = rnd(T, n).bfloat16(), (0.3 * rnd(T, n)).bfloat16()
+    w = 1.0 + 0.2 * rnd(n)
+    x1, y, dx = torch.empty_like(x), torch.empty_like(x), torch.empty_like(x)
+    eng = ga.GpuAttentionEngine(0, ga.PREC_BF16)
+
+    def fwd():
+        eng.rmsnorm_forward(x, w, eps, delta=delta, x1=x1, y=y)
+
+    def bwd():
+        eng.rmsnorm_backward(dy, x1, w, eps, d_residual=dres, dx=dx)
+
+    for _ in range(args.warmup):
+        fwd(); bwd()
+    torch.cuda.synchronize()
+
+    def timed(fn):
+        start = torch.cuda.Event(enable_timing=True)
+        stop = torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(args.steps):
+            fn()
+        stop.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(stop) / args.steps
+
+    ms = timed(lambda: (fwd(), bwd()))
+    # per-kernel device time: events that each launch timestamps itself on the
+    # stream it runs on, in a separate pass
+    eng.set_kernel_timing(True)
+    for _ in range(args.steps):
+        fwd(); bwd()
+    times = eng.kernel_times()
+    eng.set_kernel_timing(False)
+    per = {k: times[k][0] / times[k][1] for k in ("rmsnorm_fwd", "rmsnorm_bwd")}
+    nb = norm_bytes(T, n, 2)
+    step_bytes = nb["rmsnorm_fwd"] + nb["rmsnorm_bwd"]
+    gbs = step_bytes / (ms * 1e-3) / 1e9
+    dom = max(per, key=per.get)
+    achieved = nb[dom] / (per[dom] * 1e-3) / 1e9
+    cpu = None if args.no_cpu else cpu_norm_baseline(T, n, eps, step_bytes)
+    res = {
+        "metric": "residual add + RMSNorm fwd+bwd GB/s (algorithmic HBM bytes), Qwen2.5-7B shape T=512",
+        "value": round(gbs, 3),
+        "unit": "GB/s",
+        "pct_hbm_peak": round(100.0 * gbs / PEAK_HBM_GBS, 3),
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded normal x, delta, dy, d_residual, weight; device-resident)",
+        "config": {
+            "workload": "rmsnorm_qwen7b_t512: x1 = x + delta, y = RMSNorm(x1) w, and dx = "
+                        "RMSNormBackward(dy; x1, w) + d_residual",
+            "tokens": T, "hidden": n, "eps": eps, "io": "bf16 activations, fp32 weight",
+            "parallelism": "1 GPU", "algorithmic_bytes_per_step": step_bytes,
+            "kernel_us": {k: round(v * 1e3, 3) for k, v in per.items()},
+        },
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 3),
+                     "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(achieved / PEAK_HBM_GBS, 5), "traffic": norm_traffic(dom)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(res), flush=True)
+    eng.close()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -243,8 +381,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="qwen7b_s512", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--component", default="attention", choices=["attention", "proj"],
-                    help="attention (the headline) or the q/k/v projections with LoRA adapters")
+    ap.add_argument("--component", default="attention", choices=["attention", "proj", "norm"],
+                    help="attention (the headline), the q/k/v projections with LoRA adapters, or "
+                         "the residual add + RMSNorm")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run 5 plain device copies of MIB MiB (a known-size kernel that "
                          "calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE counters)")
@@ -253,8 +392,20 @@ def main():
         print(json.dumps({"error": "this build runs on one GPU only; use --gpus 1 "
                                    "(the path shards by KV-head group, see DESIGN.md)"}))
         sys.exit(2)
+    if args.copy_probe > 0:
+        import torch
+
+        src = torch.ones(args.copy_probe << 18, device="cuda:0", dtype=torch.float32)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     if args.component == "proj":
         run_proj(args)
+        return
+    if args.component == "norm":
+        run_norm(args)
         return
 
     import numpy as np
@@ -266,13 +417,6 @@ def main():
     T = sum(lengths)
     cu = None if len(lengths) == 1 else np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
     dev = torch.device("cuda:0")
-    if args.copy_probe > 0:
-        src = torch.ones(args.copy_probe << 18, device=dev, dtype=torch.float32)
-        dst = torch.empty_like(src)
-        for _ in range(5):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
     g = torch.Generator(device=dev).manual_seed(0)
 
     class Layer:
@@ -352,7 +496,7 @@ def main():
         "unit": "TFLOP/s",
         "frac": round(achieved / PEAK_BF16_TFLOPS, 5),
         "traffic": measured_traffic(args.config, dom),
-        "kernel_avg_us": {n: round(a * 1e3, 3) for n, a in avg.items()},
+        "kernel_avg_us": {n: round(avg[n] * 1e3, 3) for n in FLOPS_PER_PAIR},
     }
 
     cpu = None

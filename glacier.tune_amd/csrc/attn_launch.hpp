@@ -35,7 +35,9 @@ enum KernelId : int {
   kKernFwd = 1,
   kKernBwd = 2,
   kKernReduce = 3,
-  kKernCount = 4,
+  kKernNormFwd = 4,  // rmsnorm.hip
+  kKernNormBwd = 5,
+  kKernCount = 6,
 };
 
 // Optional per-kernel hipEvent timing on the launch stream.

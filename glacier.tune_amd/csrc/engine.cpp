@@ -230,7 +230,7 @@ class GpuAttentionEngine {
   // :505-506, :524, :579).
   void NormForward(const NormFwd& a) {
     if (a.rows == 0) return;
-    check_hip(launch_rmsnorm_forward(a, stream()), "rmsnorm forward launch");
+    check_hip(launch_rmsnorm_forward(a, stream(), &timer_), "rmsnorm forward launch");
   }
 
   // ElementwiseKernels.RMSNormBackward and the residual adds
@@ -239,7 +239,7 @@ class GpuAttentionEngine {
     if (a.rows == 0) return;
     if (a.d_weight != nullptr)
       a.rstd = static_cast<float*>(rstd_.ensure(sizeof(float) * a.rows, "norm row scales"));
-    check_hip(launch_rmsnorm_backward(a, stream()), "rmsnorm backward launch");
+    check_hip(launch_rmsnorm_backward(a, stream(), &timer_), "rmsnorm backward launch");
   }
 
   // ---- host entry points (fp32 host tensors) ----------------------------
@@ -615,7 +615,7 @@ int guarded(F&& f) {
 }
 
 const char* const kKernelNames[kKernCount] = {
-    "rope_k", "attn_fwd", "attn_bwd", "attn_bwd_reduce",
+    "rope_k", "attn_fwd", "attn_bwd", "attn_bwd_reduce", "rmsnorm_fwd", "rmsnorm_bwd",
 };
 
 }  // namespace

@@ -4,6 +4,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include "attn_launch.hpp"  // KernelTimer
+
 namespace glacier {
 
 constexpr int kNormMaxN = 8192;  // widest row taken (32 chunks of 4 per lane)
@@ -36,8 +38,8 @@ struct NormBwd {
   float* rstd;
 };
 
-// Enqueue on st.
-hipError_t launch_rmsnorm_forward(const NormFwd& a, hipStream_t st);
-hipError_t launch_rmsnorm_backward(const NormBwd& a, hipStream_t st);
+// Enqueue on st; tm (may be null) times the launches when enabled.
+hipError_t launch_rmsnorm_forward(const NormFwd& a, hipStream_t st, KernelTimer* tm);
+hipError_t launch_rmsnorm_backward(const NormBwd& a, hipStream_t st, KernelTimer* tm);
 
 }  // namespace glacier
