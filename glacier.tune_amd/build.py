@@ -31,8 +31,10 @@ OBJDIR = os.path.join(HERE, "_build")
 SOURCES = {
     "attn_kernels.hip": (),
     "attn_fwd.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form"),
+    "blas_lt.cpp": (),
     "proj_lora.hip": (),
     "rmsnorm.hip": (),
+    "lmhead.hip": (),
     "engine.cpp": (),
 }
 COMMON = [

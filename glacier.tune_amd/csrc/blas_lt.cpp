@@ -1,0 +1,117 @@
+// blas_lt.cpp -- hipBLASLt GEMMs for the projection (proj_lora.hip) and the
+// LM head (lmhead.hip).
+#include "blas_lt.hpp"
+
+#include <hipblaslt/hipblaslt.h>
+
+#include <map>
+#include <tuple>
+
+namespace glacier {
+namespace {
+
+// One matmul descriptor, four layouts and the heuristic's first algorithm
+// per GEMM shape, kept for the handle's life.  No workspace is offered, so no
+// algorithm splits the reduction: every result is bitwise repeatable.
+struct GemmPlan {
+  hipblasLtMatmulDesc_t desc = nullptr;
+  hipblasLtMatrixLayout_t a = nullptr, b = nullptr, c = nullptr;
+  hipblasLtMatmulAlgo_t algo{};
+};
+
+struct Blas {
+  hipblasLtHandle_t lt = nullptr;
+  std::map<std::tuple<bool, bool, bool, int, int, int, int, int, int>, GemmPlan> plans;
+
+  ~Blas() {
+    for (auto& kv : plans) release(kv.second);
+    if (lt != nullptr) hipblasLtDestroy(lt);
+  }
+
+  // Row-major C [M x N] = alpha op(A) [M x K] op(B) [K x N] + beta C (fp32 C,
+  // bf16 or fp32 A and B; leading dimensions are row strides), as the
+  // column-major C^T = op(B)^T op(A)^T.
+  hipblasStatus_t gemm(bool bf16_in, bool ta, bool tb, int M, int N, int K, float alpha,
+                       const void* A, int lda, const void* B, int ldb, float beta, float* C, int ldc,
+                       hipStream_t st) {
+    const auto key = std::make_tuple(bf16_in, ta, tb, M, N, K, lda, ldb, ldc);
+    auto it = plans.find(key);
+    if (it == plans.end()) {
+      GemmPlan g;
+      const hipblasStatus_t e = make_plan(bf16_in, ta, tb, M, N, K, lda, ldb, ldc, g);
+      if (e != HIPBLAS_STATUS_SUCCESS) {
+        release(g);  // the next call of this shape tries again
+        return e;
+      }
+      it = plans.emplace(key, g).first;
+    }
+    const GemmPlan& g = it->second;
+    return hipblasLtMatmul(lt, g.desc, &alpha, B, g.a, A, g.b, &beta, C, g.c, C, g.c, &g.algo,
+                           nullptr, 0, st);
+  }
+
+ private:
+  static void release(GemmPlan& g) {
+    if (g.a != nullptr) hipblasLtMatrixLayoutDestroy(g.a);
+    if (g.b != nullptr) hipblasLtMatrixLayoutDestroy(g.b);
+    if (g.c != nullptr) hipblasLtMatrixLayoutDestroy(g.c);
+    if (g.desc != nullptr) hipblasLtMatmulDescDestroy(g.desc);
+    g = GemmPlan{};
+  }
+
+  hipblasStatus_t make_plan(bool bf16_in, bool ta, bool tb, int M, int N, int K, int lda, int ldb,
+                            int ldc, GemmPlan& g) {
+    const hipDataType in_t = bf16_in ? HIP_R_16BF : HIP_R_32F;
+    const hipblasOperation_t op_a = tb ? HIPBLAS_OP_T : HIPBLAS_OP_N;  // column-major A' = op(B)^T
+    const hipblasOperation_t op_b = ta ? HIPBLAS_OP_T : HIPBLAS_OP_N;  // column-major B' = op(A)^T
+    hipblasStatus_t e = hipblasLtMatmulDescCreate(&g.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F);
+    if (e == HIPBLAS_STATUS_SUCCESS)
+      e = hipblasLtMatmulDescSetAttribute(g.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &op_a, sizeof(op_a));
+    if (e == HIPBLAS_STATUS_SUCCESS)
+      e = hipblasLtMatmulDescSetAttribute(g.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &op_b, sizeof(op_b));
+    // stored shapes (rows x cols, column-major): A' N x K or K x N, B' K x M or M x K
+    if (e == HIPBLAS_STATUS_SUCCESS)
+      e = hipblasLtMatrixLayoutCreate(&g.a, in_t, tb ? K : N, tb ? N : K, ldb);
+    if (e == HIPBLAS_STATUS_SUCCESS)
+      e = hipblasLtMatrixLayoutCreate(&g.b, in_t, ta ? M : K, ta ? K : M, lda);
+    if (e == HIPBLAS_STATUS_SUCCESS) e = hipblasLtMatrixLayoutCreate(&g.c, HIP_R_32F, N, M, ldc);
+    hipblasLtMatmulPreference_t pref = nullptr;
+    if (e == HIPBLAS_STATUS_SUCCESS) e = hipblasLtMatmulPreferenceCreate(&pref);
+    const uint64_t no_workspace = 0;
+    if (e == HIPBLAS_STATUS_SUCCESS)
+      e = hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES,
+                                                &no_workspace, sizeof(no_workspace));
+    hipblasLtMatmulHeuristicResult_t res[1];
+    int found = 0;
+    if (e == HIPBLAS_STATUS_SUCCESS)
+      e = hipblasLtMatmulAlgoGetHeuristic(lt, g.desc, g.a, g.b, g.c, g.c, pref, 1, res, &found);
+    if (pref != nullptr) hipblasLtMatmulPreferenceDestroy(pref);
+    if (e == HIPBLAS_STATUS_SUCCESS && found < 1) e = HIPBLAS_STATUS_NOT_SUPPORTED;
+    if (e == HIPBLAS_STATUS_SUCCESS) g.algo = res[0].algo;
+    return e;
+  }
+};
+
+}  // namespace
+
+void* create_blas_handle() {
+  Blas* b = new Blas;
+  if (hipblasLtCreate(&b->lt) != HIPBLAS_STATUS_SUCCESS) {
+    b->lt = nullptr;
+    delete b;
+    return nullptr;
+  }
+  return b;
+}
+
+void destroy_blas_handle(void* h) { delete static_cast<Blas*>(h); }
+
+hipError_t blas_gemm(void* h, bool bf16_in, bool ta, bool tb, int M, int N, int K, float alpha,
+                     const void* A, int lda, const void* B, int ldb, float beta, float* C, int ldc,
+                     hipStream_t st) {
+  const hipblasStatus_t e = static_cast<Blas*>(h)->gemm(bf16_in, ta, tb, M, N, K, alpha, A, lda, B,
+                                                         ldb, beta, C, ldc, st);
+  return e == HIPBLAS_STATUS_SUCCESS ? hipSuccess : hipErrorLaunchFailure;
+}
+
+}  // namespace glacier

@@ -21,9 +21,12 @@
 #include <vector>
 
 #include "../../include/glacier_attn.h"
+#include "../../include/glacier_lmhead.h"
 #include "../../include/glacier_norm.h"
 #include "../../include/glacier_qkv.h"
 #include "attn_launch.hpp"
+#include "blas_lt.hpp"
+#include "lmhead_launch.hpp"
 #include "norm_launch.hpp"
 #include "proj_launch.hpp"
 
@@ -242,6 +245,64 @@ class GpuAttentionEngine {
     check_hip(launch_rmsnorm_backward(a, stream(), &timer_), "rmsnorm backward launch");
   }
 
+  // ---- LM-head cross-entropy (glacier_lmhead.h) -------------------------
+  // FusedCrossEntropyLoss.ComputeLoss / ComputeLossAndGradients
+  // (FusedCrossEntropyLoss.cs:38-364): the kept rows are found on the host
+  // from the host targets (:53, :190), as in the reference; the loss comes
+  // back as one float.  Synchronises the stream.
+  void LmHead(LmHeadLaunch a, const int32_t* targets, float* loss, int32_t* n_valid) {
+    std::vector<int> rows, tgts, src_of(static_cast<size_t>(a.T), -1);
+    for (int t = 0; t < a.T; ++t) {
+      if (targets[t] >= 0 && targets[t] < a.V) {
+        src_of[t] = static_cast<int>(rows.size());
+        rows.push_back(t);
+        tgts.push_back(targets[t]);
+      }
+    }
+    const int n = static_cast<int>(rows.size());
+    if (n_valid != nullptr) *n_valid = n;
+    *loss = 0.0f;
+    if (a.T == 0 || (n == 0 && a.d_hidden == nullptr)) return;
+    a.n_valid = n;
+    a.ldl = (a.V + 7) / 8 * 8;
+    const size_t esz = a.io_bf16 ? 2 : 4;
+    const long per_row = (long)a.ldl * (4 + (a.io_bf16 ? 2 : 0));
+    a.chunk = static_cast<int>(std::max(1L, std::min<long>(n, kLmHeadChunkBytes / per_row)));
+    const size_t ints = 2 * static_cast<size_t>(n) + static_cast<size_t>(a.T);
+    int* idx = static_cast<int*>(lm_idx_.ensure(ints * sizeof(int), "LM-head row indices"));
+    hipStream_t st = stream();
+    if (n > 0) {
+      check_hip(hipMemcpyAsync(idx, rows.data(), n * sizeof(int), hipMemcpyHostToDevice, st),
+                "copy row indices");
+      check_hip(hipMemcpyAsync(idx + n, tgts.data(), n * sizeof(int), hipMemcpyHostToDevice, st),
+                "copy targets");
+    }
+    check_hip(hipMemcpyAsync(idx + 2 * n, src_of.data(), a.T * sizeof(int), hipMemcpyHostToDevice, st),
+              "copy row map");
+    a.rows = idx;
+    a.targets = idx + n;
+    a.src_of = idx + 2 * n;
+    if (n > 0) {
+      a.hv = lm_hv_.ensure(static_cast<size_t>(a.chunk) * a.H * esz, "LM-head packed rows");
+      a.logits = static_cast<float*>(
+          lm_logits_.ensure(static_cast<size_t>(a.chunk) * a.ldl * 4, "LM-head logits"));
+      a.dl = a.io_bf16 ? lm_dl_.ensure(static_cast<size_t>(a.chunk) * a.ldl * 2, "LM-head dlogits")
+                       : static_cast<void*>(a.logits);
+      if (a.d_hidden != nullptr)
+        a.dhv = static_cast<float*>(
+            lm_dhv_.ensure(static_cast<size_t>(n) * a.H * 4, "LM-head packed gradient"));
+      a.row_loss = static_cast<float*>(lm_loss_.ensure((static_cast<size_t>(n) + 1) * 4, "LM-head losses"));
+      a.loss = a.row_loss + n;
+    }
+    check_hip(launch_lmhead(a, st, blas()), "LM-head launch");
+    float host_loss = 0.0f;
+    if (n > 0)
+      check_hip(hipMemcpyAsync(&host_loss, a.loss, sizeof(float), hipMemcpyDeviceToHost, st),
+                "copy loss to host");
+    check_hip(hipStreamSynchronize(st), "LM-head synchronize");
+    *loss = host_loss;
+  }
+
   // ---- host entry points (fp32 host tensors) ----------------------------
   // GpuLoraEngine.ForwardAttention (GpuLoraEngine.Forward.cs:467-512).
   void ForwardAttention(int /*layerIndex*/, float* q, float* k, const float* v,
@@ -427,6 +488,7 @@ class GpuAttentionEngine {
   // projection scratch and the hipBLASLt handle (created on first use)
   DeviceBuffer yf_, dxf_, lowrank_, part_;
   DeviceBuffer rstd_;  // RMSNorm backward row scales (weight gradient)
+  DeviceBuffer lm_idx_, lm_hv_, lm_logits_, lm_dl_, lm_dhv_, lm_loss_;  // LM head
   void* blas_ = nullptr;
   // host-path device copies
   DeviceBuffer h_q_, h_k_, h_v_, h_out_, h_lse_, h_qr_, h_kr_, h_dout_, h_dq_, h_dk_, h_dv_;
@@ -840,6 +902,68 @@ int glacier_rmsnorm_backward(glacier_attn_ctx* ctx, const glacier_norm_desc* des
     ctx->eng->activate();
     ctx->eng->NormBackward(a);
   });
+}
+
+namespace {
+
+int lmhead_call(glacier_attn_ctx* ctx, const glacier_lmhead_desc* desc, const void* hidden,
+                const int32_t* targets, const void* weight, void* d_hidden, float* loss,
+                int32_t* n_valid, bool grad) {
+  return guarded([&] {
+    using glacier::fail;
+    if (desc == nullptr) fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, "desc is NULL");
+    const glacier_lmhead_desc& d = *desc;
+    if (d.tokens < 0) fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, "tokens must be >= 0");
+    if (d.hidden <= 0) fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, "hidden must be positive");
+    if (d.vocab <= 0) fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, "vocab must be positive");
+    if (d.precision != GLACIER_ATTN_PREC_FP32 && d.precision != GLACIER_ATTN_PREC_BF16)
+      fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, "unknown precision " + std::to_string(d.precision));
+    if (d.io_dtype != GLACIER_ATTN_IO_F32 && d.io_dtype != GLACIER_ATTN_IO_BF16)
+      fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, "unknown io dtype " + std::to_string(d.io_dtype));
+    if (d.io_dtype == GLACIER_ATTN_IO_BF16 && d.precision != GLACIER_ATTN_PREC_BF16)
+      fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, "bf16 device tensors need GLACIER_ATTN_PREC_BF16");
+    need(loss, "loss");
+    const bool rows = d.tokens > 0;
+    if (rows && targets == nullptr) fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, "targets is NULL");
+    glacier::need_row_tensor(hidden, "hidden", rows);
+    glacier::need_row_tensor(weight, "weight", rows);
+    if (grad) glacier::need_row_tensor(d_hidden, "d_hidden", rows);
+    if (d.hidden % 8 != 0) fail(GLACIER_ATTN_ERR_UNSUPPORTED, "hidden must be a multiple of 8");
+    if ((long long)d.tokens * d.hidden >= (1LL << 31) || (long long)d.vocab * d.hidden >= (1LL << 31))
+      fail(GLACIER_ATTN_ERR_UNSUPPORTED, "tensor too large");
+    if ((long long)d.vocab + 8 >= (1LL << 31)) fail(GLACIER_ATTN_ERR_UNSUPPORTED, "vocab too large");
+    need(ctx, "ctx");
+    // Switched off: the first GPU run of this path (fp32, 32 x 896 hidden,
+    // vocabulary 151936) ended in an illegal memory access, and no cause has
+    // been shown yet; nothing is launched until one is.
+    fail(GLACIER_ATTN_ERR_UNSUPPORTED,
+         "the device LM-head path is switched off: its first GPU run faulted and the cause is not "
+         "yet known");
+    glacier::LmHeadLaunch a{};
+    a.T = d.tokens;
+    a.H = d.hidden;
+    a.V = d.vocab;
+    a.io_bf16 = d.io_dtype == GLACIER_ATTN_IO_BF16;
+    a.hidden = hidden;
+    a.weight = weight;
+    a.d_hidden = grad ? d_hidden : nullptr;
+    std::lock_guard<std::mutex> g(ctx->eng->lock());
+    ctx->eng->activate();
+    ctx->eng->LmHead(a, targets, loss, n_valid);
+  });
+}
+
+}  // namespace
+
+int glacier_lmhead_loss(glacier_attn_ctx* ctx, const glacier_lmhead_desc* desc, const void* hidden,
+                        const int32_t* targets, const void* weight, float* loss, int32_t* n_valid) {
+  return lmhead_call(ctx, desc, hidden, targets, weight, nullptr, loss, n_valid, false);
+}
+
+int glacier_lmhead_loss_and_grad(glacier_attn_ctx* ctx, const glacier_lmhead_desc* desc,
+                                 const void* hidden, const int32_t* targets, const void* weight,
+                                 void* d_hidden, float* loss, int32_t* n_valid) {
+  return lmhead_call(ctx, desc, hidden, targets, weight, d_hidden, loss, n_valid, true);
 }
 
 }  // extern "C"

@@ -46,11 +46,8 @@ struct ProjScratchNeed {
 };
 ProjScratchNeed proj_scratch_need(const ProjLaunch& a, bool backward);
 
-// Enqueue on st; blas is a hipBLASLt handle with its GEMM plans, from
-// create_blas_handle().
+// Enqueue on st; blas is a handle from create_blas_handle() (blas_lt.hpp).
 hipError_t launch_proj_forward(const ProjLaunch& a, hipStream_t st, void* blas);
 hipError_t launch_proj_backward(const ProjLaunch& a, hipStream_t st, void* blas);
-void* create_blas_handle();
-void destroy_blas_handle(void* h);
 
 }  // namespace glacier

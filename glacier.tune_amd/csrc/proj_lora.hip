@@ -11,7 +11,7 @@
 //             dA_p += s_p X^T (dY_p B_p^T),  dB_p += s_p (X A_p)^T dY_p
 //
 // The base products X W_p^T and dY_p W_p are hipBLASLt GEMMs with fp32
-// results.  Everything low-rank is here, each kernel taking every
+// results (blas_lt.cpp).  Everything low-rank is here, each kernel taking every
 // projection of the call in one launch:
 //   lowrank_rows    L = X A_p and dL = dY_p B_p^T (output r columns wide,
 //                   reduction over in / out): 16-row slabs, the reduction
@@ -30,10 +30,7 @@
 #include "attn_common.hpp"
 #include "proj_launch.hpp"
 
-#include <hipblaslt/hipblaslt.h>
-
-#include <map>
-#include <tuple>
+#include "blas_lt.hpp"
 
 namespace glacier {
 namespace {
@@ -402,94 +399,6 @@ __global__ __launch_bounds__(kOutThreads) void lowrank_out_kernel(OutJobs jobs, 
 
 unsigned blocks(long n, int per) { return static_cast<unsigned>((n + per - 1) / per); }
 
-// The base products run on hipBLASLt: one matmul descriptor, four layouts and
-// the heuristic's first algorithm per GEMM shape, kept for the handle's life.
-// No workspace is offered, so no algorithm splits the reduction: every
-// result is bitwise repeatable.
-struct GemmPlan {
-  hipblasLtMatmulDesc_t desc = nullptr;
-  hipblasLtMatrixLayout_t a = nullptr, b = nullptr, c = nullptr;
-  hipblasLtMatmulAlgo_t algo{};
-};
-
-struct Blas {
-  hipblasLtHandle_t lt = nullptr;
-  std::map<std::tuple<bool, bool, bool, int, int, int, int, int, int>, GemmPlan> plans;
-
-  ~Blas() {
-    for (auto& kv : plans) release(kv.second);
-    if (lt != nullptr) hipblasLtDestroy(lt);
-  }
-
-  // Row-major C [M x N] = alpha op(A) [M x K] op(B) [K x N] + beta C (fp32 C,
-  // bf16 or fp32 A and B; leading dimensions are row strides), as the
-  // column-major C^T = op(B)^T op(A)^T.
-  hipblasStatus_t gemm(bool bf16_in, bool ta, bool tb, int M, int N, int K, float alpha,
-                       const void* A, int lda, const void* B, int ldb, float beta, float* C, int ldc,
-                       hipStream_t st) {
-    const auto key = std::make_tuple(bf16_in, ta, tb, M, N, K, lda, ldb, ldc);
-    auto it = plans.find(key);
-    if (it == plans.end()) {
-      GemmPlan g;
-      const hipblasStatus_t e = make_plan(bf16_in, ta, tb, M, N, K, lda, ldb, ldc, g);
-      if (e != HIPBLAS_STATUS_SUCCESS) {
-        release(g);  // the next call of this shape tries again
-        return e;
-      }
-      it = plans.emplace(key, g).first;
-    }
-    const GemmPlan& g = it->second;
-    return hipblasLtMatmul(lt, g.desc, &alpha, B, g.a, A, g.b, &beta, C, g.c, C, g.c, &g.algo,
-                           nullptr, 0, st);
-  }
-
- private:
-  static void release(GemmPlan& g) {
-    if (g.a != nullptr) hipblasLtMatrixLayoutDestroy(g.a);
-    if (g.b != nullptr) hipblasLtMatrixLayoutDestroy(g.b);
-    if (g.c != nullptr) hipblasLtMatrixLayoutDestroy(g.c);
-    if (g.desc != nullptr) hipblasLtMatmulDescDestroy(g.desc);
-    g = GemmPlan{};
-  }
-
-  hipblasStatus_t make_plan(bool bf16_in, bool ta, bool tb, int M, int N, int K, int lda, int ldb,
-                            int ldc, GemmPlan& g) {
-    const hipDataType in_t = bf16_in ? HIP_R_16BF : HIP_R_32F;
-    const hipblasOperation_t op_a = tb ? HIPBLAS_OP_T : HIPBLAS_OP_N;  // column-major A' = op(B)^T
-    const hipblasOperation_t op_b = ta ? HIPBLAS_OP_T : HIPBLAS_OP_N;  // column-major B' = op(A)^T
-    hipblasStatus_t e = hipblasLtMatmulDescCreate(&g.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F);
-    if (e == HIPBLAS_STATUS_SUCCESS)
-      e = hipblasLtMatmulDescSetAttribute(g.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &op_a, sizeof(op_a));
-    if (e == HIPBLAS_STATUS_SUCCESS)
-      e = hipblasLtMatmulDescSetAttribute(g.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &op_b, sizeof(op_b));
-    // stored shapes (rows x cols, column-major): A' N x K or K x N, B' K x M or M x K
-    if (e == HIPBLAS_STATUS_SUCCESS)
-      e = hipblasLtMatrixLayoutCreate(&g.a, in_t, tb ? K : N, tb ? N : K, ldb);
-    if (e == HIPBLAS_STATUS_SUCCESS)
-      e = hipblasLtMatrixLayoutCreate(&g.b, in_t, ta ? M : K, ta ? K : M, lda);
-    if (e == HIPBLAS_STATUS_SUCCESS) e = hipblasLtMatrixLayoutCreate(&g.c, HIP_R_32F, N, M, ldc);
-    hipblasLtMatmulPreference_t pref = nullptr;
-    if (e == HIPBLAS_STATUS_SUCCESS) e = hipblasLtMatmulPreferenceCreate(&pref);
-    const uint64_t no_workspace = 0;
-    if (e == HIPBLAS_STATUS_SUCCESS)
-      e = hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES,
-                                                &no_workspace, sizeof(no_workspace));
-    hipblasLtMatmulHeuristicResult_t res[1];
-    int found = 0;
-    if (e == HIPBLAS_STATUS_SUCCESS)
-      e = hipblasLtMatmulAlgoGetHeuristic(lt, g.desc, g.a, g.b, g.c, g.c, pref, 1, res, &found);
-    if (pref != nullptr) hipblasLtMatmulPreferenceDestroy(pref);
-    if (e == HIPBLAS_STATUS_SUCCESS && found < 1) e = HIPBLAS_STATUS_NOT_SUPPORTED;
-    if (e == HIPBLAS_STATUS_SUCCESS) g.algo = res[0].algo;
-    return e;
-  }
-};
-
-#define PROJ_CHECK_BLAS(expr)                                          \
-  do {                                                                 \
-    if ((expr) != HIPBLAS_STATUS_SUCCESS) return hipErrorLaunchFailure; \
-  } while (0)
-
 // The low-rank products X A_p / dY_p B_p^T of a call: which are needed, and
 // where their results go (slot z of ProjLaunch::lowrank, [T][r] each).
 struct RowsPlan {
@@ -566,7 +475,7 @@ hipError_t run_out(const ProjLaunch& a, OutJobs& jobs, hipStream_t st) {
 const float* slot(const ProjLaunch& a, int z) { return a.lowrank + (long)z * a.T * a.rank; }
 
 template <typename IO>
-hipError_t forward_impl(const ProjLaunch& a, hipStream_t st, Blas& h) {
+hipError_t forward_impl(const ProjLaunch& a, hipStream_t st, void* h) {
   constexpr bool BF = sizeof(IO) == 2;
   long off = 0;
   OutJobs out{};
@@ -574,7 +483,7 @@ hipError_t forward_impl(const ProjLaunch& a, hipStream_t st, Blas& h) {
   for (int p = 0; p < a.n_proj; ++p) {
     const ProjSpec& s = a.p[p];
     // Yf_p = X W_p^T
-    PROJ_CHECK_BLAS(h.gemm(BF, false, true, a.T, s.out, a.in, 1.0f, a.x, a.in, s.w, a.in, 0.0f,
+    GL_CHECK(blas_gemm(h, BF, false, true, a.T, s.out, a.in, 1.0f, a.x, a.in, s.w, a.in, 0.0f,
                            a.yf + off, s.out, st));
     out.j[p] = OutJob{a.yf + off, s.bias, s.y, s.out, 0, 0, {}, {}, {}};
     off += (long)a.T * s.out;
@@ -593,12 +502,12 @@ hipError_t forward_impl(const ProjLaunch& a, hipStream_t st, Blas& h) {
 }
 
 template <typename IO>
-hipError_t backward_impl(const ProjLaunch& a, hipStream_t st, Blas& h) {
+hipError_t backward_impl(const ProjLaunch& a, hipStream_t st, void* h) {
   constexpr bool BF = sizeof(IO) == 2;
   // dXf = sum_p dY_p W_p
   for (int p = 0; p < a.n_proj; ++p) {
     const ProjSpec& s = a.p[p];
-    PROJ_CHECK_BLAS(h.gemm(BF, false, false, a.T, a.in, s.out, 1.0f, s.dy, s.out, s.w, a.in,
+    GL_CHECK(blas_gemm(h, BF, false, false, a.T, a.in, s.out, 1.0f, s.dy, s.out, s.w, a.in,
                            p == 0 ? 0.0f : 1.0f, a.dxf, a.in, st));
   }
   // dL_p = dY_p B_p^T, and L_p = X A_p where grad_B_p is wanted
@@ -666,26 +575,11 @@ ProjScratchNeed proj_scratch_need(const ProjLaunch& a, bool backward) {
 }
 
 hipError_t launch_proj_forward(const ProjLaunch& a, hipStream_t st, void* blas) {
-  Blas& h = *static_cast<Blas*>(blas);
-  return a.io_bf16 ? forward_impl<bf16>(a, st, h) : forward_impl<float>(a, st, h);
+  return a.io_bf16 ? forward_impl<bf16>(a, st, blas) : forward_impl<float>(a, st, blas);
 }
 
 hipError_t launch_proj_backward(const ProjLaunch& a, hipStream_t st, void* blas) {
-  Blas& h = *static_cast<Blas*>(blas);
-  return a.io_bf16 ? backward_impl<bf16>(a, st, h) : backward_impl<float>(a, st, h);
+  return a.io_bf16 ? backward_impl<bf16>(a, st, blas) : backward_impl<float>(a, st, blas);
 }
-
-// hipBLASLt handle and GEMM plans owned by an engine (null on failure).
-void* create_blas_handle() {
-  Blas* b = new Blas;
-  if (hipblasLtCreate(&b->lt) != HIPBLAS_STATUS_SUCCESS) {
-    b->lt = nullptr;
-    delete b;
-    return nullptr;
-  }
-  return b;
-}
-
-void destroy_blas_handle(void* h) { delete static_cast<Blas*>(h); }
 
 }  // namespace glacier

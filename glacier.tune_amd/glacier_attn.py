@@ -28,7 +28,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libglacier_attn.so")
 HEADERS = [os.path.join(os.path.dirname(HERE), "include", h)
-           for h in ("glacier_attn.h", "glacier_qkv.h", "glacier_norm.h")]
+           for h in ("glacier_attn.h", "glacier_qkv.h", "glacier_norm.h", "glacier_lmhead.h")]
 
 OK, ERR_INVALID_ARGUMENT, ERR_UNSUPPORTED, ERR_DEVICE, ERR_OUT_OF_MEMORY = 0, 1, 2, 3, 4
 PREC_FP32, PREC_BF16 = 0, 1
@@ -95,6 +95,17 @@ class NormDesc(ctypes.Structure):
     ]
 
 
+class LmHeadDesc(ctypes.Structure):
+    """glacier_lmhead_desc (include/glacier_lmhead.h)."""
+    _fields_ = [
+        ("tokens", ctypes.c_int32),
+        ("hidden", ctypes.c_int32),
+        ("vocab", ctypes.c_int32),
+        ("precision", ctypes.c_int32),
+        ("io_dtype", ctypes.c_int32),
+    ]
+
+
 class LoraProj(ctypes.Structure):
     _fields_ = [
         ("w", ctypes.c_void_p),
@@ -118,7 +129,7 @@ def header_functions() -> list[str]:
     names = set()
     for h in HEADERS:
         text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
-        names |= set(re.findall(r"\b(glacier_(?:attn|proj|rmsnorm)_[a-z_]+)\s*\(", text))
+        names |= set(re.findall(r"\b(glacier_(?:attn|proj|rmsnorm|lmhead)_[a-z_]+)\s*\(", text))
     return sorted(names)
 
 
@@ -154,6 +165,11 @@ def load():
                                            ctypes.POINTER(ctypes.c_int64)]
     L.glacier_proj_forward.argtypes = [vp, ctypes.POINTER(ProjDesc), vp, ctypes.POINTER(LoraProj),
                                        c_int]
+    i32p = ctypes.POINTER(ctypes.c_int32)
+    L.glacier_lmhead_loss.argtypes = [vp, ctypes.POINTER(LmHeadDesc), vp, vp, vp,
+                                      ctypes.POINTER(ctypes.c_float), i32p]
+    L.glacier_lmhead_loss_and_grad.argtypes = [vp, ctypes.POINTER(LmHeadDesc), vp, vp, vp, vp,
+                                               ctypes.POINTER(ctypes.c_float), i32p]
     L.glacier_rmsnorm_forward.argtypes = [vp, ctypes.POINTER(NormDesc), vp, vp, vp, vp, vp]
     L.glacier_rmsnorm_backward.argtypes = [vp, ctypes.POINTER(NormDesc), vp, vp, vp, vp, vp, vp]
     L.glacier_proj_backward.argtypes = [vp, ctypes.POINTER(ProjDesc), vp,
@@ -457,6 +473,50 @@ class GpuAttentionEngine:
                                                self._ptr(d_residual), self._ptr(dx),
                                                self._ptr(d_weight)))
         return dx
+
+    # ---- LM-head cross-entropy (glacier_lmhead.h) -------------------------
+    def _lmhead(self, hidden, targets, weight, d_hidden, grad, precision):
+        import numpy as np
+
+        for t, name in ((hidden, "hidden"), (weight, "weight")):
+            if not (t.is_cuda and t.is_contiguous() and t.dim() == 2):
+                raise TypeError(f"{name} must be a contiguous 2-D GPU tensor")
+        if weight.dtype != hidden.dtype or weight.shape[1] != hidden.shape[1]:
+            raise TypeError("weight must be [vocab, hidden] of hidden's dtype")
+        tg = np.ascontiguousarray(np.asarray(targets), np.int32)
+        if tg.shape != (hidden.shape[0],):
+            raise TypeError("targets must have one entry per row of hidden")
+        desc = LmHeadDesc()
+        desc.tokens, desc.hidden = int(hidden.shape[0]), int(hidden.shape[1])
+        desc.vocab = int(weight.shape[0])
+        desc.io_dtype = self._io_of(hidden)
+        desc.precision = int(self.precision if precision is None else precision)
+        loss = ctypes.c_float()
+        nv = ctypes.c_int32()
+        tp = tg.ctypes.data_as(ctypes.c_void_p)
+        self._bind_stream()
+        if grad:
+            _check(load().glacier_lmhead_loss_and_grad(self._h, ctypes.byref(desc), self._ptr(hidden),
+                                                       tp, self._ptr(weight), self._ptr(d_hidden),
+                                                       ctypes.byref(loss), ctypes.byref(nv)))
+        else:
+            _check(load().glacier_lmhead_loss(self._h, ctypes.byref(desc), self._ptr(hidden), tp,
+                                              self._ptr(weight), ctypes.byref(loss), ctypes.byref(nv)))
+        return loss.value, nv.value
+
+    def lmhead_loss(self, hidden, targets, weight, precision=None):
+        """Mean cross-entropy of softmax(hidden weight^T) against targets (host
+        ints; rows outside [0, vocab) dropped).  Returns (loss, n_valid)."""
+        return self._lmhead(hidden, targets, weight, None, False, precision)
+
+    def lmhead_loss_and_grad(self, hidden, targets, weight, d_hidden=None, precision=None):
+        """As lmhead_loss, plus d_hidden [T, hidden] (overwritten).  Returns
+        (loss, n_valid, d_hidden)."""
+        import torch
+
+        d_hidden = torch.empty_like(hidden) if d_hidden is None else d_hidden
+        loss, nv = self._lmhead(hidden, targets, weight, d_hidden, True, precision)
+        return loss, nv, d_hidden
 
     # ---- instrumentation ---------------------------------------------------
     def set_kernel_timing(self, enable: bool) -> None:

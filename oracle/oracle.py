@@ -60,6 +60,8 @@ def lib():
         L.oracle_proj_backward.argtypes = [_f32p, _f32p, _f32p, vp, vp, f, vp, vp, vp, i, i, i, i]
         L.oracle_rmsnorm_forward.argtypes = [_f32p, vp, _f32p, f, vp, _f32p, i, i]
         L.oracle_rmsnorm_backward.argtypes = [_f32p, _f32p, _f32p, f, vp, _f32p, vp, i, i]
+        L.oracle_ce_loss.argtypes = [_f32p, _i32p, _f32p, vp, i, i, i, ctypes.POINTER(ctypes.c_int)]
+        L.oracle_ce_loss.restype = f
         L.oracle_set_num_threads.argtypes = [i]
         _lib = L
     return _lib
@@ -291,6 +293,20 @@ def rmsnorm_backward(dy, x, w, eps, d_residual=None, d_weight=None):
     dx = np.empty_like(x)
     lib().oracle_rmsnorm_backward(dy, x, w, eps, _ptr(d_residual), dx, _ptr(d_weight), rows, n)
     return dx
+
+
+def ce_loss(hidden, targets, w, grad=True):
+    """FusedCrossEntropyLoss.ComputeLoss / ComputeLossAndGradients: hidden [T, H],
+    targets [T] (rows outside [0, V) are dropped), w [V, H].  Returns (loss,
+    n_valid, d_hidden or None)."""
+    hidden = _c(hidden); w = _c(w)
+    targets = np.ascontiguousarray(targets, np.int32)
+    T, H = hidden.shape
+    V = w.shape[0]
+    d = np.empty((T, H), np.float32) if grad else None
+    nv = ctypes.c_int(0)
+    loss = lib().oracle_ce_loss(hidden, targets, w, _ptr(d), T, H, V, ctypes.byref(nv))
+    return float(loss), nv.value, d
 
 
 def proj_fp64(x, w, bias=None, a=None, b=None, scaling=0.0):

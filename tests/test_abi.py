@@ -22,7 +22,8 @@ def test_library_exports_every_header_function():
     assert set(declared) <= exported
     # nothing else leaks into the ABI under the library's prefixes
     assert {e for e in exported
-            if e.startswith(("glacier_attn_", "glacier_proj_", "glacier_rmsnorm_"))} == set(declared)
+            if e.startswith(("glacier_attn_", "glacier_proj_", "glacier_rmsnorm_",
+                             "glacier_lmhead_"))} == set(declared)
     assert {"glacier_proj_forward", "glacier_proj_backward"} <= set(declared)
 
 
@@ -204,4 +205,44 @@ def test_rmsnorm_argument_errors_come_before_any_device_work():
     rc, msg = _norm_rc(delta=False, x1=False)
     assert rc == ga.ERR_INVALID_ARGUMENT and "ctx" in msg
     rc, msg = _norm_rc(backward=True)
+    assert rc == ga.ERR_INVALID_ARGUMENT and "ctx" in msg
+
+
+def _lmhead_rc(T=8, H=64, V=100, prec=ga.PREC_BF16, io=ga.IO_BF16, grad=True, targets=True,
+               misaligned=()):
+    L = ga.load()
+    desc = ga.LmHeadDesc(T, H, V, prec, io)
+    addr = lambda name: 8 if name in misaligned else 16  # validation fails before use
+    tg = (ctypes.c_int32 * max(T, 1))() if targets else None
+    loss = ctypes.c_float(-1.0)
+    nv = ctypes.c_int32(-1)
+    if grad:
+        rc = L.glacier_lmhead_loss_and_grad(None, ctypes.byref(desc), addr("hidden"), tg,
+                                            addr("weight"), addr("d_hidden"), ctypes.byref(loss),
+                                            ctypes.byref(nv))
+    else:
+        rc = L.glacier_lmhead_loss(None, ctypes.byref(desc), addr("hidden"), tg, addr("weight"),
+                                   ctypes.byref(loss), ctypes.byref(nv))
+    return rc, L.glacier_attn_last_error().decode()
+
+
+def test_lmhead_argument_errors_come_before_any_device_work():
+    rc, msg = _lmhead_rc(T=-1)
+    assert rc == ga.ERR_INVALID_ARGUMENT and "tokens" in msg
+    rc, msg = _lmhead_rc(H=0)
+    assert rc == ga.ERR_INVALID_ARGUMENT and "hidden" in msg
+    rc, msg = _lmhead_rc(V=0)
+    assert rc == ga.ERR_INVALID_ARGUMENT and "vocab" in msg
+    rc, msg = _lmhead_rc(prec=ga.PREC_FP32, io=ga.IO_BF16)
+    assert rc == ga.ERR_INVALID_ARGUMENT and "bf16" in msg
+    rc, msg = _lmhead_rc(targets=False)
+    assert rc == ga.ERR_INVALID_ARGUMENT and "targets" in msg
+    rc, msg = _lmhead_rc(H=60)
+    assert rc == ga.ERR_UNSUPPORTED and "multiple of 8" in msg
+    for name in ("hidden", "weight", "d_hidden"):
+        rc, msg = _lmhead_rc(misaligned=(name,))
+        assert rc == ga.ERR_UNSUPPORTED and "16-byte aligned" in msg and name in msg, name
+    rc, msg = _lmhead_rc(grad=False, misaligned=("d_hidden",))  # unused without the gradient
+    assert rc == ga.ERR_INVALID_ARGUMENT and "ctx" in msg
+    rc, msg = _lmhead_rc()
     assert rc == ga.ERR_INVALID_ARGUMENT and "ctx" in msg

@@ -496,3 +496,109 @@ def test_rmsnorm_planted_mistakes_are_caught():
     }
     for name, bad in bwd_slips.items():
         assert oracle.max_rel_err(dx, bad) > 1e-3, name
+
+
+# --- LM-head cross-entropy (oracle/ce_oracle.c) ------------------------------
+
+def _ce_inputs(T, H, V, seed=0, wscale=0.3):
+    rng = np.random.default_rng(seed)
+    h = rng.standard_normal((T, H)).astype(np.float32)
+    w = (wscale * rng.standard_normal((V, H))).astype(np.float32)
+    return h, w
+
+
+def test_ce_loss_is_mean_logsumexp_minus_target_logit():
+    """Against scipy's logsumexp in float64 over the kept rows only (targets -100
+    and >= V dropped), with targets either side of the 4096-wide vocab tiles."""
+    from scipy.special import logsumexp
+
+    T, H, V = 8, 24, 9000
+    h, w = _ce_inputs(T, H, V, seed=1)
+    tg = np.array([0, 4095, 4096, 8999, -100, 9000, 17, 8191], np.int32)
+    loss, n, _ = oracle.ce_loss(h, tg, w, grad=False)
+    keep = [i for i in range(T) if 0 <= tg[i] < V]
+    logits = h.astype(np.float64) @ w.T.astype(np.float64)
+    want = np.mean([logsumexp(logits[i]) - logits[i, tg[i]] for i in keep])
+    assert n == len(keep) == 6
+    assert abs(loss - want) < 1e-5 * abs(want)
+
+
+def test_ce_loss_closed_forms():
+    """W = 0: every logit is 0, the loss is log V and the gradient is 0.  A
+    vocabulary of one: loss 0."""
+    T, H, V = 5, 8, 777
+    h, _ = _ce_inputs(T, H, V)
+    tg = np.arange(T, dtype=np.int32)
+    loss, n, d = oracle.ce_loss(h, tg, np.zeros((V, H), np.float32))
+    assert n == T and abs(loss - np.log(V)) < 1e-6 * np.log(V)
+    assert np.all(d == 0.0)
+    loss1, _, d1 = oracle.ce_loss(h, np.zeros(T, np.int32), np.ones((1, H), np.float32))
+    assert loss1 == 0.0 and np.all(d1 == 0.0)
+    # no kept row: loss 0, gradient 0
+    loss0, n0, d0 = oracle.ce_loss(h, np.full(T, -1, np.int32), np.ones((V, H), np.float32))
+    assert loss0 == 0.0 and n0 == 0 and np.all(d0 == 0.0)
+
+
+def test_ce_gradient_is_the_derivative_of_the_loss():
+    """Central differences (float64) of the mean cross-entropy w.r.t. the hidden
+    states; dropped rows get zero gradient."""
+    from scipy.special import logsumexp
+
+    T, H, V = 4, 6, 4500
+    h, w = _ce_inputs(T, H, V, seed=2)
+    tg = np.array([3, -100, 4321, 4096], np.int32)
+    _, _, d = oracle.ce_loss(h, tg, w)
+    W = w.astype(np.float64)
+    keep = [i for i in range(T) if 0 <= tg[i] < V]
+
+    def loss(Hm):
+        l = Hm @ W.T
+        return np.mean([logsumexp(l[i]) - l[i, tg[i]] for i in keep])
+
+    Hm = h.astype(np.float64)
+    num = np.zeros_like(Hm)
+    eps = 1e-5
+    for idx in np.ndindex(Hm.shape):
+        hi, lo = Hm.copy(), Hm.copy()
+        hi[idx] += eps; lo[idx] -= eps
+        num[idx] = (loss(hi) - loss(lo)) / (2 * eps)
+    assert np.all(d[1] == 0.0)
+    assert oracle.max_rel_err(d, num) < 1e-4
+
+
+def test_ce_large_logits_stay_finite_and_planted_mistakes_are_caught():
+    """Logits near 1e3 (exp overflows without the max shift) stay finite, and
+    plausible slips change the result beyond the parity tolerances."""
+    from scipy.special import logsumexp, softmax
+
+    T, H, V = 6, 8, 5000
+    h, w = _ce_inputs(T, H, V, seed=3, wscale=150.0)
+    tg = np.array([1, 2, 4999, 4096, -1, 77], np.int32)
+    loss, n, d = oracle.ce_loss(h, tg, w)
+    assert np.isfinite(loss) and np.all(np.isfinite(d))
+    h, w = _ce_inputs(T, H, V, seed=4)
+    loss, n, d = oracle.ce_loss(h, tg, w)
+    keep = [i for i in range(T) if 0 <= tg[i] < V]
+    L = h.astype(np.float64) @ w.T.astype(np.float64)
+    W = w.astype(np.float64)
+    P = softmax(L, axis=1)
+    onehot = np.zeros_like(P)
+    for i in keep:
+        onehot[i, tg[i]] = 1.0
+    mask = np.zeros((T, 1)); mask[keep] = 1.0
+    good = ((P - onehot) * mask) @ W / len(keep)
+    assert oracle.max_rel_err(d, good) < 1e-4
+    slips = {
+        "no -1 at the target": (P * mask) @ W / len(keep),
+        "divided by T": ((P - onehot) * mask) @ W / T,
+        "dropped rows kept": (P - onehot) @ W / len(keep),
+    }
+    for name, bad in slips.items():
+        assert oracle.max_rel_err(d, bad) > 1e-3, name
+    lse = np.array([logsumexp(L[i]) for i in range(T)])
+    loss_slips = {
+        "mean over T": np.sum([lse[i] - L[i, tg[i]] for i in keep]) / T,
+        "max logit instead of lse": np.mean([L[i].max() - L[i, tg[i]] for i in keep]),
+    }
+    for name, bad in loss_slips.items():
+        assert abs(loss - bad) > 1e-3 * abs(loss), name
