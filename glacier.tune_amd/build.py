@@ -35,6 +35,7 @@ SOURCES = {
     "proj_lora.hip": (),
     "rmsnorm.hip": (),
     "lmhead.hip": (),
+    "lora_file.cpp": (),
     "engine.cpp": (),
 }
 COMMON = [

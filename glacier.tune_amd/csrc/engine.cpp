@@ -27,6 +27,7 @@
 #include "attn_launch.hpp"
 #include "blas_lt.hpp"
 #include "lmhead_launch.hpp"
+#include "lora_file.hpp"
 #include "norm_launch.hpp"
 #include "proj_launch.hpp"
 
@@ -954,6 +955,45 @@ int lmhead_call(glacier_attn_ctx* ctx, const glacier_lmhead_desc* desc, const vo
 }
 
 }  // namespace
+
+// ---- the 'LORA' v1 adapter file (glacier_lora_file.h) ---------------------
+int glacier_lora_save(const char* path, int32_t layer_count, int32_t rank, float alpha,
+                      int32_t n_tensors, const char* const* names, const int32_t* dim0,
+                      const int32_t* dim1, const float* const* data) {
+  return guarded([&] {
+    std::string err;
+    const int rc = glacier::lora::save(path, layer_count, rank, alpha, n_tensors, names, dim0, dim1,
+                                       data, err);
+    if (rc != GLACIER_ATTN_OK) glacier::fail(rc, err);
+  });
+}
+
+int glacier_lora_open(const char* path, glacier_lora_header* header, glacier_lora_reader** reader) {
+  return guarded([&] {
+    std::string err;
+    const int rc = glacier::lora::open(path, header, reader, err);
+    if (rc != GLACIER_ATTN_OK) glacier::fail(rc, err);
+  });
+}
+
+int glacier_lora_next(glacier_lora_reader* reader, char* name, int32_t name_cap, int32_t* dim0,
+                      int32_t* dim1) {
+  return guarded([&] {
+    std::string err;
+    const int rc = glacier::lora::next(reader, name, name_cap, dim0, dim1, err);
+    if (rc != GLACIER_ATTN_OK) glacier::fail(rc, err);
+  });
+}
+
+int glacier_lora_read(glacier_lora_reader* reader, float* dst, int32_t transpose) {
+  return guarded([&] {
+    std::string err;
+    const int rc = glacier::lora::read(reader, dst, transpose, err);
+    if (rc != GLACIER_ATTN_OK) glacier::fail(rc, err);
+  });
+}
+
+void glacier_lora_close(glacier_lora_reader* reader) { glacier::lora::close(reader); }
 
 int glacier_lmhead_loss(glacier_attn_ctx* ctx, const glacier_lmhead_desc* desc, const void* hidden,
                         const int32_t* targets, const void* weight, float* loss, int32_t* n_valid) {

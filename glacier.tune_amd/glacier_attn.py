@@ -28,7 +28,8 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libglacier_attn.so")
 HEADERS = [os.path.join(os.path.dirname(HERE), "include", h)
-           for h in ("glacier_attn.h", "glacier_qkv.h", "glacier_norm.h", "glacier_lmhead.h")]
+           for h in ("glacier_attn.h", "glacier_qkv.h", "glacier_norm.h", "glacier_lmhead.h",
+                     "glacier_lora_file.h")]
 
 OK, ERR_INVALID_ARGUMENT, ERR_UNSUPPORTED, ERR_DEVICE, ERR_OUT_OF_MEMORY = 0, 1, 2, 3, 4
 PREC_FP32, PREC_BF16 = 0, 1
@@ -57,8 +58,12 @@ class OutOfMemory(GlacierAttnError, MemoryError):
     pass
 
 
+class InvalidData(GlacierAttnError):
+    """A file is missing, truncated or malformed (GLACIER_LORA_ERR_DATA)."""
+
+
 _ERRORS = {ERR_INVALID_ARGUMENT: InvalidArgument, ERR_UNSUPPORTED: Unsupported,
-           ERR_DEVICE: DeviceError, ERR_OUT_OF_MEMORY: OutOfMemory}
+           ERR_DEVICE: DeviceError, ERR_OUT_OF_MEMORY: OutOfMemory, 5: InvalidData}
 
 
 class Desc(ctypes.Structure):
@@ -106,6 +111,17 @@ class LmHeadDesc(ctypes.Structure):
     ]
 
 
+class LoraHeader(ctypes.Structure):
+    """glacier_lora_header (include/glacier_lora_file.h)."""
+    _fields_ = [
+        ("version", ctypes.c_uint32),
+        ("layer_count", ctypes.c_int32),
+        ("rank", ctypes.c_int32),
+        ("alpha", ctypes.c_float),
+        ("tensor_count", ctypes.c_int32),
+    ]
+
+
 class LoraProj(ctypes.Structure):
     _fields_ = [
         ("w", ctypes.c_void_p),
@@ -129,7 +145,7 @@ def header_functions() -> list[str]:
     names = set()
     for h in HEADERS:
         text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
-        names |= set(re.findall(r"\b(glacier_(?:attn|proj|rmsnorm|lmhead)_[a-z_]+)\s*\(", text))
+        names |= set(re.findall(r"\b(glacier_(?:attn|proj|rmsnorm|lmhead|lora)_[a-z_]+)\s*\(", text))
     return sorted(names)
 
 
@@ -166,6 +182,15 @@ def load():
     L.glacier_proj_forward.argtypes = [vp, ctypes.POINTER(ProjDesc), vp, ctypes.POINTER(LoraProj),
                                        c_int]
     i32p = ctypes.POINTER(ctypes.c_int32)
+    L.glacier_lora_save.argtypes = [ctypes.c_char_p, c_int, c_int, c_float, c_int,
+                                    ctypes.POINTER(ctypes.c_char_p), i32p, i32p,
+                                    ctypes.POINTER(fp)]
+    L.glacier_lora_open.argtypes = [ctypes.c_char_p, ctypes.POINTER(LoraHeader),
+                                    ctypes.POINTER(vp)]
+    L.glacier_lora_next.argtypes = [vp, ctypes.c_char_p, c_int, i32p, i32p]
+    L.glacier_lora_read.argtypes = [vp, vp, c_int]
+    L.glacier_lora_close.argtypes = [vp]
+    L.glacier_lora_close.restype = None
     L.glacier_lmhead_loss.argtypes = [vp, ctypes.POINTER(LmHeadDesc), vp, vp, vp,
                                       ctypes.POINTER(ctypes.c_float), i32p]
     L.glacier_lmhead_loss_and_grad.argtypes = [vp, ctypes.POINTER(LmHeadDesc), vp, vp, vp, vp,
@@ -535,3 +560,51 @@ class GpuAttentionEngine:
 
     def synchronize(self) -> None:
         _check(load().glacier_attn_synchronize(self._h))
+
+
+# ---- the 'LORA' v1 adapter file (include/glacier_lora_file.h) -------------
+ERR_DATA = 5  # GLACIER_LORA_ERR_DATA
+
+
+def lora_save(path, layer_count, rank, alpha, tensors):
+    """Writes adapter_model.bin: tensors is a list of (name, 2-D float32 array)."""
+    import numpy as np
+
+    L = load()
+    arrs = [np.ascontiguousarray(a, np.float32) for _, a in tensors]
+    n = len(arrs)
+    names = (ctypes.c_char_p * max(n, 1))(*[nm.encode() for nm, _ in tensors])
+    d0 = (ctypes.c_int32 * max(n, 1))(*[a.shape[0] for a in arrs])
+    d1 = (ctypes.c_int32 * max(n, 1))(*[a.shape[1] for a in arrs])
+    fp = ctypes.POINTER(ctypes.c_float)
+    data = (fp * max(n, 1))(*[a.ctypes.data_as(fp) for a in arrs])
+    _check(L.glacier_lora_save(os.fsencode(path), int(layer_count), int(rank), float(alpha), n,
+                               names, d0, d1, data))
+
+
+def lora_load(path, transpose=None):
+    """Reads an adapter file: returns (header dict, list of (name, array)).
+    transpose(name, dim0, dim1) -> bool, if given, picks records to read in the
+    other layout ([dim1][dim0])."""
+    import numpy as np
+
+    L = load()
+    hdr = LoraHeader()
+    r = ctypes.c_void_p()
+    _check(L.glacier_lora_open(os.fsencode(path), ctypes.byref(hdr), ctypes.byref(r)))
+    out = []
+    try:
+        buf = ctypes.create_string_buffer(4096)
+        d0, d1 = ctypes.c_int32(), ctypes.c_int32()
+        for _ in range(hdr.tensor_count):
+            _check(L.glacier_lora_next(r, buf, len(buf), ctypes.byref(d0), ctypes.byref(d1)))
+            name = buf.value.decode()
+            tr = bool(transpose and transpose(name, d0.value, d1.value))
+            a = np.empty((d1.value, d0.value) if tr else (d0.value, d1.value), np.float32)
+            _check(L.glacier_lora_read(r, a.ctypes.data_as(ctypes.c_void_p), 1 if tr else 0))
+            out.append((name, a))
+    finally:
+        L.glacier_lora_close(r)
+    header = {"version": hdr.version, "layer_count": hdr.layer_count, "rank": hdr.rank,
+              "alpha": hdr.alpha, "tensor_count": hdr.tensor_count}
+    return header, out

@@ -23,7 +23,7 @@ def test_library_exports_every_header_function():
     # nothing else leaks into the ABI under the library's prefixes
     assert {e for e in exported
             if e.startswith(("glacier_attn_", "glacier_proj_", "glacier_rmsnorm_",
-                             "glacier_lmhead_"))} == set(declared)
+                             "glacier_lmhead_", "glacier_lora_"))} == set(declared)
     assert {"glacier_proj_forward", "glacier_proj_backward"} <= set(declared)
 
 
