@@ -320,7 +320,9 @@ __global__ __launch_bounds__(kThreads * fwd_groups<T>()) void attn_fwd_kernel(
 // Backward, two launches:
 //   attn_bwd    grid (Hq/Hkv, Hkv, 2 ntiles).  z < ntiles: dK/dV of one
 //               (query head, key tile), accumulated in registers over the
-//               query tiles and written as that head's fp32 partial;
+//               query tiles (fp32) and written as that head's partial in
+//               the compute dtype (bf16 in the bf16 mode, halving the
+//               partials' traffic both ways);
 //               z >= ntiles: dQ of one (query head, query tile), inverse RoPE
 //               applied on the store.  Both kinds form the row terms
 //               D_i = dO_i . O_i of the query tiles they stage with the same
@@ -550,7 +552,7 @@ template <typename IO, typename T, int D>
 __device__ inline void bwd_dkdv_tile(
     const TileDesc td, const IO* __restrict__ q_rot, const IO* __restrict__ d_out,
     const IO* __restrict__ out, const IO* __restrict__ k_rot, const IO* __restrict__ v,
-    const float* __restrict__ lse, float* __restrict__ wk, float* __restrict__ wv,
+    const float* __restrict__ lse, T* __restrict__ wk, T* __restrict__ wv,
     int total_tokens, float scale_log2, float scale) {
   using M = Mfma<T>;
   using L = Lds<T, D>;
@@ -750,7 +752,7 @@ template <typename IO, typename T, int D>
 __global__ __launch_bounds__(kThreads * bwd_groups<T>()) void attn_bwd_kernel(
     const IO* __restrict__ q_rot, const IO* __restrict__ d_out, const IO* __restrict__ out,
     const IO* __restrict__ k_rot, const IO* __restrict__ v, const float* __restrict__ lse,
-    IO* __restrict__ dq, float* __restrict__ wk, float* __restrict__ wv,
+    IO* __restrict__ dq, T* __restrict__ wk, T* __restrict__ wv,
     const TileDesc* __restrict__ tiles_bwd, int total_tokens, float scale_log2, float scale,
     const float* __restrict__ cos_t, const float* __restrict__ sin_t) {
   const TileDesc td = tiles_bwd[blockIdx.z];
@@ -766,9 +768,16 @@ __global__ __launch_bounds__(kThreads * bwd_groups<T>()) void attn_bwd_kernel(
 // (token, kv head) row, so a workgroup covers kRedThreads / (D / 8) rows.
 constexpr int kRedThreads = 128;
 
-template <typename IO, int D>
+// 4 consecutive partial elements (compute dtype) as fp32.
+__device__ inline f32x4 load_partial4(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
+__device__ inline f32x4 load_partial4(const bf16* p) {
+  const bf16x4 v = *reinterpret_cast<const bf16x4*>(p);
+  return f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
+}
+
+template <typename IO, typename T, int D>
 __global__ __launch_bounds__(kRedThreads) void attn_bwd_reduce_kernel(
-    const float* __restrict__ wk, const float* __restrict__ wv, IO* __restrict__ dk,
+    const T* __restrict__ wk, const T* __restrict__ wv, IO* __restrict__ dk,
     IO* __restrict__ dv, const int32_t* __restrict__ pos_of, int total_tokens, int ratio,
     int n_heads_kv, const float* __restrict__ cos_t, const float* __restrict__ sin_t) {
   constexpr int H = D / 2;
@@ -784,8 +793,8 @@ __global__ __launch_bounds__(kRedThreads) void attn_bwd_reduce_kernel(
   const long pos = pos_of != nullptr ? pos_of[tok] : tok;
   const f32x4 cs = *reinterpret_cast<const f32x4*>(cos_t + pos * H + p0);
   const f32x4 sn = *reinterpret_cast<const f32x4*>(sin_t + pos * H + p0);
-  const float* wkr = wk + (tok * n_heads_q + (long)j * ratio) * D + p0;
-  const float* wvr = wv + (tok * n_heads_q + (long)j * ratio) * D + p0;
+  const T* wkr = wk + (tok * n_heads_q + (long)j * ratio) * D + p0;
+  const T* wvr = wv + (tok * n_heads_q + (long)j * ratio) * D + p0;
   f32x4 k0 = {0.0f, 0.0f, 0.0f, 0.0f}, k1 = k0, v0 = k0, v1 = k0;
   constexpr int RMAX = 8;
   if (ratio <= RMAX) {
@@ -796,10 +805,10 @@ __global__ __launch_bounds__(kRedThreads) void attn_bwd_reduce_kernel(
 #pragma unroll
     for (int hh = 0; hh < RMAX; ++hh) {
       const long o = (long)(hh < ratio ? hh : 0) * D;
-      pk0[hh] = *reinterpret_cast<const f32x4*>(wkr + o);
-      pk1[hh] = *reinterpret_cast<const f32x4*>(wkr + o + H);
-      pv0[hh] = *reinterpret_cast<const f32x4*>(wvr + o);
-      pv1[hh] = *reinterpret_cast<const f32x4*>(wvr + o + H);
+      pk0[hh] = load_partial4(wkr + o);
+      pk1[hh] = load_partial4(wkr + o + H);
+      pv0[hh] = load_partial4(wvr + o);
+      pv1[hh] = load_partial4(wvr + o + H);
     }
 #pragma unroll
     for (int hh = 0; hh < RMAX; ++hh) {
@@ -812,10 +821,10 @@ __global__ __launch_bounds__(kRedThreads) void attn_bwd_reduce_kernel(
     }
   } else {
     for (int hh = 0; hh < ratio; ++hh) {
-      k0 += *reinterpret_cast<const f32x4*>(wkr + (long)hh * D);
-      k1 += *reinterpret_cast<const f32x4*>(wkr + (long)hh * D + H);
-      v0 += *reinterpret_cast<const f32x4*>(wvr + (long)hh * D);
-      v1 += *reinterpret_cast<const f32x4*>(wvr + (long)hh * D + H);
+      k0 += load_partial4(wkr + (long)hh * D);
+      k1 += load_partial4(wkr + (long)hh * D + H);
+      v0 += load_partial4(wvr + (long)hh * D);
+      v1 += load_partial4(wvr + (long)hh * D + H);
     }
   }
   f32x4 y0, y1;
@@ -904,8 +913,8 @@ hipError_t backward_impl(const BwdLaunch& a, hipStream_t st, KernelTimer* tm) {
                           dim3(kThreads * bwd_groups<T>()), lds, st, t.start(), t.stop(), 0,
                           static_cast<const IO*>(a.q_rot), static_cast<const IO*>(a.d_out),
                           static_cast<const IO*>(a.out), static_cast<const IO*>(a.k_rot),
-                          static_cast<const IO*>(a.v), a.lse, static_cast<IO*>(a.dq), a.wk, a.wv,
-                          a.tiles_bwd, a.total_tokens, a.scale_log2, a.scale, a.cos_t, a.sin_t);
+                          static_cast<const IO*>(a.v), a.lse, static_cast<IO*>(a.dq),
+                          static_cast<T*>(a.wk), static_cast<T*>(a.wv), a.tiles_bwd, a.total_tokens, a.scale_log2, a.scale, a.cos_t, a.sin_t);
     GL_CHECK(hipGetLastError());
     t.launched();
   }
@@ -914,8 +923,9 @@ hipError_t backward_impl(const BwdLaunch& a, hipStream_t st, KernelTimer* tm) {
     const long rows = (long)a.total_tokens * a.n_heads_kv;
     const unsigned grid = static_cast<unsigned>((rows + rows_per_wg - 1) / rows_per_wg);
     LaunchTiming t(tm, kKernReduce);
-    hipExtLaunchKernelGGL((attn_bwd_reduce_kernel<IO, D>), dim3(grid), dim3(kRedThreads), 0, st,
-                          t.start(), t.stop(), 0, a.wk, a.wv, static_cast<IO*>(a.dk),
+    hipExtLaunchKernelGGL((attn_bwd_reduce_kernel<IO, T, D>), dim3(grid), dim3(kRedThreads), 0, st,
+                          t.start(), t.stop(), 0, static_cast<const T*>(a.wk),
+                          static_cast<const T*>(a.wv), static_cast<IO*>(a.dk),
                           static_cast<IO*>(a.dv), a.single_seq ? nullptr : a.pos_of, a.total_tokens,
                           ratio, a.n_heads_kv, a.cos_t, a.sin_t);
     GL_CHECK(hipGetLastError());

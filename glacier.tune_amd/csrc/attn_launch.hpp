@@ -146,7 +146,7 @@ struct BwdLaunch {
   const void *d_out, *q_rot, *k_rot, *v, *out;
   const float* lse;
   void *dq, *dk, *dv;
-  float *wk, *wv;                // per-query-head dK/dV partials [T][Hq][D]
+  void *wk, *wv;                 // per-query-head dK/dV partials [T][Hq][D], compute dtype
   const TileDesc* tiles_bwd;     // [2 n_tiles] dK/dV and dQ tiles, longest expected first
   const int32_t* pos_of;
   const float *cos_t, *sin_t;

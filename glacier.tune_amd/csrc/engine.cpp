@@ -203,8 +203,10 @@ class GpuAttentionEngine {
     a.scale_log2 = kLog2e * a.scale;
     a.d_out = d_out; a.q_rot = q_rot; a.k_rot = k_rot; a.v = v; a.out = out;
     a.lse = lse; a.dq = dq; a.dk = dk; a.dv = dv;
-    a.wk = static_cast<float*>(wk_.ensure(T * Hq * D * sizeof(float), "dK partials"));
-    a.wv = static_cast<float*>(wv_.ensure(T * Hq * D * sizeof(float), "dV partials"));
+    // the partials are kept in the compute dtype (bf16 halves their traffic)
+    const size_t wsz = compute_elem_size(s.precision, s.io_bf16);
+    a.wk = wk_.ensure(T * Hq * D * wsz, "dK partials");
+    a.wv = wv_.ensure(T * Hq * D * wsz, "dV partials");
     const TileDesc* t = static_cast<const TileDesc*>(ts.tiles.ptr);
     a.tiles_bwd = t + ts.n_tiles;
     a.pos_of = static_cast<const int32_t*>(ts.pos.ptr);
