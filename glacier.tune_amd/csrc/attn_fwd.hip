@@ -522,8 +522,8 @@ hipError_t launch_fwd_bf16(const FwdLaunch& a, hipStream_t st, KernelTimer* tm) 
   constexpr size_t lds = FwdLayout<D>::BYTES;
   GL_CHECK(allow_lds(fn, lds));
   LaunchTiming t(tm, kKernFwd);
-  hipExtLaunchKernelGGL(fn, dim3(a.n_heads_q / a.n_heads_kv, a.n_heads_kv, a.n_tiles),
-                        dim3(kFwdWaves * 64), lds, st, t.start(), t.stop(), 0,
+  GL_LAUNCH(t, fn, dim3(a.n_heads_q / a.n_heads_kv, a.n_heads_kv, a.n_tiles),
+                        dim3(kFwdWaves * 64), lds, st,
                         static_cast<const IO*>(a.q), static_cast<const bf16*>(a.kc),
                         static_cast<const bf16*>(a.vc != nullptr ? a.vc : a.v),
                         static_cast<IO*>(a.out), a.lse, static_cast<IO*>(a.q_rot), a.tiles_fwd,

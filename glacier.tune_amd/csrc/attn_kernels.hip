@@ -321,8 +321,9 @@ __global__ __launch_bounds__(kThreads * fwd_groups<T>()) void attn_fwd_kernel(
 //   attn_bwd    grid (Hq/Hkv, Hkv, 2 ntiles).  z < ntiles: dK/dV of one
 //               (query head, key tile), accumulated in registers over the
 //               query tiles (fp32) and written as that head's partial in
-//               the compute dtype (bf16 in the bf16 mode, halving the
-//               partials' traffic both ways);
+//               the caller's tensor dtype (bf16 for bf16 tensors, halving the
+//               partials' traffic both ways; fp32 for fp32 tensors, so the
+//               group sum of the fp32-tensor path accumulates in fp32);
 //               z >= ntiles: dQ of one (query head, query tile), inverse RoPE
 //               applied on the store.  Both kinds form the row terms
 //               D_i = dO_i . O_i of the query tiles they stage with the same
@@ -552,7 +553,7 @@ template <typename IO, typename T, int D>
 __device__ inline void bwd_dkdv_tile(
     const TileDesc td, const IO* __restrict__ q_rot, const IO* __restrict__ d_out,
     const IO* __restrict__ out, const IO* __restrict__ k_rot, const IO* __restrict__ v,
-    const float* __restrict__ lse, T* __restrict__ wk, T* __restrict__ wv,
+    const float* __restrict__ lse, IO* __restrict__ wk, IO* __restrict__ wv,
     int total_tokens, float scale_log2, float scale) {
   using M = Mfma<T>;
   using L = Lds<T, D>;
@@ -752,7 +753,7 @@ template <typename IO, typename T, int D>
 __global__ __launch_bounds__(kThreads * bwd_groups<T>()) void attn_bwd_kernel(
     const IO* __restrict__ q_rot, const IO* __restrict__ d_out, const IO* __restrict__ out,
     const IO* __restrict__ k_rot, const IO* __restrict__ v, const float* __restrict__ lse,
-    IO* __restrict__ dq, T* __restrict__ wk, T* __restrict__ wv,
+    IO* __restrict__ dq, IO* __restrict__ wk, IO* __restrict__ wv,
     const TileDesc* __restrict__ tiles_bwd, int total_tokens, float scale_log2, float scale,
     const float* __restrict__ cos_t, const float* __restrict__ sin_t) {
   const TileDesc td = tiles_bwd[blockIdx.z];
@@ -768,7 +769,7 @@ __global__ __launch_bounds__(kThreads * bwd_groups<T>()) void attn_bwd_kernel(
 // (token, kv head) row, so a workgroup covers kRedThreads / (D / 8) rows.
 constexpr int kRedThreads = 128;
 
-// 4 consecutive partial elements (compute dtype) as fp32.
+// 4 consecutive partial elements (the tensors' dtype) as fp32.
 __device__ inline f32x4 load_partial4(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
 __device__ inline f32x4 load_partial4(const bf16* p) {
   const bf16x4 v = *reinterpret_cast<const bf16x4*>(p);
@@ -777,7 +778,7 @@ __device__ inline f32x4 load_partial4(const bf16* p) {
 
 template <typename IO, typename T, int D>
 __global__ __launch_bounds__(kRedThreads) void attn_bwd_reduce_kernel(
-    const T* __restrict__ wk, const T* __restrict__ wv, IO* __restrict__ dk,
+    const IO* __restrict__ wk, const IO* __restrict__ wv, IO* __restrict__ dk,
     IO* __restrict__ dv, const int32_t* __restrict__ pos_of, int total_tokens, int ratio,
     int n_heads_kv, const float* __restrict__ cos_t, const float* __restrict__ sin_t) {
   constexpr int H = D / 2;
@@ -793,8 +794,8 @@ __global__ __launch_bounds__(kRedThreads) void attn_bwd_reduce_kernel(
   const long pos = pos_of != nullptr ? pos_of[tok] : tok;
   const f32x4 cs = *reinterpret_cast<const f32x4*>(cos_t + pos * H + p0);
   const f32x4 sn = *reinterpret_cast<const f32x4*>(sin_t + pos * H + p0);
-  const T* wkr = wk + (tok * n_heads_q + (long)j * ratio) * D + p0;
-  const T* wvr = wv + (tok * n_heads_q + (long)j * ratio) * D + p0;
+  const IO* wkr = wk + (tok * n_heads_q + (long)j * ratio) * D + p0;
+  const IO* wvr = wv + (tok * n_heads_q + (long)j * ratio) * D + p0;
   f32x4 k0 = {0.0f, 0.0f, 0.0f, 0.0f}, k1 = k0, v0 = k0, v1 = k0;
   constexpr int RMAX = 8;
   if (ratio <= RMAX) {
@@ -873,7 +874,7 @@ hipError_t forward_impl(const FwdLaunch& a, hipStream_t st, KernelTimer* tm) {
     const unsigned grid = static_cast<unsigned>((n + kThreads - 1) / kThreads);
     IO* k_rot = static_cast<IO*>(a.k_rot);
     LaunchTiming t(tm, kKernRopeK);
-    hipExtLaunchKernelGGL((rope_k_kernel<IO, T, D>), dim3(grid), blk, 0, st, t.start(), t.stop(), 0,
+    GL_LAUNCH(t, (rope_k_kernel<IO, T, D>), dim3(grid), blk, 0, st,
                           static_cast<const IO*>(a.k), k_rot,
                           (static_cast<void*>(kc) == static_cast<void*>(k_rot)) ? nullptr : kc,
                           static_cast<const IO*>(a.v), static_cast<T*>(a.vc),
@@ -889,8 +890,8 @@ hipError_t forward_impl(const FwdLaunch& a, hipStream_t st, KernelTimer* tm) {
     constexpr size_t lds = fwd_lds<T, D>();
     GL_CHECK(allow_lds(fn, lds));
     LaunchTiming t(tm, kKernFwd);
-    hipExtLaunchKernelGGL(fn, dim3(a.n_heads_q, a.n_tiles), dim3(kThreads * fwd_groups<T>()), lds,
-                          st, t.start(), t.stop(), 0, static_cast<const IO*>(a.q),
+    GL_LAUNCH(t, fn, dim3(a.n_heads_q, a.n_tiles), dim3(kThreads * fwd_groups<T>()), lds,
+                          st, static_cast<const IO*>(a.q),
                           static_cast<const T*>(kc), static_cast<const IO*>(a.v),
                           static_cast<IO*>(a.out), a.lse, static_cast<IO*>(a.q_rot),
                           a.single_seq ? nullptr : a.tiles_fwd, a.n_tiles, a.n_heads_q,
@@ -909,12 +910,12 @@ hipError_t backward_impl(const BwdLaunch& a, hipStream_t st, KernelTimer* tm) {
     constexpr size_t lds = bwd_lds<T, D>();
     GL_CHECK(allow_lds(fn, lds));
     LaunchTiming t(tm, kKernBwd);
-    hipExtLaunchKernelGGL(fn, dim3(ratio, a.n_heads_kv, 2 * a.n_tiles),
-                          dim3(kThreads * bwd_groups<T>()), lds, st, t.start(), t.stop(), 0,
+    GL_LAUNCH(t, fn, dim3(ratio, a.n_heads_kv, 2 * a.n_tiles),
+                          dim3(kThreads * bwd_groups<T>()), lds, st,
                           static_cast<const IO*>(a.q_rot), static_cast<const IO*>(a.d_out),
                           static_cast<const IO*>(a.out), static_cast<const IO*>(a.k_rot),
                           static_cast<const IO*>(a.v), a.lse, static_cast<IO*>(a.dq),
-                          static_cast<T*>(a.wk), static_cast<T*>(a.wv), a.tiles_bwd, a.total_tokens, a.scale_log2, a.scale, a.cos_t, a.sin_t);
+                          static_cast<IO*>(a.wk), static_cast<IO*>(a.wv), a.tiles_bwd, a.total_tokens, a.scale_log2, a.scale, a.cos_t, a.sin_t);
     GL_CHECK(hipGetLastError());
     t.launched();
   }
@@ -923,9 +924,9 @@ hipError_t backward_impl(const BwdLaunch& a, hipStream_t st, KernelTimer* tm) {
     const long rows = (long)a.total_tokens * a.n_heads_kv;
     const unsigned grid = static_cast<unsigned>((rows + rows_per_wg - 1) / rows_per_wg);
     LaunchTiming t(tm, kKernReduce);
-    hipExtLaunchKernelGGL((attn_bwd_reduce_kernel<IO, T, D>), dim3(grid), dim3(kRedThreads), 0, st,
-                          t.start(), t.stop(), 0, static_cast<const T*>(a.wk),
-                          static_cast<const T*>(a.wv), static_cast<IO*>(a.dk),
+    GL_LAUNCH(t, (attn_bwd_reduce_kernel<IO, T, D>), dim3(grid), dim3(kRedThreads), 0, st,
+                          static_cast<const IO*>(a.wk),
+                          static_cast<const IO*>(a.wv), static_cast<IO*>(a.dk),
                           static_cast<IO*>(a.dv), a.single_seq ? nullptr : a.pos_of, a.total_tokens,
                           ratio, a.n_heads_kv, a.cos_t, a.sin_t);
     GL_CHECK(hipGetLastError());

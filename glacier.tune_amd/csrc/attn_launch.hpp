@@ -146,7 +146,7 @@ struct BwdLaunch {
   const void *d_out, *q_rot, *k_rot, *v, *out;
   const float* lse;
   void *dq, *dk, *dv;
-  void *wk, *wv;                 // per-query-head dK/dV partials [T][Hq][D], compute dtype
+  void *wk, *wv;                 // per-query-head dK/dV partials [T][Hq][D], tensors' dtype
   const TileDesc* tiles_bwd;     // [2 n_tiles] dK/dV and dQ tiles, longest expected first
   const int32_t* pos_of;
   const float *cos_t, *sin_t;
@@ -170,6 +170,17 @@ hipError_t allow_lds(F* fn, size_t bytes) {
                              hipFuncAttributeMaxDynamicSharedMemorySize,
                              static_cast<int>(bytes));
 }
+
+// A kernel launch on st: with t's events when timing is on
+// (hipExtLaunchKernelGGL), else a plain launch that stream capture records
+// like any other.  KERNEL in parentheses when it has template arguments.
+#define GL_LAUNCH(t, KERNEL, grid, block, lds, st, ...)                                        \
+  do {                                                                                      \
+    if ((t).start() != nullptr)                                                             \
+      hipExtLaunchKernelGGL(KERNEL, grid, block, lds, st, (t).start(), (t).stop(), 0, __VA_ARGS__); \
+    else                                                                                    \
+      hipLaunchKernelGGL(KERNEL, grid, block, lds, st, __VA_ARGS__);                        \
+  } while (0)
 
 #define GL_CHECK(expr)               \
   do {                               \

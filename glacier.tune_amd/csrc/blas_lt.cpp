@@ -10,7 +10,7 @@
 namespace glacier {
 namespace {
 
-// One matmul descriptor, four layouts and the heuristic's first algorithm
+// One matmul descriptor, four layouts and the heuristic's best zero-workspace algorithm
 // per GEMM shape, kept for the handle's life.  No workspace is offered, so no
 // algorithm splits the reduction: every result is bitwise repeatable.
 struct GemmPlan {
@@ -81,13 +81,20 @@ struct Blas {
     if (e == HIPBLAS_STATUS_SUCCESS)
       e = hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES,
                                                 &no_workspace, sizeof(no_workspace));
-    hipblasLtMatmulHeuristicResult_t res[1];
+    // The GEMMs run with no workspace: take the heuristic's best algorithm
+    // that needs none, and fail the plan (an error status, no GEMM) if none
+    // of those returned does.
+    constexpr int kCand = 8;
+    hipblasLtMatmulHeuristicResult_t res[kCand];
     int found = 0;
     if (e == HIPBLAS_STATUS_SUCCESS)
-      e = hipblasLtMatmulAlgoGetHeuristic(lt, g.desc, g.a, g.b, g.c, g.c, pref, 1, res, &found);
+      e = hipblasLtMatmulAlgoGetHeuristic(lt, g.desc, g.a, g.b, g.c, g.c, pref, kCand, res, &found);
     if (pref != nullptr) hipblasLtMatmulPreferenceDestroy(pref);
-    if (e == HIPBLAS_STATUS_SUCCESS && found < 1) e = HIPBLAS_STATUS_NOT_SUPPORTED;
-    if (e == HIPBLAS_STATUS_SUCCESS) g.algo = res[0].algo;
+    int pick = -1;
+    for (int i = 0; e == HIPBLAS_STATUS_SUCCESS && i < found && pick < 0; ++i)
+      if (res[i].state == HIPBLAS_STATUS_SUCCESS && res[i].workspaceSize == 0) pick = i;
+    if (e == HIPBLAS_STATUS_SUCCESS && pick < 0) e = HIPBLAS_STATUS_NOT_SUPPORTED;
+    if (e == HIPBLAS_STATUS_SUCCESS) g.algo = res[pick].algo;
     return e;
   }
 };

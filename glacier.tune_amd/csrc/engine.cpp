@@ -203,8 +203,10 @@ class GpuAttentionEngine {
     a.scale_log2 = kLog2e * a.scale;
     a.d_out = d_out; a.q_rot = q_rot; a.k_rot = k_rot; a.v = v; a.out = out;
     a.lse = lse; a.dq = dq; a.dk = dk; a.dv = dv;
-    // the partials are kept in the compute dtype (bf16 halves their traffic)
-    const size_t wsz = compute_elem_size(s.precision, s.io_bf16);
+    // the per-head partials are kept in the tensors' dtype: bf16 tensors get
+    // bf16 partials (half the traffic), fp32 tensors fp32 partials, so the
+    // group reduction of the fp32-tensor entry points sums fp32 values
+    const size_t wsz = s.io_bf16 ? 2 : 4;
     a.wk = wk_.ensure(T * Hq * D * wsz, "dK partials");
     a.wv = wv_.ensure(T * Hq * D * wsz, "dV partials");
     const TileDesc* t = static_cast<const TileDesc*>(ts.tiles.ptr);
@@ -243,8 +245,19 @@ class GpuAttentionEngine {
   // (TransformerBlock.cs:672-677, :827-836).
   void NormBackward(NormBwd a) {
     if (a.rows == 0) return;
-    if (a.d_weight != nullptr)
+    a.dy_w = a.dy;
+    if (a.d_weight != nullptr) {
       a.rstd = static_cast<float*>(rstd_.ensure(sizeof(float) * a.rows, "norm row scales"));
+      // The weight gradient is formed after dx is stored; when dx overwrites
+      // dy it reads a copy of dy taken first.
+      if (a.dx == a.dy) {
+        const size_t bytes = (size_t)a.rows * a.n * (a.io_bf16 ? 2 : 4);
+        void* copy = dyw_.ensure(bytes, "norm dy copy");
+        check_hip(hipMemcpyAsync(copy, a.dy, bytes, hipMemcpyDeviceToDevice, stream()),
+                  "copy dy for the weight gradient");
+        a.dy_w = copy;
+      }
+    }
     check_hip(launch_rmsnorm_backward(a, stream(), &timer_), "rmsnorm backward launch");
   }
 
@@ -490,7 +503,7 @@ class GpuAttentionEngine {
   DeviceBuffer kc_, vc_, wk_, wv_;
   // projection scratch and the hipBLASLt handle (created on first use)
   DeviceBuffer yf_, dxf_, lowrank_, part_;
-  DeviceBuffer rstd_;  // RMSNorm backward row scales (weight gradient)
+  DeviceBuffer rstd_, dyw_;  // RMSNorm backward row scales, dy copy (weight gradient)
   DeviceBuffer lm_idx_, lm_hv_, lm_logits_, lm_dl_, lm_dhv_, lm_loss_;  // LM head
   void* blas_ = nullptr;
   // host-path device copies
@@ -900,7 +913,7 @@ int glacier_rmsnorm_backward(glacier_attn_ctx* ctx, const glacier_norm_desc* des
     glacier::need_row_tensor(d_weight, "d_weight", false);
     need(ctx, "ctx");
     glacier::NormBwd a{desc->rows, desc->n, desc->eps, desc->io_dtype == GLACIER_ATTN_IO_BF16,
-                       dy, x, weight, d_residual, dx, d_weight, nullptr};
+                       dy, x, weight, d_residual, dx, d_weight, nullptr, dy};
     std::lock_guard<std::mutex> g(ctx->eng->lock());
     ctx->eng->activate();
     ctx->eng->NormBackward(a);

@@ -16,6 +16,7 @@ struct glacier_lora_reader {
   long size = 0;           // bytes in the file
   int32_t left = 0;        // records not yet started
   bool pending = false;    // a record's payload is next in the file
+  bool failed = false;     // a malformed or truncated record was met: every later call fails
   int32_t dim0 = 0, dim1 = 0;
 };
 
@@ -141,40 +142,52 @@ int open(const char* path, glacier_lora_header* header, glacier_lora_reader** re
   return kOk;
 }
 
+// The record header at the current position.  A name buffer that is too
+// small leaves the reader at the record's start, so a retry with a larger
+// buffer reads the same record; a malformed or truncated record marks the
+// reader failed (every later next/read returns GLACIER_LORA_ERR_DATA).
 int next(glacier_lora_reader* r, char* name, int32_t name_cap, int32_t* dim0, int32_t* dim1,
          std::string& err) {
   if (r == nullptr || name == nullptr || dim0 == nullptr || dim1 == nullptr)
     return bad(err, kInvalid, "reader, name, dim0 and dim1 are required");
+  if (r->failed) return bad(err, kData, "the LoRA file was found malformed by an earlier call");
   if (r->pending) return bad(err, kInvalid, "the previous record has not been read or skipped");
   if (r->left <= 0) return bad(err, kInvalid, "no more records");
+  const long start = std::ftell(r->f);
+  auto corrupt = [&](const std::string& msg) {
+    r->failed = true;
+    return bad(err, kData, msg);
+  };
   // the name: a 7-bit varint byte count, then UTF-8
   uint32_t len = 0;
   int shift = 0;
   for (;;) {
     const int c = std::fgetc(r->f);
-    if (c == EOF) return bad(err, kData, "truncated LoRA record name");
+    if (c == EOF) return corrupt("truncated LoRA record name");
     len |= static_cast<uint32_t>(c & 0x7F) << shift;
     if ((c & 0x80) == 0) break;
     shift += 7;
-    if (shift > 28) return bad(err, kData, "malformed LoRA record name length");
+    if (shift > 28) return corrupt("malformed LoRA record name length");
   }
-  if (static_cast<long>(len) > remaining(r)) return bad(err, kData, "truncated LoRA record name");
-  if (name_cap <= 0 || len + 1 > static_cast<uint32_t>(name_cap))
+  if (static_cast<long>(len) > remaining(r)) return corrupt("truncated LoRA record name");
+  if (name_cap <= 0 || len + 1 > static_cast<uint32_t>(name_cap)) {
+    if (std::fseek(r->f, start, SEEK_SET) != 0) return corrupt("seek failed");
     return bad(err, kInvalid, "name buffer too small: the record name needs " +
                                   std::to_string(len + 1) + " bytes");
-  if (std::fread(name, 1, len, r->f) != len) return bad(err, kData, "truncated LoRA record name");
+  }
+  if (std::fread(name, 1, len, r->f) != len) return corrupt("truncated LoRA record name");
   name[len] = '\0';
   int32_t d0 = 0, d1 = 0;
   if (std::fread(&d0, 4, 1, r->f) != 1 || std::fread(&d1, 4, 1, r->f) != 1)
-    return bad(err, kData, std::string("truncated LoRA record header for '") + name + "'");
+    return corrupt(std::string("truncated LoRA record header for '") + name + "'");
   if (d0 <= 0 || d1 <= 0)
-    return bad(err, kData, "invalid LoRA tensor dimensions [" + std::to_string(d0) + ", " +
-                               std::to_string(d1) + "] for '" + name + "'");
+    return corrupt("invalid LoRA tensor dimensions [" + std::to_string(d0) + ", " +
+                   std::to_string(d1) + "] for '" + name + "'");
   const long bytes = static_cast<long>(d0) * d1 * static_cast<long>(sizeof(float));
   if (bytes > remaining(r))
-    return bad(err, kData, std::string("truncated LoRA binary payload for '") + name +
-                               "': expected " + std::to_string(bytes) + " bytes, only " +
-                               std::to_string(remaining(r)) + " remaining");
+    return corrupt(std::string("truncated LoRA binary payload for '") + name + "': expected " +
+                   std::to_string(bytes) + " bytes, only " + std::to_string(remaining(r)) +
+                   " remaining");
   r->pending = true;
   r->dim0 = d0;
   r->dim1 = d1;
@@ -186,21 +199,25 @@ int next(glacier_lora_reader* r, char* name, int32_t name_cap, int32_t* dim0, in
 
 int read(glacier_lora_reader* r, float* dst, int32_t transpose, std::string& err) {
   if (r == nullptr) return bad(err, kInvalid, "reader is NULL");
+  if (r->failed) return bad(err, kData, "the LoRA file was found malformed by an earlier call");
   if (!r->pending) return bad(err, kInvalid, "no record is pending: call glacier_lora_next first");
   const size_t n = static_cast<size_t>(r->dim0) * r->dim1;
   r->pending = false;
+  auto corrupt = [&](const char* msg) {
+    r->failed = true;
+    return bad(err, kData, msg);
+  };
   if (dst == nullptr) {
     if (std::fseek(r->f, static_cast<long>(n * sizeof(float)), SEEK_CUR) != 0)
-      return bad(err, kData, "seek failed");
+      return corrupt("seek failed");
     return kOk;
   }
   if (!transpose) {
-    if (std::fread(dst, sizeof(float), n, r->f) != n) return bad(err, kData, "truncated LoRA payload");
+    if (std::fread(dst, sizeof(float), n, r->f) != n) return corrupt("truncated LoRA payload");
     return kOk;
   }
   std::vector<float> tmp(n);
-  if (std::fread(tmp.data(), sizeof(float), n, r->f) != n)
-    return bad(err, kData, "truncated LoRA payload");
+  if (std::fread(tmp.data(), sizeof(float), n, r->f) != n) return corrupt("truncated LoRA payload");
   for (int32_t i = 0; i < r->dim0; ++i)
     for (int32_t j = 0; j < r->dim1; ++j)
       dst[static_cast<size_t>(j) * r->dim0 + i] = tmp[static_cast<size_t>(i) * r->dim1 + j];

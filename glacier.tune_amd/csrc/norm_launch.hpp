@@ -24,7 +24,8 @@ struct NormFwd {
 };
 
 // Backward: dx = RMSNormBackward(dy; x, w) + d_residual (null: nothing added);
-// d_weight += sum over rows of dy x r when not null (rstd: [rows] scratch then).
+// d_weight += sum over rows of dy x r when not null (rstd: [rows] scratch then;
+// dy_w: the dy that sum reads, a copy of dy when dx overwrites it).
 struct NormBwd {
   int rows, n;
   float eps;
@@ -36,6 +37,7 @@ struct NormBwd {
   void* dx;
   float* d_weight;
   float* rstd;
+  const void* dy_w;
 };
 
 // Enqueue on st; tm (may be null) times the launches when enabled.

@@ -185,7 +185,7 @@ __global__ __launch_bounds__(256) void rmsnorm_dw_kernel(NormBwd a) {
   const int i = blockIdx.x * 256 + threadIdx.x;
   if (i >= a.n) return;
   const IO* x = static_cast<const IO*>(a.x) + i;
-  const IO* dy = static_cast<const IO*>(a.dy) + i;
+  const IO* dy = static_cast<const IO*>(a.dy_w) + i;  // dy as passed in, even when dx overwrote it
   float acc = 0.0f;
   int t = 0;
   for (; t + 8 <= a.rows; t += 8) {
@@ -226,7 +226,7 @@ hipError_t fwd(const NormFwd& a, hipStream_t st, KernelTimer* tm) {
   LaunchTiming t(tm, kKernNormFwd);
   switch (chunks_per_lane(a.n)) {
 #define GL_NORM(C)                                                                              \
-  hipExtLaunchKernelGGL((rmsnorm_fwd_kernel<IO, C>), grid, block, 0, st, t.start(), t.stop(), 0, \
+  GL_LAUNCH(t, (rmsnorm_fwd_kernel<IO, C>), grid, block, 0, st, \
                         a)
     case 1: GL_NORM(1); break;
     case 2: GL_NORM(2); break;
@@ -250,7 +250,7 @@ hipError_t bwd(const NormBwd& a, hipStream_t st, KernelTimer* tm) {
     LaunchTiming t(tm, kKernNormBwd);
     switch (chunks_per_lane(a.n)) {
 #define GL_NORM(C)                                                                              \
-  hipExtLaunchKernelGGL((rmsnorm_bwd_kernel<IO, C>), grid, block, 0, st, t.start(), t.stop(), 0, \
+  GL_LAUNCH(t, (rmsnorm_bwd_kernel<IO, C>), grid, block, 0, st, \
                         a)
       case 1: GL_NORM(1); break;
       case 2: GL_NORM(2); break;

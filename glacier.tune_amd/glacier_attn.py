@@ -230,6 +230,117 @@ def kernel_names() -> list[str]:
     return [L.glacier_attn_kernel_name(i).decode() for i in range(L.glacier_attn_kernel_count())]
 
 
+def _need(t, name, shape, dtype=None, like=None):
+    """Checks a device tensor against what the descriptor promises the kernels
+    (shape, dtype, contiguity, device) before its pointer crosses the ABI: a
+    mismatched tensor would otherwise become an out-of-bounds device access.
+    `like` gives the dtype and device of a reference tensor."""
+    if t is None:
+        raise TypeError(f"{name} is required")
+    if tuple(t.shape) != tuple(shape):
+        raise TypeError(f"{name} must have shape {tuple(shape)}, got {tuple(t.shape)}")
+    want = like.dtype if like is not None else dtype
+    if want is not None and t.dtype != want:
+        raise TypeError(f"{name} must be {want}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise TypeError(f"{name} must be contiguous")
+
+
+def _on_gpu(*named):
+    """Every given (name, tensor) on the GPU, on the first one's device."""
+    dev = None
+    for name, t in named:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise TypeError(f"{name} must be a GPU tensor")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise TypeError(f"{name} must be on {dev}, got {t.device}")
+
+
+def check_forward_args(q, k, v, out=None, lse=None, q_rot=None, k_rot=None):
+    """The forward's tensors: q [T,Hq,D], k and v [T,Hkv,D] of q's dtype;
+    out and q_rot like q, k_rot like k, lse float32 [Hq,T]."""
+    import torch
+
+    if q.dim() != 3 or k.dim() != 3:
+        raise TypeError("q must be [T, Hq, D] and k [T, Hkv, D]")
+    T, hq, d = q.shape
+    hkv = k.shape[1]
+    _need(q, "q", (T, hq, d), like=None, dtype=q.dtype)
+    _need(k, "k", (T, hkv, d), like=q)
+    _need(v, "v", (T, hkv, d), like=q)
+    for t, name, shape in ((out, "out", (T, hq, d)), (q_rot, "q_rot", (T, hq, d)),
+                           (k_rot, "k_rot", (T, hkv, d))):
+        if t is not None:
+            _need(t, name, shape, like=q)
+    if lse is not None:
+        _need(lse, "lse", (hq, T), dtype=torch.float32)
+    _on_gpu(("q", q), ("k", k), ("v", v), ("out", out), ("lse", lse), ("q_rot", q_rot),
+            ("k_rot", k_rot))
+
+
+def check_backward_args(d_out, q_rot, k_rot, v, out, lse, dq=None, dk=None, dv=None):
+    """The backward's tensors: d_out, q_rot, out, dq [T,Hq,D]; k_rot, v, dk,
+    dv [T,Hkv,D], all of q_rot's dtype; lse float32 [Hq,T]."""
+    import torch
+
+    if q_rot.dim() != 3 or k_rot.dim() != 3:
+        raise TypeError("q_rot must be [T, Hq, D] and k_rot [T, Hkv, D]")
+    T, hq, d = q_rot.shape
+    hkv = k_rot.shape[1]
+    _need(q_rot, "q_rot", (T, hq, d), dtype=q_rot.dtype)
+    for t, name, shape in ((d_out, "d_out", (T, hq, d)), (out, "out", (T, hq, d)),
+                           (k_rot, "k_rot", (T, hkv, d)), (v, "v", (T, hkv, d)),
+                           (dq, "dq", (T, hq, d)), (dk, "dk", (T, hkv, d)), (dv, "dv", (T, hkv, d))):
+        if t is not None or name in ("d_out", "out", "k_rot", "v"):
+            _need(t, name, shape, like=q_rot)
+    _need(lse, "lse", (hq, T), dtype=torch.float32)
+    _on_gpu(("q_rot", q_rot), ("d_out", d_out), ("out", out), ("k_rot", k_rot), ("v", v),
+            ("lse", lse), ("dq", dq), ("dk", dk), ("dv", dv))
+
+
+def check_proj_args(x, projs, rank, backward):
+    """x [T, in]; per projection w [out, in] of x's dtype, float32 bias
+    [out], lora a [in, rank], b [rank, out], grad_a/grad_b like a/b, and y
+    (forward) or dy (backward) [T, out] of x's dtype."""
+    import torch
+
+    if x.dim() != 2:
+        raise TypeError("x must be [T, in]")
+    T, n_in = x.shape
+    _need(x, "x", (T, n_in), dtype=x.dtype)
+    for i, pr in enumerate(projs):
+        w = pr.get("w")
+        if w is None or w.dim() != 2:
+            raise TypeError(f"proj[{i}].w must be a [out, in] tensor")
+        n_out = w.shape[0]
+        _need(w, f"proj[{i}].w", (n_out, n_in), like=x)
+        f32 = {"bias": (n_out,), "a": (n_in, rank), "b": (rank, n_out),
+               "grad_a": (n_in, rank), "grad_b": (rank, n_out)}
+        for key, shape in f32.items():
+            if pr.get(key) is not None:
+                _need(pr[key], f"proj[{i}].{key}", shape, dtype=torch.float32)
+        io = "dy" if backward else "y"
+        if backward or pr.get(io) is not None:
+            _need(pr.get(io), f"proj[{i}].{io}", (T, n_out), like=x)
+    _on_gpu(("x", x), *[(f"proj[{i}].{key}", pr.get(key)) for i, pr in enumerate(projs)
+                        for key in ("w", "bias", "a", "b", "grad_a", "grad_b", "y", "dy")])
+
+
+def check_norm_args(x, weight, d_weight=None):
+    """weight (and d_weight) float32 [n] for x [rows, n]."""
+    import torch
+
+    n = x.shape[1]
+    _need(weight, "weight", (n,), dtype=torch.float32)
+    if d_weight is not None:
+        _need(d_weight, "d_weight", (n,), dtype=torch.float32)
+    _on_gpu(("x", x), ("weight", weight), ("d_weight", d_weight))
+
+
 class GpuAttentionEngine:
     """One library context: a device, a stream and grow-only scratch."""
 
@@ -331,11 +442,10 @@ class GpuAttentionEngine:
         import torch
 
         prec = self.precision if precision is None else precision
+        check_forward_args(q, k, v, out, lse if save else None, q_rot if save else None,
+                           k_rot if save else None)
         T, hq, d = q.shape
         hkv = k.shape[1]
-        for t in (q, k, v):
-            if not t.is_contiguous() or t.dtype != q.dtype or not t.is_cuda:
-                raise TypeError("q, k, v must be contiguous GPU tensors of one dtype")
         io = self._io_of(q)
         out = torch.empty_like(q) if out is None else out
         if save:
@@ -357,11 +467,9 @@ class GpuAttentionEngine:
         import torch
 
         prec = self.precision if precision is None else precision
+        check_backward_args(d_out, q_rot, k_rot, v, out, lse, dq, dk, dv)
         T, hq, d = q_rot.shape
         hkv = k_rot.shape[1]
-        for t in (d_out, q_rot, k_rot, v, out):
-            if not t.is_contiguous() or t.dtype != q_rot.dtype or not t.is_cuda:
-                raise TypeError("backward tensors must be contiguous GPU tensors of one dtype")
         io = self._io_of(q_rot)
         dq = torch.empty_like(q_rot) if dq is None else dq
         dk = torch.empty_like(k_rot) if dk is None else dk
@@ -374,9 +482,44 @@ class GpuAttentionEngine:
                                             self._ptr(dk), self._ptr(dv)))
         return dq, dk, dv
 
+    def bind_step(self, fwd, bwd, rope_freq_base, precision=None, cu_seqlens=None):
+        """A forward + backward on fixed tensors with every argument checked
+        and converted once: returns step(), which enqueues glacier_attn_forward
+        then glacier_attn_backward on torch's current stream (bound now) with
+        the prepared arguments.  fwd = dict(q, k, v, out, lse, q_rot, k_rot),
+        bwd = dict(d_out, dq, dk, dv) (q_rot, k_rot, v, out, lse from fwd).
+        The tensors must stay alive and in place while step() is used."""
+        prec = self.precision if precision is None else precision
+        q, k, v = fwd["q"], fwd["k"], fwd["v"]
+        check_forward_args(q, k, v, fwd["out"], fwd["lse"], fwd["q_rot"], fwd["k_rot"])
+        check_backward_args(bwd["d_out"], fwd["q_rot"], fwd["k_rot"], v, fwd["out"], fwd["lse"],
+                            bwd["dq"], bwd["dk"], bwd["dv"])
+        T, hq, d = q.shape
+        desc, keep = self._desc(T, hq, k.shape[1], d, rope_freq_base, prec, self._io_of(q),
+                                cu_seqlens)
+        self._bind_stream()
+        L, p, h, dp = load(), self._ptr, self._h, ctypes.byref(desc)
+        fa = (h, dp, p(q), p(k), p(v), p(fwd["out"]), p(fwd["lse"]), p(fwd["q_rot"]),
+              p(fwd["k_rot"]))
+        ba = (h, dp, p(bwd["d_out"]), p(fwd["q_rot"]), p(fwd["k_rot"]), p(v), p(fwd["out"]),
+              p(fwd["lse"]), p(bwd["dq"]), p(bwd["dk"]), p(bwd["dv"]))
+        f, b = L.glacier_attn_forward, L.glacier_attn_backward
+
+        def step():
+            rc = f(*fa)
+            if rc != OK:
+                _check(rc)
+            rc = b(*ba)
+            if rc != OK:
+                _check(rc)
+
+        step._keep = (desc, keep)  # the descriptor and cu_seqlens outlive the calls
+        return step
+
     # ---- projections with LoRA adapters (device tensors) ------------------
     @staticmethod
     def _proj_array(projs, x, rank, backward):
+        check_proj_args(x, projs, rank, backward)
         arr = (LoraProj * len(projs))()
         p = GpuAttentionEngine._ptr
         for i, pr in enumerate(projs):
@@ -471,6 +614,7 @@ class GpuAttentionEngine:
         import torch
 
         desc = self._norm_desc(x, eps)
+        check_norm_args(x, weight)
         for t, name in ((delta, "delta"), (x1, "x1"), (y, "y")):
             self._like(t, x, name)
         y = torch.empty_like(x) if y is None else y
@@ -489,6 +633,9 @@ class GpuAttentionEngine:
         import torch
 
         desc = self._norm_desc(x, eps)
+        check_norm_args(x, weight, d_weight)
+        if dy is None:
+            raise TypeError("dy is required")
         for t, name in ((dy, "dy"), (d_residual, "d_residual"), (dx, "dx")):
             self._like(t, x, name)
         dx = torch.empty_like(x) if dx is None else dx

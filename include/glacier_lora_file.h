@@ -62,7 +62,11 @@ int glacier_lora_open(const char *path, glacier_lora_header *header, glacier_lor
 
 /* The next record's name (NUL-terminated; name_cap must fit it) and dims.
  * Each record must then be consumed with glacier_lora_read before the next
- * call.  INVALID_ARGUMENT after the last record. */
+ * call.  INVALID_ARGUMENT after the last record.  A name_cap too small for
+ * the name gives INVALID_ARGUMENT with the needed size in the error text and
+ * leaves the reader at the record's start, so a retry with a larger buffer
+ * reads the same record.  A malformed or truncated record gives
+ * GLACIER_LORA_ERR_DATA, and so does every later next/read on the reader. */
 int glacier_lora_next(glacier_lora_reader *reader, char *name, int32_t name_cap, int32_t *dim0,
                       int32_t *dim1);
 

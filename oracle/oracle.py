@@ -36,6 +36,15 @@ def build() -> None:
     subprocess.run(["make", "-s", "-C", _HERE], check=True)
 
 
+def use_library(path: str) -> None:
+    """Loads the oracle from another build of the same sources (bench.py's
+    -march=native copy for the timed CPU baseline) in place of liboracle.so."""
+    global _lib, _LIB_PATH
+    _LIB_PATH = path
+    _lib = None
+    lib()
+
+
 def lib():
     global _lib
     if _lib is None:

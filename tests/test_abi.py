@@ -246,3 +246,54 @@ def test_lmhead_argument_errors_come_before_any_device_work():
     assert rc == ga.ERR_INVALID_ARGUMENT and "ctx" in msg
     rc, msg = _lmhead_rc()
     assert rc == ga.ERR_INVALID_ARGUMENT and "ctx" in msg
+
+
+def test_python_front_end_checks_device_tensors_before_the_abi():
+    """Every tensor whose pointer the front end passes is checked against the
+    shapes the descriptor promises (shape, dtype, contiguity before device), so
+    a mismatched tensor raises TypeError instead of reaching a kernel as an
+    out-of-bounds access.  CPU tensors with the wrong shape or dtype show the
+    shape/dtype checks; the device check comes last."""
+    import torch
+
+    T, hq, hkv, d = 8, 4, 2, 64
+    q = torch.zeros(T, hq, d, dtype=torch.bfloat16)
+    k = torch.zeros(T, hkv, d, dtype=torch.bfloat16)
+    lse = torch.zeros(hq, T)
+
+    def raises(fn, text):
+        with pytest.raises(TypeError, match=text):
+            fn()
+
+    raises(lambda: ga.check_forward_args(q, k, k[:, :1]), "v must have shape")
+    raises(lambda: ga.check_forward_args(q, k, k.float()), "v must be torch.bfloat16")
+    raises(lambda: ga.check_forward_args(q, k, k, out=q[:4]), "out must have shape")
+    raises(lambda: ga.check_forward_args(q, k, k, lse=lse.T.contiguous()), "lse must have shape")
+    raises(lambda: ga.check_forward_args(q, k, k, lse=lse.bfloat16()), "lse must be torch.float32")
+    raises(lambda: ga.check_forward_args(q, k, k, k_rot=q), "k_rot must have shape")
+    raises(lambda: ga.check_forward_args(q, k, k, q_rot=q.transpose(0, 1).contiguous().transpose(0, 1)),
+           "q_rot must be contiguous")
+    raises(lambda: ga.check_forward_args(q, k, k), "must be a GPU tensor")  # all shapes fine
+    raises(lambda: ga.check_backward_args(q, q, k, k, q, lse[:, :4]), "lse must have shape")
+    raises(lambda: ga.check_backward_args(q, q, k, k, q, lse.double()), "lse must be torch.float32")
+    raises(lambda: ga.check_backward_args(q, q, k, k, q[:, :2], lse), "out must have shape")
+    raises(lambda: ga.check_backward_args(q, q, k, k, q, lse, dk=q), "dk must have shape")
+    raises(lambda: ga.check_backward_args(q.float(), q, k, k, q, lse), "d_out must be torch.bfloat16")
+
+    x = torch.zeros(T, 32, dtype=torch.bfloat16)
+    w = torch.zeros(16, 32, dtype=torch.bfloat16)
+    good = {"w": w, "a": torch.zeros(32, 4), "b": torch.zeros(4, 16), "bias": torch.zeros(16),
+            "dy": torch.zeros(T, 16, dtype=torch.bfloat16)}
+    raises(lambda: ga.check_proj_args(x, [dict(good, a=torch.zeros(32, 8))], 4, True), r"proj\[0\].a must have shape")
+    raises(lambda: ga.check_proj_args(x, [dict(good, b=torch.zeros(16, 4))], 4, True), r"proj\[0\].b must have shape")
+    raises(lambda: ga.check_proj_args(x, [dict(good, bias=torch.zeros(15))], 4, True), r"proj\[0\].bias must have shape")
+    raises(lambda: ga.check_proj_args(x, [dict(good, grad_a=torch.zeros(32, 4, dtype=torch.float64))], 4, True),
+           r"proj\[0\].grad_a must be torch.float32")
+    raises(lambda: ga.check_proj_args(x, [dict(good, w=torch.zeros(16, 31, dtype=torch.bfloat16))], 4, True),
+           r"proj\[0\].w must have shape")
+    raises(lambda: ga.check_proj_args(x, [dict(good, dy=torch.zeros(T, 17, dtype=torch.bfloat16))], 4, True),
+           r"proj\[0\].dy must have shape")
+    raises(lambda: ga.check_proj_args(x, [dict(good, dy=None)], 4, True), r"proj\[0\].dy is required")
+    raises(lambda: ga.check_norm_args(x, torch.zeros(31)), "weight must have shape")
+    raises(lambda: ga.check_norm_args(x, torch.zeros(32), torch.zeros(32, dtype=torch.bfloat16)),
+           "d_weight must be torch.float32")

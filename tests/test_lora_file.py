@@ -126,3 +126,69 @@ def test_rank_zero_allows_any_alpha_and_bad_calls_are_rejected(tmp_path):
     assert hdr["rank"] == 0 and got == []
     with pytest.raises(ga.InvalidArgument):
         ga.lora_save(tmp_path / "x.bin", 1, 2, 4.0, [("a", np.zeros((0, 2), np.float32))])
+
+
+def _reader(path):
+    import ctypes
+
+    L = ga.load()
+    hdr = ga.LoraHeader()
+    r = ctypes.c_void_p()
+    assert L.glacier_lora_open(os.fsencode(path), ctypes.byref(hdr), ctypes.byref(r)) == ga.OK
+    return L, r
+
+
+def test_retry_after_a_too_small_name_buffer_reads_the_same_record(tmp_path):
+    """A name buffer that is too small leaves the reader at the record's start:
+    the retry the error text invites reads the record, and the rest follows."""
+    import ctypes
+
+    ts = _tensors(seed=4)
+    long_name = "blk.0." + "x" * 300 + ".lora_a.weight"  # two-byte length prefix
+    ts[0] = (long_name, ts[0][1])
+    path = tmp_path / "adapter_model.bin"
+    ga.lora_save(path, 1, 4, 8.0, ts)
+    L, r = _reader(path)
+    try:
+        d0, d1 = ctypes.c_int32(), ctypes.c_int32()
+        small = ctypes.create_string_buffer(16)
+        rc = L.glacier_lora_next(r, small, len(small), ctypes.byref(d0), ctypes.byref(d1))
+        assert rc == ga.ERR_INVALID_ARGUMENT
+        need = int(L.glacier_attn_last_error().decode().rsplit("needs ", 1)[1].split()[0])
+        assert need == len(long_name) + 1
+        for name, want in ts:
+            buf = ctypes.create_string_buffer(need)
+            assert L.glacier_lora_next(r, buf, need, ctypes.byref(d0), ctypes.byref(d1)) == ga.OK
+            assert buf.value.decode() == name and (d0.value, d1.value) == want.shape
+            got = np.empty(want.shape, np.float32)
+            assert L.glacier_lora_read(r, got.ctypes.data_as(ctypes.c_void_p), 0) == ga.OK
+            np.testing.assert_array_equal(got, want)
+    finally:
+        L.glacier_lora_close(r)
+
+
+@pytest.mark.parametrize("cut", ["name", "dims", "payload"])
+def test_a_malformed_record_fails_every_later_call(tmp_path, cut):
+    """After a truncated or malformed record the reader stays failed: no later
+    call reads the rest of the (untrusted) bytes as new records."""
+    import ctypes
+
+    ts = _tensors(seed=5)
+    raw = _file(1, 4, 8.0, [_record(n, a) for n, a in ts])
+    first = len(_file(1, 4, 8.0, [])) + len(_record(*ts[0]))
+    name_len = len(_dotnet_string(ts[1][0]))
+    end = {"name": first + 3, "dims": first + name_len + 2, "payload": first + name_len + 8 + 5}[cut]
+    path = tmp_path / "adapter_model.bin"
+    path.write_bytes(raw[:end])
+    L, r = _reader(path)
+    try:
+        d0, d1 = ctypes.c_int32(), ctypes.c_int32()
+        buf = ctypes.create_string_buffer(256)
+        assert L.glacier_lora_next(r, buf, 256, ctypes.byref(d0), ctypes.byref(d1)) == ga.OK
+        assert L.glacier_lora_read(r, None, 0) == ga.OK
+        assert L.glacier_lora_next(r, buf, 256, ctypes.byref(d0), ctypes.byref(d1)) == ga.ERR_DATA
+        for _ in range(2):
+            assert L.glacier_lora_next(r, buf, 256, ctypes.byref(d0), ctypes.byref(d1)) == ga.ERR_DATA
+            assert L.glacier_lora_read(r, None, 0) == ga.ERR_DATA
+    finally:
+        L.glacier_lora_close(r)

@@ -112,6 +112,14 @@ def test_rmsnorm_weight_gradient_aliasing_repeatability_and_empty(eng):
     eng.rmsnorm_backward(dyin, xd, wd, EPS, dx=dyin)
     torch.cuda.synchronize()
     assert torch.equal(xin, y) and torch.equal(dyin, dx1)
+    # in place with the weight gradient: d_weight is formed from dy as passed
+    # in, not from the dx that overwrote it
+    dyin = dyd.clone()
+    dw2 = torch.zeros(n, device="cuda:0")
+    eng.rmsnorm_backward(dyin, xd, wd, EPS, dx=dyin, d_weight=dw2)
+    torch.cuda.synchronize()
+    assert torch.equal(dyin, dx1)
+    assert oracle.max_rel_err(dw2.cpu().numpy(), dw_ref) <= FP32_GATE
     # empty
     e = torch.empty((0, n), device="cuda:0")
     _, ye = eng.rmsnorm_forward(e, wd, EPS)
