@@ -62,8 +62,10 @@ CONFIGS = {
 
 # Algorithmic FLOPs per unmasked (query, key, head) triple, per kernel: the
 # forward does QK^T and PV (4 D); the backward kernel dP, dV, dK and dQ (8 D);
-# rope_k and the dK/dV head reduction are credited with none.  Sum: 12 D.
-FLOPS_PER_PAIR = {"attn_fwd": 4, "attn_bwd": 8, "rope_k": 0, "attn_bwd_reduce": 0}
+# rope_k, the backward's row stats and the dK/dV head reduction are credited
+# with none.  Sum: 12 D.
+FLOPS_PER_PAIR = {"attn_fwd": 4, "attn_bwd": 8, "rope_k": 0, "attn_bwd_reduce": 0,
+                  "attn_bwd_stats": 0}
 
 
 # HBM bytes per launch of each kernel at qwen7b_s512, from two rocprofv3 --pmc
@@ -556,7 +558,11 @@ def main():
     try:
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
+            if bound is not None:
+                bound.rebind()  # enqueue on the capture stream
             step()
+        if bound is not None:
+            bound.rebind()
         for _ in range(3):
             graph.replay()
         torch.cuda.synchronize()

@@ -25,12 +25,13 @@ CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libglacier_attn.so")
 OBJDIR = os.path.join(HERE, "_build")
 
-# source -> extra hipcc flags.  attn_fwd.hip: the MFMAs the compiler emits
-# write VGPRs (their results feed VALU code); its accumulators are pinned to
-# AGPRs by inline assembly.
+# source -> extra hipcc flags.  attn_fwd.hip, attn_bwd.hip: the MFMAs the
+# compiler emits write VGPRs (their results feed VALU code); the long-lived
+# accumulators are pinned to AGPRs by inline assembly.
 SOURCES = {
     "attn_kernels.hip": (),
     "attn_fwd.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form"),
+    "attn_bwd.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form"),
     "blas_lt.cpp": (),
     "proj_lora.hip": (),
     "rmsnorm.hip": (),

@@ -905,7 +905,16 @@ hipError_t forward_impl(const FwdLaunch& a, hipStream_t st, KernelTimer* tm) {
 template <typename IO, typename T, int D>
 hipError_t backward_impl(const BwdLaunch& a, hipStream_t st, KernelTimer* tm) {
   const int ratio = a.n_heads_q / a.n_heads_kv;
-  {
+  bool rows32 = false;
+  if constexpr (std::is_same<IO, bf16>::value) {
+    const long long min_pairs = D == 128 ? kBwdRows32MinPairsD128 : kBwdRows32MinPairsD64;
+    rows32 = a.variant == kBwdRows32 || (a.variant == kBwdAuto && a.pairs >= min_pairs);
+  }
+  if (rows32) {
+    // bf16 tensors, long sequences: the 32-row-wave kernel fed by LDS DMA
+    // (attn_bwd.hip)
+    GL_CHECK(launch_bwd2<D>(a, st, tm));
+  } else {
     auto fn = attn_bwd_kernel<IO, T, D>;
     constexpr size_t lds = bwd_lds<T, D>();
     GL_CHECK(allow_lds(fn, lds));

@@ -37,7 +37,8 @@ enum KernelId : int {
   kKernReduce = 3,
   kKernNormFwd = 4,  // rmsnorm.hip
   kKernNormBwd = 5,
-  kKernCount = 6,
+  kKernBwdStats = 6,  // attn_bwd.hip: row stats before the bf16 backward
+  kKernCount = 7,
 };
 
 // Optional per-kernel hipEvent timing on the launch stream.
@@ -136,17 +137,29 @@ struct FwdLaunch {
   const float *cos_t, *sin_t;    // [max len][D/2]
 };
 
+// Backward kernel choice for bf16 tensors.  kBwdAuto takes the 32-row-wave
+// kernel (attn_bwd.hip) once a head's causal pair count reaches the measured
+// break-even below, the 16-row-wave kernel (attn_kernels.hip) under it: the
+// 32-row kernel's extra row-stats launch and larger per-workgroup fixed
+// costs only pay off on long sequences.
+enum BwdVariant : int { kBwdAuto = 0, kBwdRows16 = 1, kBwdRows32 = 2 };
+constexpr long long kBwdRows32MinPairsD128 = 1024LL * 1025 / 2;  // one S=1024 sequence
+constexpr long long kBwdRows32MinPairsD64 = 2048LL * 2049 / 2;   // one S=2048 sequence
+
 struct BwdLaunch {
   int precision;
   bool io_bf16;
   bool single_seq;               // one sequence: tile order is computed in-kernel
+  int variant;                   // BwdVariant
   int head_dim, n_heads_q, n_heads_kv, total_tokens;
   int n_tiles;
+  long long pairs;               // causal (query, key) pairs per head: sum L (L + 1) / 2
   float scale_log2, scale;
   const void *d_out, *q_rot, *k_rot, *v, *out;
   const float* lse;
   void *dq, *dk, *dv;
   void *wk, *wv;                 // per-query-head dK/dV partials [T][Hq][D], tensors' dtype
+  void* stats;                   // bf16 tensors: [Hq][T] float2 (-lse log2 e, dO . O)
   const TileDesc* tiles_bwd;     // [2 n_tiles] dK/dV and dQ tiles, longest expected first
   const int32_t* pos_of;
   const float *cos_t, *sin_t;
@@ -161,6 +174,11 @@ size_t compute_elem_size(int precision, bool io_bf16);
 // (__bf16 or float); D: 64 or 128.
 template <typename IO, int D>
 hipError_t launch_fwd_bf16(const FwdLaunch& a, hipStream_t st, KernelTimer* tm);
+
+// The bf16-tensor backward (attn_bwd.hip): the row-stats kernel and the
+// dK/dV + dQ kernel, writing dq and the per-head dK/dV partials; D: 64 or 128.
+template <int D>
+hipError_t launch_bwd2(const BwdLaunch& a, hipStream_t st, KernelTimer* tm);
 
 // Kernels whose dynamic LDS exceeds 64 KB must say so before their launch.
 template <typename F>

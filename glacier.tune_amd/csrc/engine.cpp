@@ -12,6 +12,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <memory>
@@ -95,6 +96,7 @@ struct Shape {
 // Tile lists of one sequence layout, resident on the device.
 struct TileSet {
   int n_tiles = 0, max_len = 0;
+  long long pairs = 0;  // causal (query, key) pairs per head
   DeviceBuffer tiles;  // [3 n_tiles] TileDesc: fwd order, then the backward order
   DeviceBuffer pos;    // [T] int32
 };
@@ -113,6 +115,16 @@ class GpuAttentionEngine {
                std::to_string(n) + " devices)");
     check_hip(hipSetDevice(device_), "hipSetDevice");
     check_hip(hipStreamCreateWithFlags(&own_stream_, hipStreamNonBlocking), "hipStreamCreate");
+    // GLACIER_ATTN_BWD=rows16|rows32 pins the bf16 backward kernel (tests
+    // cover both on every shape); unset or "auto" picks by sequence length.
+    if (const char* v = std::getenv("GLACIER_ATTN_BWD")) {
+      const std::string m(v);
+      if (m == "rows16") bwd_variant_ = kBwdRows16;
+      else if (m == "rows32") bwd_variant_ = kBwdRows32;
+      else if (m != "auto" && !m.empty())
+        fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT,
+             "GLACIER_ATTN_BWD must be auto, rows16 or rows32, not " + m);
+    }
   }
 
   ~GpuAttentionEngine() {
@@ -194,11 +206,13 @@ class GpuAttentionEngine {
     a.precision = s.precision;
     a.io_bf16 = s.io_bf16;
     a.single_seq = s.cu.size() == 2;
+    a.variant = bwd_variant_;
     a.head_dim = s.head_dim;
     a.n_heads_q = s.n_heads_q;
     a.n_heads_kv = s.n_heads_kv;
     a.total_tokens = s.total_tokens;
     a.n_tiles = ts.n_tiles;
+    a.pairs = ts.pairs;
     a.scale = 1.0f / std::sqrt(static_cast<float>(s.head_dim));
     a.scale_log2 = kLog2e * a.scale;
     a.d_out = d_out; a.q_rot = q_rot; a.k_rot = k_rot; a.v = v; a.out = out;
@@ -209,6 +223,10 @@ class GpuAttentionEngine {
     const size_t wsz = s.io_bf16 ? 2 : 4;
     a.wk = wk_.ensure(T * Hq * D * wsz, "dK partials");
     a.wv = wv_.ensure(T * Hq * D * wsz, "dV partials");
+    // bf16 tensors: the row stats [Hq][T] float2, plus 64 entries of padding
+    // (the kernel reads them in blocks of 4 rows; rows past a sequence's end
+    // are masked out, so the padding's contents never reach a result)
+    if (s.io_bf16) a.stats = stats_.ensure((T * Hq + 64) * 2 * sizeof(float), "row stats");
     const TileDesc* t = static_cast<const TileDesc*>(ts.tiles.ptr);
     a.tiles_bwd = t + ts.n_tiles;
     a.pos_of = static_cast<const int32_t*>(ts.pos.ptr);
@@ -425,6 +443,7 @@ class GpuAttentionEngine {
       for (int t = 0; t < nt; ++t) nat.push_back(TileDesc{tok0, len, t, 0});
       for (int i = 0; i < len; ++i) pos[tok0 + i] = i;
       ts->max_len = std::max(ts->max_len, len);
+      ts->pairs += static_cast<long long>(len) * (len + 1) / 2;
     }
     ts->n_tiles = static_cast<int>(nat.size());
     if (ts->n_tiles > 65535)
@@ -500,7 +519,8 @@ class GpuAttentionEngine {
   int rope_len_ = 0, rope_dim_ = 0;
   float rope_base_ = 0.0f;
   // device-path scratch
-  DeviceBuffer kc_, vc_, wk_, wv_;
+  DeviceBuffer kc_, vc_, wk_, wv_, stats_;
+  int bwd_variant_ = kBwdAuto;
   // projection scratch and the hipBLASLt handle (created on first use)
   DeviceBuffer yf_, dxf_, lowrank_, part_;
   DeviceBuffer rstd_, dyw_;  // RMSNorm backward row scales, dy copy (weight gradient)
@@ -694,6 +714,7 @@ int guarded(F&& f) {
 
 const char* const kKernelNames[kKernCount] = {
     "rope_k", "attn_fwd", "attn_bwd", "attn_bwd_reduce", "rmsnorm_fwd", "rmsnorm_bwd",
+    "attn_bwd_stats",
 };
 
 }  // namespace

@@ -506,6 +506,8 @@ class GpuAttentionEngine:
         f, b = L.glacier_attn_forward, L.glacier_attn_backward
 
         def step():
+            """Enqueues on the stream bound last (bind_step binds torch's
+            current stream; rebind() binds it again, e.g. under capture)."""
             rc = f(*fa)
             if rc != OK:
                 _check(rc)
@@ -514,6 +516,7 @@ class GpuAttentionEngine:
                 _check(rc)
 
         step._keep = (desc, keep)  # the descriptor and cu_seqlens outlive the calls
+        step.rebind = self._bind_stream
         return step
 
     # ---- projections with LoRA adapters (device tensors) ------------------

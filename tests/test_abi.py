@@ -82,7 +82,7 @@ def test_device_descriptor_validation():
 def test_kernel_names_and_last_error_reset():
     names = ga.kernel_names()
     assert names == ["rope_k", "attn_fwd", "attn_bwd", "attn_bwd_reduce", "rmsnorm_fwd",
-                     "rmsnorm_bwd"]
+                     "rmsnorm_bwd", "attn_bwd_stats"]
     L = ga.load()
     assert L.glacier_attn_kernel_name(99) is None
     _fwd_host_rc(8, 3, 2, 64)

@@ -12,6 +12,7 @@ configs[4] (Llama-3-8B B=2 S=2048) against a float32 torch reference on the
 GPU (the oracle would take minutes there), plus edge cases.
 """
 import functools
+import os
 import sys
 
 import numpy as np
@@ -40,6 +41,30 @@ def engines():
     yield {ga.PREC_FP32: e32, ga.PREC_BF16: e16}
     e32.close()
     e16.close()
+
+
+BWD_KERNELS = ("rows16", "rows32")
+
+
+@pytest.fixture(scope="module")
+def bf16_kernels():
+    """bf16-mode engines pinned to each backward kernel for bf16 tensors
+    (GLACIER_ATTN_BWD is read when an engine is created)."""
+    assert torch.cuda.is_available(), "GPU tests need a ROCm GPU"
+    made = {}
+    old = os.environ.get("GLACIER_ATTN_BWD")
+    try:
+        for name in BWD_KERNELS:
+            os.environ["GLACIER_ATTN_BWD"] = name
+            made[name] = ga.GpuAttentionEngine(0, ga.PREC_BF16)
+    finally:
+        if old is None:
+            os.environ.pop("GLACIER_ATTN_BWD", None)
+        else:
+            os.environ["GLACIER_ATTN_BWD"] = old
+    yield made
+    for e in made.values():
+        e.close()
 
 
 def make_inputs(S, Hq, Hkv, D, seed=1, bf16=False):
@@ -131,10 +156,49 @@ def test_bf16_device_tensors_match_oracle(engines, name):
     assert all(e <= BF16_GATE for e in err.values()), err
 
 
-@pytest.mark.parametrize("S,Hq,Hkv,D", [
+@pytest.mark.parametrize("kernel", BWD_KERNELS)
+@pytest.mark.parametrize("name", list(CONFIGS))
+def test_bf16_device_tensors_each_backward_kernel(bf16_kernels, name, kernel):
+    S, Hq, Hkv, D, base = CONFIGS[name]
+    _say(f"[bf16 device io, {kernel} backward] {name}")
+    (q, k, v, dO), ref = oracle_case(S, Hq, Hkv, D, base, 1, True)
+    got = run_device(bf16_kernels[kernel], q, k, v, dO, base, torch.bfloat16)
+    err = errors(got, ref)
+    _say(f"  errors {err}")
+    assert all(e <= BF16_GATE for e in err.values()), err
+
+
+RAGGED = [
     (1, 2, 1, 64), (2, 4, 4, 128), (17, 7, 1, 128), (63, 4, 2, 64), (64, 2, 2, 64),
     (65, 6, 3, 128), (100, 8, 2, 64), (129, 14, 2, 128), (200, 2, 1, 64),
-])
+]
+
+
+@pytest.mark.parametrize("S,Hq,Hkv,D", RAGGED)
+@pytest.mark.parametrize("kernel", BWD_KERNELS)
+def test_bf16_device_ragged_shapes_each_backward_kernel(bf16_kernels, S, Hq, Hkv, D, kernel):
+    """Partial tiles, one-token sequences and every GQA ratio through both
+    backward kernels of bf16 tensors."""
+    base = 1.0e4
+    _say(f"[bf16 device shape, {kernel}] S={S} Hq={Hq} Hkv={Hkv} D={D}")
+    (q, k, v, dO), ref = oracle_case(S, Hq, Hkv, D, base, 3, True)
+    got = run_device(bf16_kernels[kernel], q, k, v, dO, base, torch.bfloat16)
+    err = errors(got, ref)
+    assert all(e <= BF16_GATE for e in err.values()), err
+
+
+@pytest.mark.parametrize("kernel", BWD_KERNELS)
+def test_bf16_device_backward_is_bitwise_repeatable(bf16_kernels, kernel):
+    S, Hq, Hkv, D, base = 300, 14, 2, 128, 1.0e6
+    _say(f"[determinism, bf16 device, {kernel}]")
+    q, k, v, dO = make_inputs(S, Hq, Hkv, D, 7, True)
+    a = run_device(bf16_kernels[kernel], q, k, v, dO, base, torch.bfloat16)
+    b = run_device(bf16_kernels[kernel], q, k, v, dO, base, torch.bfloat16)
+    for key in a:
+        assert np.array_equal(a[key], b[key]), key
+
+
+@pytest.mark.parametrize("S,Hq,Hkv,D", RAGGED)
 @pytest.mark.parametrize("prec", [ga.PREC_FP32, ga.PREC_BF16])
 def test_small_and_ragged_shapes(engines, S, Hq, Hkv, D, prec):
     base = 1.0e4
@@ -176,7 +240,7 @@ def test_recompute_and_backward_are_bitwise_repeatable(engines, prec):
         assert np.array_equal(a[key], b[key]), key
 
 
-def test_varlen_packed_batch_matches_oracle_per_segment(engines):
+def test_varlen_packed_batch_matches_oracle_per_segment(engines, bf16_kernels):
     """BASELINE configs[2] shape: 4 packed sequences, lengths U[64,512] (seed 5),
     block-diagonal causal mask, 7B heads, bf16."""
     Hq, Hkv, D, base = 28, 4, 128, 1.0e6
@@ -187,10 +251,11 @@ def test_varlen_packed_batch_matches_oracle_per_segment(engines):
     _say(f"[varlen] lens={lens.tolist()}")
     q, k, v, dO = make_inputs(T, Hq, Hkv, D, 9, True)
     ref = oracle.layer_fwd_bwd_varlen(q, k, v, dO, cu, base)
-    got = run_device(engines[ga.PREC_BF16], q, k, v, dO, base, torch.bfloat16, cu=cu)
-    err = errors(got, ref)
-    _say(f"  errors {err}")
-    assert all(e <= BF16_GATE for e in err.values()), err
+    for eng in (engines[ga.PREC_BF16], *bf16_kernels.values()):
+        got = run_device(eng, q, k, v, dO, base, torch.bfloat16, cu=cu)
+        err = errors(got, ref)
+        _say(f"  errors {err}")
+        assert all(e <= BF16_GATE for e in err.values()), err
     # fp32 device tensors with fp32 math on the same packing
     (q, k, v, dO) = make_inputs(T, Hq, Hkv, D, 9, False)
     ref = oracle.layer_fwd_bwd_varlen(q, k, v, dO, cu, base)
@@ -238,12 +303,13 @@ def torch_reference(q, k, v, dO, base, cu):
                 dv=vd.grad)
 
 
-@pytest.mark.parametrize("name,lens,Hq,Hkv,base", [
-    ("long_s4096", [4096], 28, 4, 1.0e6),
-    ("llama3_b2_s2048", [2048, 2048], 32, 8, 5.0e5),
+@pytest.mark.parametrize("name,lens,Hq,Hkv,D,base", [
+    ("long_s4096", [4096], 28, 4, 128, 1.0e6),
+    ("llama3_b2_s2048", [2048, 2048], 32, 8, 128, 5.0e5),
+    ("qwen05b_s2048", [2048], 14, 2, 64, 1.0e6),
+    ("long_and_ragged", [1100, 7, 1, 65, 64], 28, 4, 128, 1.0e6),
 ])
-def test_large_shapes_match_torch_fp32_reference(engines, name, lens, Hq, Hkv, base):
-    D = 128
+def test_large_shapes_match_torch_fp32_reference(engines, name, lens, Hq, Hkv, D, base):
     cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
     T = int(cu[-1])
     _say(f"[large] {name} T={T}")
