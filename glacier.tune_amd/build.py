@@ -32,6 +32,7 @@ SOURCES = {
     "attn_kernels.hip": (),
     "attn_fwd.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form"),
     "attn_bwd.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form"),
+    "attn_noalloc.hip": (),
     "blas_lt.cpp": (),
     "proj_lora.hip": (),
     "rmsnorm.hip": (),

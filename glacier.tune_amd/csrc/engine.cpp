@@ -29,6 +29,7 @@
 #include "blas_lt.hpp"
 #include "lmhead_launch.hpp"
 #include "lora_file.hpp"
+#include "noalloc.hpp"
 #include "norm_launch.hpp"
 #include "proj_launch.hpp"
 
@@ -93,6 +94,197 @@ struct Shape {
   std::vector<int32_t> cu;  // n_seqs + 1 offsets
 };
 
+// A validated call shape that points at the caller's cu_seqlens instead of
+// copying it (the allocation-free entry point builds no host containers).
+struct ShapeArgs {
+  int total_tokens = 0, n_seqs = 1;
+  const int32_t* cu = nullptr;  // nullptr: one sequence of total_tokens
+  int n_heads_q = 0, n_heads_kv = 0, head_dim = 0;
+  float rope_freq_base = 0.0f;
+  int precision = 0;
+  bool io_bf16 = false;
+  int max_len = 0;
+  int seq_start(int b) const { return cu != nullptr ? cu[b] : (b == 0 ? 0 : total_tokens); }
+};
+
+// Shape part of one backward launch.
+struct BwdCall {
+  int total_tokens, n_heads_q, n_heads_kv, head_dim, precision;
+  bool io_bf16, single_seq;
+  int n_tiles;
+  long long pairs;
+};
+
+// RoPE angle of pair i at position pos: the fp32 operations of
+// RoPEKernel.cs:64-68 (glibc powf, then cosf/sinf of pos * freq).
+inline float rope_freq(int i, int head_dim, float base) {
+  return 1.0f / powf(base, static_cast<float>(2 * i) / static_cast<float>(head_dim));
+}
+
+// Backward dK/dV and dQ tiles of one sequence layout in launch order, longest
+// expected first (list scheduling: the long tiles of both kinds start at once
+// and the short ones fill the tail).  The cost is linear in the tile pairs a
+// tile visits, with constants fitted to measured workgroup durations (D = 128,
+// units of 0.1 us); it only orders the launch.
+inline int bwd_tile_cost(int n_tiles_in_seq, int tile, int kind) {
+  return kind == 0 ? 63 + 16 * (n_tiles_in_seq - tile) : 53 + 12 * (tile + 1);
+}
+
+// ---- allocation-free backward: its buffers inside the fixed scratch -------
+constexpr int kNoAllocMaxSeqs = 1024;
+constexpr int kNoAllocMaxTokens = GLACIER_ATTN_MAX_SEQ_LEN;
+constexpr int kNoAllocMaxTiles = kNoAllocMaxTokens / kTile + kNoAllocMaxSeqs;
+constexpr int kNoAllocMaxCost = 63 + 16 * (kNoAllocMaxTokens / kTile);
+constexpr int kNoAllocRopeChunk = 16384;  // floats staged per table upload
+
+// What one device's scratch holds across calls: the RoPE tables and the tile
+// and position tables of the last sequence layout.
+struct NoAllocResident {
+  int rope_cap = 0, rope_dim = 0;
+  float rope_base = 0.0f;
+  size_t tiles_off = 0;  // 0: no tile table resident
+  int n_seqs = 0, total_tokens = 0;
+  int32_t cu[kNoAllocMaxSeqs + 1] = {};
+};
+
+std::mutex g_noalloc_mutex;  // guards the records and host staging below
+NoAllocResident g_noalloc[kNoAllocMaxDevices];
+TileDesc g_noalloc_tiles[2 * kNoAllocMaxTiles];
+int32_t g_noalloc_pos[kNoAllocMaxTokens];
+int32_t g_noalloc_count[kNoAllocMaxCost + 2];
+float g_noalloc_freq[512];  // head_dim / 2 (head_dim <= 1024, make_shape_args)
+float g_noalloc_stage[kNoAllocRopeChunk];
+
+size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+
+struct NoAllocBwd {
+  void *wk, *wv, *stats;
+  const TileDesc* tiles_bwd;
+  const int32_t* pos_of;
+  const float *cos_t, *sin_t;
+  int n_tiles;
+  long long pairs;
+};
+
+// Lays out one backward call inside the scratch at `base` on `device`:
+//   [cos table][sin table][dK/dV + dQ tile table][positions][row stats][dK partials][dV partials]
+// (each region 256-byte aligned).  The RoPE tables and the tile/position
+// tables are uploaded only when the call's head_dim, theta, longest sequence
+// or sequence layout differ from what the scratch holds; the upload first
+// waits for the whole device, since any earlier call may still read them.
+// Every other region is written by the call's own kernels before it is read.
+NoAllocBwd noalloc_bwd_workspace(int device, void* base, const ShapeArgs& s) {
+  if (s.n_seqs > kNoAllocMaxSeqs)
+    fail(GLACIER_ATTN_ERR_UNSUPPORTED, "the allocation-free backward takes at most " +
+                                           std::to_string(kNoAllocMaxSeqs) + " sequences per call");
+  if (s.total_tokens > kNoAllocMaxTokens)
+    fail(GLACIER_ATTN_ERR_UNSUPPORTED, "the allocation-free backward takes at most " +
+                                           std::to_string(kNoAllocMaxTokens) + " tokens per call");
+  const size_t T = s.total_tokens, Hq = s.n_heads_q, D = s.head_dim;
+  const int half = s.head_dim / 2;
+  int n_tiles = 0;
+  long long pairs = 0;
+  for (int b = 0; b < s.n_seqs; ++b) {
+    const int len = s.seq_start(b + 1) - s.seq_start(b);
+    n_tiles += (len + kTile - 1) / kTile;
+    pairs += static_cast<long long>(len) * (len + 1) / 2;
+  }
+  std::lock_guard<std::mutex> g(g_noalloc_mutex);
+  NoAllocResident& r = g_noalloc[device];
+  const bool rope_ok = r.rope_cap >= s.max_len && r.rope_dim == s.head_dim &&
+                       r.rope_base == s.rope_freq_base;
+  const int rope_cap = rope_ok ? r.rope_cap : (std::max(s.max_len, 1) + 255) / 256 * 256;
+  const size_t rope_bytes = align256(static_cast<size_t>(rope_cap) * half * sizeof(float));
+  const size_t off_tiles = 2 * rope_bytes;
+  const size_t off_pos = off_tiles + align256(2 * static_cast<size_t>(n_tiles) * sizeof(TileDesc));
+  const size_t off_stats = off_pos + align256(T * sizeof(int32_t));
+  const size_t stats_bytes = s.io_bf16 ? align256((T * Hq + 64) * 2 * sizeof(float)) : 0;
+  const size_t part = align256(T * Hq * D * (s.io_bf16 ? 2 : 4));
+  const size_t off_wk = off_stats + stats_bytes, off_wv = off_wk + part;
+  const size_t need = off_wv + part;
+  if (need > kNoAllocScratchBytes)
+    fail(GLACIER_ATTN_ERR_UNSUPPORTED,
+         "the allocation-free backward needs " + std::to_string(need) +
+             " bytes of scratch for this call; its fixed scratch holds " +
+             std::to_string(kNoAllocScratchBytes) + " (GLACIER_ATTN_NOALLOC_SCRATCH_BYTES)");
+  bool tiles_ok = r.tiles_off == off_tiles && r.n_seqs == s.n_seqs &&
+                  r.total_tokens == s.total_tokens;
+  for (int b = 0; tiles_ok && b <= s.n_seqs; ++b) tiles_ok = r.cu[b] == s.seq_start(b);
+  char* const sb = static_cast<char*>(base);
+  if (!rope_ok || !tiles_ok) {
+    check_hip(hipDeviceSynchronize(), "allocation-free backward: wait before a table update");
+    if (!rope_ok) {
+      r.rope_cap = 0;
+      for (int i = 0; i < half; ++i) g_noalloc_freq[i] = rope_freq(i, s.head_dim, s.rope_freq_base);
+      const int rows = kNoAllocRopeChunk / half;
+      for (int table = 0; table < 2; ++table) {
+        for (int p0 = 0; p0 < rope_cap; p0 += rows) {
+          const int p1 = std::min(rope_cap, p0 + rows);
+          for (int pos = p0; pos < p1; ++pos)
+            for (int i = 0; i < half; ++i) {
+              const float theta = static_cast<float>(pos) * g_noalloc_freq[i];
+              g_noalloc_stage[(pos - p0) * half + i] = table == 0 ? cosf(theta) : sinf(theta);
+            }
+          check_hip(hipMemcpy(sb + table * rope_bytes + static_cast<size_t>(p0) * half * sizeof(float),
+                              g_noalloc_stage, static_cast<size_t>(p1 - p0) * half * sizeof(float),
+                              hipMemcpyHostToDevice),
+                    "allocation-free backward: RoPE table upload");
+        }
+      }
+      r.rope_cap = rope_cap;
+      r.rope_dim = s.head_dim;
+      r.rope_base = s.rope_freq_base;
+    }
+    if (!tiles_ok) {
+      r.tiles_off = 0;
+      // stable counting sort of the tiles (natural order: sequence, tile,
+      // dK/dV before dQ) by expected cost, longest first
+      std::fill(g_noalloc_count, g_noalloc_count + kNoAllocMaxCost + 2, 0);
+      for (int b = 0; b < s.n_seqs; ++b) {
+        const int len = s.seq_start(b + 1) - s.seq_start(b);
+        const int nt = (len + kTile - 1) / kTile;
+        for (int t = 0; t < nt; ++t)
+          for (int kind = 0; kind < 2; ++kind) ++g_noalloc_count[bwd_tile_cost(nt, t, kind)];
+      }
+      int next = 0;
+      for (int c = kNoAllocMaxCost; c >= 0; --c) {
+        const int n = g_noalloc_count[c];
+        g_noalloc_count[c] = next;
+        next += n;
+      }
+      for (int b = 0; b < s.n_seqs; ++b) {
+        const int tok0 = s.seq_start(b), len = s.seq_start(b + 1) - tok0;
+        const int nt = (len + kTile - 1) / kTile;
+        for (int t = 0; t < nt; ++t)
+          for (int kind = 0; kind < 2; ++kind)
+            g_noalloc_tiles[g_noalloc_count[bwd_tile_cost(nt, t, kind)]++] =
+                TileDesc{tok0, len, t, kind};
+        for (int i = 0; i < len; ++i) g_noalloc_pos[tok0 + i] = i;
+      }
+      check_hip(hipMemcpy(sb + off_tiles, g_noalloc_tiles, 2 * static_cast<size_t>(n_tiles) * sizeof(TileDesc),
+                          hipMemcpyHostToDevice),
+                "allocation-free backward: tile table upload");
+      check_hip(hipMemcpy(sb + off_pos, g_noalloc_pos, T * sizeof(int32_t), hipMemcpyHostToDevice),
+                "allocation-free backward: position table upload");
+      r.n_seqs = s.n_seqs;
+      r.total_tokens = s.total_tokens;
+      for (int b = 0; b <= s.n_seqs; ++b) r.cu[b] = s.seq_start(b);
+      r.tiles_off = off_tiles;
+    }
+  }
+  NoAllocBwd w{};
+  w.cos_t = reinterpret_cast<const float*>(sb);
+  w.sin_t = reinterpret_cast<const float*>(sb + rope_bytes);
+  w.tiles_bwd = reinterpret_cast<const TileDesc*>(sb + off_tiles);
+  w.pos_of = reinterpret_cast<const int32_t*>(sb + off_pos);
+  w.stats = s.io_bf16 ? sb + off_stats : nullptr;
+  w.wk = sb + off_wk;
+  w.wv = sb + off_wv;
+  w.n_tiles = n_tiles;
+  w.pairs = pairs;
+  return w;
+}
+
 // Tile lists of one sequence layout, resident on the device.
 struct TileSet {
   int n_tiles = 0, max_len = 0;
@@ -115,6 +307,9 @@ class GpuAttentionEngine {
                std::to_string(n) + " devices)");
     check_hip(hipSetDevice(device_), "hipSetDevice");
     check_hip(hipStreamCreateWithFlags(&own_stream_, hipStreamNonBlocking), "hipStreamCreate");
+    // the allocation-free backward's scratch address on this device; a
+    // failure here only disables that entry point (it retries and reports)
+    if (noalloc_scratch_init(device_) != hipSuccess) (void)hipGetLastError();
     // GLACIER_ATTN_BWD=rows16|rows32 pins the bf16 backward kernel (tests
     // cover both on every shape); unset or "auto" picks by sequence length.
     if (const char* v = std::getenv("GLACIER_ATTN_BWD")) {
@@ -194,6 +389,24 @@ class GpuAttentionEngine {
     check_hip(launch_forward(a, stream(), &timer_), "attention forward launch");
   }
 
+  // Shape part of a backward launch (pointers are filled by the caller).
+  BwdLaunch bwd_launch_of(const BwdCall& c) const {
+    BwdLaunch a{};
+    a.precision = c.precision;
+    a.io_bf16 = c.io_bf16;
+    a.single_seq = c.single_seq;
+    a.variant = bwd_variant_;
+    a.head_dim = c.head_dim;
+    a.n_heads_q = c.n_heads_q;
+    a.n_heads_kv = c.n_heads_kv;
+    a.total_tokens = c.total_tokens;
+    a.n_tiles = c.n_tiles;
+    a.pairs = c.pairs;
+    a.scale = 1.0f / std::sqrt(static_cast<float>(c.head_dim));
+    a.scale_log2 = kLog2e * a.scale;
+    return a;
+  }
+
   // LaunchAttnTrainBwd + inverse LaunchRopeBatch (GpuLoraEngine.Backward.cs:354-412, :452).
   void LaunchAttnTrainBwd(const Shape& s, const void* d_out, const void* q_rot,
                           const void* k_rot, const void* v, const void* out,
@@ -202,19 +415,9 @@ class GpuAttentionEngine {
     const TileSet& ts = tiles_for(s);
     EnsureRopeTable(ts.max_len, s.head_dim, s.rope_freq_base);
     const size_t T = s.total_tokens, Hq = s.n_heads_q, D = s.head_dim;
-    BwdLaunch a{};
-    a.precision = s.precision;
-    a.io_bf16 = s.io_bf16;
-    a.single_seq = s.cu.size() == 2;
-    a.variant = bwd_variant_;
-    a.head_dim = s.head_dim;
-    a.n_heads_q = s.n_heads_q;
-    a.n_heads_kv = s.n_heads_kv;
-    a.total_tokens = s.total_tokens;
-    a.n_tiles = ts.n_tiles;
-    a.pairs = ts.pairs;
-    a.scale = 1.0f / std::sqrt(static_cast<float>(s.head_dim));
-    a.scale_log2 = kLog2e * a.scale;
+    BwdLaunch a = bwd_launch_of(BwdCall{s.total_tokens, s.n_heads_q, s.n_heads_kv, s.head_dim,
+                                        s.precision, s.io_bf16, s.cu.size() == 2, ts.n_tiles,
+                                        ts.pairs});
     a.d_out = d_out; a.q_rot = q_rot; a.k_rot = k_rot; a.v = v; a.out = out;
     a.lse = lse; a.dq = dq; a.dk = dk; a.dv = dv;
     // the per-head partials are kept in the tensors' dtype: bf16 tensors get
@@ -233,6 +436,41 @@ class GpuAttentionEngine {
     a.cos_t = static_cast<const float*>(rope_cos_.ptr);
     a.sin_t = static_cast<const float*>(rope_sin_.ptr);
     check_hip(launch_backward(a, stream(), &timer_), "attention backward launch");
+  }
+
+  // The same backward with every buffer beyond the caller's tensors taken
+  // from the device's fixed scratch array (noalloc_bwd_workspace): no device
+  // memory is allocated, and nothing on the host either once the call's
+  // sequence layout and RoPE table are resident.  No kernel timing.
+  void LaunchAttnTrainBwdNoAlloc(const ShapeArgs& s, const void* d_out, const void* q_rot,
+                                 const void* k_rot, const void* v, const void* out,
+                                 const float* lse, void* dq, void* dk, void* dv) {
+    if (s.total_tokens == 0) return;
+    void* base = noalloc_scratch(device_);
+    if (base == nullptr) {
+      const hipError_t e = noalloc_scratch_init(device_);
+      if (e != hipSuccess) {
+        (void)hipGetLastError();
+        fail(GLACIER_ATTN_ERR_DEVICE,
+             std::string("the allocation-free backward's scratch is unavailable on this device: ") +
+                 hipGetErrorString(e));
+      }
+      base = noalloc_scratch(device_);
+    }
+    NoAllocBwd w = noalloc_bwd_workspace(device_, base, s);
+    BwdLaunch a = bwd_launch_of(BwdCall{s.total_tokens, s.n_heads_q, s.n_heads_kv, s.head_dim,
+                                        s.precision, s.io_bf16, s.n_seqs == 1, w.n_tiles,
+                                        w.pairs});
+    a.d_out = d_out; a.q_rot = q_rot; a.k_rot = k_rot; a.v = v; a.out = out;
+    a.lse = lse; a.dq = dq; a.dk = dk; a.dv = dv;
+    a.wk = w.wk;
+    a.wv = w.wv;
+    a.stats = w.stats;
+    a.tiles_bwd = w.tiles_bwd;
+    a.pos_of = w.pos_of;
+    a.cos_t = w.cos_t;
+    a.sin_t = w.sin_t;
+    check_hip(launch_backward(a, stream(), nullptr), "attention backward launch");
   }
 
   // ---- projection with LoRA adapters (glacier_qkv.h) --------------------
@@ -410,8 +648,7 @@ class GpuAttentionEngine {
     const int half = head_dim / 2;
     std::vector<float> cs((size_t)len * half), sn((size_t)len * half);
     std::vector<float> freq(half);
-    for (int i = 0; i < half; i++)
-      freq[i] = 1.0f / powf(base, static_cast<float>(2 * i) / static_cast<float>(head_dim));
+    for (int i = 0; i < half; i++) freq[i] = rope_freq(i, head_dim, base);
     for (int pos = 0; pos < len; pos++)
       for (int i = 0; i < half; i++) {
         const float theta = static_cast<float>(pos) * freq[i];
@@ -458,15 +695,12 @@ class GpuAttentionEngine {
       return remaining(x) > remaining(y);
     });
     // Backward: dK/dV and dQ tiles share one launch, longest expected first
-    // (list scheduling, so the long tiles of both kinds start at once and the
-    // short ones fill the tail).  The cost is linear in the tile pairs a tile
-    // visits, with constants fitted to measured workgroup durations (D = 128,
-    // units of 0.1 us); it only orders the launch.
+    // (bwd_tile_cost).
     std::vector<std::pair<int, TileDesc>> bw;
     for (const TileDesc& t : nat) {
       const int nt = (t.len + kTile - 1) / kTile;
-      bw.push_back({63 + 16 * (nt - t.tile), TileDesc{t.tok0, t.len, t.tile, 0}});
-      bw.push_back({53 + 12 * (t.tile + 1), TileDesc{t.tok0, t.len, t.tile, 1}});
+      for (int kind = 0; kind < 2; ++kind)
+        bw.push_back({bwd_tile_cost(nt, t.tile, kind), TileDesc{t.tok0, t.len, t.tile, kind}});
     }
     std::stable_sort(bw.begin(), bw.end(),
                      [](const std::pair<int, TileDesc>& x, const std::pair<int, TileDesc>& y) {
@@ -533,9 +767,10 @@ class GpuAttentionEngine {
 namespace {
 
 // Validates a shape before anything touches the GPU.  Throws Error.
-Shape make_shape(int total_tokens, int n_seqs, const int32_t* cu, int hq, int hkv,
-                 int d, float base, int precision, int io) {
-  Shape s;
+// Validates one call's shape without copying anything (on success nothing
+// is allocated); make_shape builds the engine's cached form from it.
+ShapeArgs make_shape_args(int total_tokens, int n_seqs, const int32_t* cu, int hq, int hkv,
+                          int d, float base, int precision, int io) {
   if (n_seqs < 1) fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, "n_seqs must be >= 1");
   if (total_tokens < 0) fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, "total_tokens must be >= 0");
   if (hq <= 0 || hkv <= 0)
@@ -555,39 +790,52 @@ Shape make_shape(int total_tokens, int n_seqs, const int32_t* cu, int hq, int hk
     fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, "unknown io dtype " + std::to_string(io));
   if (io == GLACIER_ATTN_IO_BF16 && precision != GLACIER_ATTN_PREC_BF16)
     fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, "bf16 device tensors need GLACIER_ATTN_PREC_BF16");
-  s.cu.resize(n_seqs + 1);
   if (cu == nullptr) {
     if (n_seqs != 1)
       fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, "cu_seqlens is required when n_seqs > 1");
-    s.cu[0] = 0;
-    s.cu[1] = total_tokens;
   } else {
     if (cu[0] != 0) fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, "cu_seqlens[0] must be 0");
-    for (int b = 0; b <= n_seqs; ++b) {
-      if (b > 0 && cu[b] < cu[b - 1])
+    for (int b = 1; b <= n_seqs; ++b)
+      if (cu[b] < cu[b - 1])
         fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, "cu_seqlens must be non-decreasing");
-      s.cu[b] = cu[b];
-    }
     if (cu[n_seqs] != total_tokens)
       fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, "cu_seqlens[n_seqs] must equal total_tokens");
   }
-  int max_len = 0;
-  for (int b = 0; b < n_seqs; ++b) max_len = std::max(max_len, s.cu[b + 1] - s.cu[b]);
+  ShapeArgs s;
+  s.total_tokens = total_tokens;
+  s.n_seqs = n_seqs;
+  s.cu = cu;
+  for (int b = 0; b < n_seqs; ++b) s.max_len = std::max(s.max_len, s.seq_start(b + 1) - s.seq_start(b));
   if (d != 64 && d != 128)
     fail(GLACIER_ATTN_ERR_UNSUPPORTED,
          "head_dim " + std::to_string(d) + " is not supported by the GPU kernels (64 or 128)");
-  if (max_len > GLACIER_ATTN_MAX_SEQ_LEN)
-    fail(GLACIER_ATTN_ERR_UNSUPPORTED, "sequence of " + std::to_string(max_len) +
+  if (s.max_len > GLACIER_ATTN_MAX_SEQ_LEN)
+    fail(GLACIER_ATTN_ERR_UNSUPPORTED, "sequence of " + std::to_string(s.max_len) +
                                            " tokens exceeds GLACIER_ATTN_MAX_SEQ_LEN");
   if ((long long)total_tokens * hq * d >= (1LL << 40))
     fail(GLACIER_ATTN_ERR_UNSUPPORTED, "tensor too large");
-  s.total_tokens = total_tokens;
   s.n_heads_q = hq;
   s.n_heads_kv = hkv;
   s.head_dim = d;
   s.rope_freq_base = base;
   s.precision = precision;
   s.io_bf16 = io == GLACIER_ATTN_IO_BF16;
+  return s;
+}
+
+Shape make_shape(int total_tokens, int n_seqs, const int32_t* cu, int hq, int hkv,
+                 int d, float base, int precision, int io) {
+  const ShapeArgs a = make_shape_args(total_tokens, n_seqs, cu, hq, hkv, d, base, precision, io);
+  Shape s;
+  s.cu.resize(n_seqs + 1);
+  for (int b = 0; b <= n_seqs; ++b) s.cu[b] = a.seq_start(b);
+  s.total_tokens = a.total_tokens;
+  s.n_heads_q = a.n_heads_q;
+  s.n_heads_kv = a.n_heads_kv;
+  s.head_dim = a.head_dim;
+  s.rope_freq_base = a.rope_freq_base;
+  s.precision = a.precision;
+  s.io_bf16 = a.io_bf16;
   return s;
 }
 
@@ -814,6 +1062,26 @@ int glacier_attn_backward(glacier_attn_ctx* ctx, const glacier_attn_desc* desc,
     std::lock_guard<std::mutex> g(ctx->eng->lock());
     ctx->eng->activate();
     ctx->eng->LaunchAttnTrainBwd(s, d_out, q_rot, k_rot, v, out, lse, dq, dk, dv);
+  });
+}
+
+int glacier_attn_backward_noalloc(glacier_attn_ctx* ctx, const glacier_attn_desc* desc,
+                                  const void* d_out, const void* q_rot, const void* k_rot,
+                                  const void* v, const void* out, const float* lse, void* dq,
+                                  void* dk, void* dv) {
+  return guarded([&] {
+    if (desc == nullptr) glacier::fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT, "desc is NULL");
+    const glacier::ShapeArgs s = glacier::make_shape_args(
+        desc->total_tokens, desc->n_seqs, desc->cu_seqlens, desc->n_heads_q, desc->n_heads_kv,
+        desc->head_dim, desc->rope_freq_base, desc->precision, desc->io_dtype);
+    need(ctx, "ctx");
+    if (s.total_tokens > 0) {
+      need(d_out, "d_out"); need(q_rot, "q_rot"); need(k_rot, "k_rot"); need(v, "v");
+      need(out, "out"); need(lse, "lse"); need(dq, "dq"); need(dk, "dk"); need(dv, "dv");
+    }
+    std::lock_guard<std::mutex> g(ctx->eng->lock());
+    ctx->eng->activate();
+    ctx->eng->LaunchAttnTrainBwdNoAlloc(s, d_out, q_rot, k_rot, v, out, lse, dq, dk, dv);
   });
 }
 

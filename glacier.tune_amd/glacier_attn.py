@@ -171,6 +171,8 @@ def load():
     L.glacier_attn_forward.argtypes = [vp, ctypes.POINTER(Desc), vp, vp, vp, vp, vp, vp, vp]
     L.glacier_attn_backward.argtypes = [vp, ctypes.POINTER(Desc), vp, vp, vp, vp, vp, vp, vp,
                                         vp, vp]
+    L.glacier_attn_backward_noalloc.argtypes = [vp, ctypes.POINTER(Desc), vp, vp, vp, vp, vp, vp,
+                                                vp, vp, vp]
     L.glacier_attn_set_stream.argtypes = [vp, vp]
     L.glacier_attn_use_own_stream.argtypes = [vp]
     L.glacier_attn_synchronize.argtypes = [vp]

@@ -154,6 +154,38 @@ int glacier_attn_backward(glacier_attn_ctx *ctx, const glacier_attn_desc *desc,
                           const void *k_rot, const void *v, const void *out,
                           const float *lse, void *dq, void *dk, void *dv);
 
+/* ---- allocation-free backward ------------------------------------------- */
+
+/* Bytes of the fixed device array behind glacier_attn_backward_noalloc: 80
+ * MiB, held by every GPU that loads the library until the process ends. */
+#define GLACIER_ATTN_NOALLOC_SCRATCH_BYTES (80u * 1024u * 1024u)
+
+/* glacier_attn_backward without any device allocation.  It has no
+ * counterpart in the reference: it is for callers that cannot allocate
+ * (code recorded under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  Same arguments, kernels and results (bitwise) as
+ * glacier_attn_backward, and it calls no hipMalloc, hipFree or other
+ * allocating routine; every buffer beyond the caller's tensors lives in one
+ * fixed device array of GLACIER_ATTN_NOALLOC_SCRATCH_BYTES per GPU, laid
+ * out per call as (each part rounded up to 256 bytes)
+ *   RoPE cos and sin tables    2 x 4 * ceil_256(L) * D/2   (L: longest sequence)
+ *   tile and position tables   32 * tiles + 4 * T          (tiles: sum of ceil(len/64))
+ *   row stats (bf16 tensors)   8 * (T * Hq + 64)
+ *   dK and dV partials         2 x esz * T * Hq * D        (esz 2 bf16, 4 fp32 tensors)
+ * A call that needs more, or has more than 1024 sequences or 65536 tokens,
+ * returns GLACIER_ATTN_ERR_UNSUPPORTED and leaves the outputs untouched.
+ * The first call with a new sequence layout, head_dim, theta or a longer
+ * sequence than the array's tables cover waits for the whole device and
+ * uploads the tables (synchronous copies: make that call before capturing
+ * a graph); calls that repeat a layout only enqueue the kernels.  The array
+ * is shared by every call on the GPU, from any context, stream or thread,
+ * and keeps the last call's contents: calls that overlap on one GPU race,
+ * so the caller serialises them. */
+int glacier_attn_backward_noalloc(glacier_attn_ctx *ctx, const glacier_attn_desc *desc,
+                                  const void *d_out, const void *q_rot,
+                                  const void *k_rot, const void *v, const void *out,
+                                  const float *lse, void *dq, void *dk, void *dv);
+
 /* Makes every entry point enqueue on `hip_stream` (a hipStream_t; NULL is
  * the HIP null stream).  A new context uses a non-blocking stream of its own
  * (default priority). */

@@ -79,6 +79,22 @@ def test_device_descriptor_validation():
     assert rc == ga.ERR_UNSUPPORTED
 
 
+def test_noalloc_backward_argument_errors_come_before_any_device_work():
+    L = ga.load()
+    rc = L.glacier_attn_backward_noalloc(None, None, *([None] * 9))
+    assert rc == ga.ERR_INVALID_ARGUMENT and b"desc" in L.glacier_attn_last_error()
+    cu = np.array([0, 5, 3, 9], np.int32)
+    desc, _keep = ga.GpuAttentionEngine._desc(9, 4, 2, 64, 1e4, ga.PREC_BF16, ga.IO_BF16, cu)
+    rc = L.glacier_attn_backward_noalloc(None, ctypes.byref(desc), *([None] * 9))
+    assert rc == ga.ERR_INVALID_ARGUMENT and b"non-decreasing" in L.glacier_attn_last_error()
+    desc, _keep = ga.GpuAttentionEngine._desc(9, 4, 2, 96, 1e4, ga.PREC_BF16, ga.IO_BF16, None)
+    rc = L.glacier_attn_backward_noalloc(None, ctypes.byref(desc), *([None] * 9))
+    assert rc == ga.ERR_UNSUPPORTED
+    desc, _keep = ga.GpuAttentionEngine._desc(9, 4, 2, 64, 1e4, ga.PREC_BF16, ga.IO_BF16, None)
+    rc = L.glacier_attn_backward_noalloc(None, ctypes.byref(desc), *([None] * 9))
+    assert rc == ga.ERR_INVALID_ARGUMENT and b"ctx" in L.glacier_attn_last_error()
+
+
 def test_kernel_names_and_last_error_reset():
     names = ga.kernel_names()
     assert names == ["rope_k", "attn_fwd", "attn_bwd", "attn_bwd_reduce", "rmsnorm_fwd",
