@@ -331,6 +331,43 @@ def test_large_shapes_match_torch_fp32_reference(engines, name, lens, Hq, Hkv, D
     assert all(e <= BF16_GATE for e in err.values()), err
 
 
+LARGE_FP32 = [
+    ("long_s4096", [4096], 28, 4, 1.0e6),
+    ("llama3_b2_s2048", [2048, 2048], 32, 8, 5.0e5),
+]
+
+
+@pytest.mark.parametrize("name,lens,Hq,Hkv,base", LARGE_FP32)
+def test_large_shapes_fp32_mode_match_torch_fp32_reference(engines, name, lens, Hq, Hkv, base):
+    """BASELINE configs[3] and [4] in the fp32-operand mode, fp32 tensors, at
+    the 1e-4 gate (the float32 reference: plain matmul/softmax/autograd)."""
+    D = 128
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    T = int(cu[-1])
+    _say(f"[large fp32] {name} T={T}")
+    prev_tf32 = torch.backends.cuda.matmul.allow_tf32
+    torch.backends.cuda.matmul.allow_tf32 = False
+    try:
+        g = torch.Generator(device="cuda").manual_seed(4321)
+        q = torch.randn(T, Hq, D, device="cuda", generator=g)
+        k = torch.randn(T, Hkv, D, device="cuda", generator=g)
+        v = torch.randn(T, Hkv, D, device="cuda", generator=g)
+        dO = 0.01 * torch.randn(T, Hq, D, device="cuda", generator=g)
+        eng = engines[ga.PREC_FP32]
+        cuarg = None if len(lens) == 1 else cu
+        out, lse, q_rot, k_rot = eng.forward(q, k, v, base, cu_seqlens=cuarg)
+        dq, dk, dv = eng.backward(dO, q_rot, k_rot, v, out, lse, base, cu_seqlens=cuarg)
+        torch.cuda.synchronize()
+        ref = torch_reference(q, k, v, dO, base, cu)
+    finally:
+        torch.backends.cuda.matmul.allow_tf32 = prev_tf32
+    got = dict(out=out, lse=lse, dq=dq, dk=dk, dv=dv)
+    err = {key: float((got[key].float() - ref[key]).abs().max() / ref[key].abs().max())
+           for key in got}
+    _say(f"  errors {err}")
+    assert all(e <= FP32_GATE for e in err.values()), err
+
+
 # ---------------------------------------------------------------------------
 # Error behaviour and special values
 # ---------------------------------------------------------------------------
