@@ -170,7 +170,7 @@ int next(glacier_lora_reader* r, char* name, int32_t name_cap, int32_t* dim0, in
     if (shift > 28) return corrupt("malformed LoRA record name length");
   }
   if (static_cast<long>(len) > remaining(r)) return corrupt("truncated LoRA record name");
-  if (name_cap <= 0 || len + 1 > static_cast<uint32_t>(name_cap)) {
+  if (name_cap <= 0 || static_cast<uint64_t>(len) + 1 > static_cast<uint64_t>(name_cap)) {
     if (std::fseek(r->f, start, SEEK_SET) != 0) return corrupt("seek failed");
     return bad(err, kInvalid, "name buffer too small: the record name needs " +
                                   std::to_string(len + 1) + " bytes");
@@ -183,8 +183,9 @@ int next(glacier_lora_reader* r, char* name, int32_t name_cap, int32_t* dim0, in
   if (d0 <= 0 || d1 <= 0)
     return corrupt("invalid LoRA tensor dimensions [" + std::to_string(d0) + ", " +
                    std::to_string(d1) + "] for '" + name + "'");
-  const long bytes = static_cast<long>(d0) * d1 * static_cast<long>(sizeof(float));
-  if (bytes > remaining(r))
+  // (2^31 - 1)^2 * 4 bytes still fits 64 unsigned bits
+  const uint64_t bytes = static_cast<uint64_t>(d0) * static_cast<uint64_t>(d1) * sizeof(float);
+  if (bytes > static_cast<uint64_t>(remaining(r)))
     return corrupt(std::string("truncated LoRA binary payload for '") + name + "': expected " +
                    std::to_string(bytes) + " bytes, only " + std::to_string(remaining(r)) +
                    " remaining");

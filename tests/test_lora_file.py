@@ -98,7 +98,8 @@ def test_the_reference_corrupted_dims_fixture_reads_as_written(tmp_path):
 
 
 @pytest.mark.parametrize("case", ["magic", "version", "negative_count", "alpha_zero", "alpha_nan",
-                                  "zero_dim", "truncated_payload", "truncated_name", "missing"])
+                                  "zero_dim", "huge_dims", "truncated_payload", "truncated_name",
+                                  "missing"])
 def test_malformed_files_are_rejected(tmp_path, case):
     a = np.ones((4, 2), np.float32)
     good = _record("blk.0.attn_q.lora_a.weight", a)
@@ -109,6 +110,9 @@ def test_malformed_files_are_rejected(tmp_path, case):
         "alpha_zero": _file(1, 2, 0.0, [good]),
         "alpha_nan": _file(1, 2, float("nan"), [good]),
         "zero_dim": _file(1, 2, 4.0, [_dotnet_string("blk.0.x.lora_a.weight") + struct.pack("<ii", 0, 2)]),
+        # (2^31 - 1)^2 floats: the payload size overflows 63 bits
+        "huge_dims": _file(1, 2, 4.0, [_dotnet_string("blk.0.x.lora_a.weight")
+                                       + struct.pack("<ii", 2**31 - 1, 2**31 - 1) + a.tobytes()]),
         "truncated_payload": _file(1, 2, 4.0, [good[:-4]]),
         "truncated_name": _file(1, 2, 4.0, [_dotnet_string("blk.0.attn_q.lora_a.weight")[:10]]),
     }.get(case)
