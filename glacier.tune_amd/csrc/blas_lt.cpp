@@ -69,12 +69,13 @@ struct Blas {
       e = hipblasLtMatmulDescSetAttribute(g.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &op_a, sizeof(op_a));
     if (e == HIPBLAS_STATUS_SUCCESS)
       e = hipblasLtMatmulDescSetAttribute(g.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &op_b, sizeof(op_b));
-    // stored shapes (rows x cols, column-major): A' N x K or K x N, B' K x M or M x K
+    const GemmLayouts l = gemm_layouts(ta, tb, M, N, K, lda, ldb, ldc);
     if (e == HIPBLAS_STATUS_SUCCESS)
-      e = hipblasLtMatrixLayoutCreate(&g.a, in_t, tb ? K : N, tb ? N : K, ldb);
+      e = hipblasLtMatrixLayoutCreate(&g.a, in_t, l.b_first.rows, l.b_first.cols, l.b_first.ld);
     if (e == HIPBLAS_STATUS_SUCCESS)
-      e = hipblasLtMatrixLayoutCreate(&g.b, in_t, ta ? M : K, ta ? K : M, lda);
-    if (e == HIPBLAS_STATUS_SUCCESS) e = hipblasLtMatrixLayoutCreate(&g.c, HIP_R_32F, N, M, ldc);
+      e = hipblasLtMatrixLayoutCreate(&g.b, in_t, l.a_second.rows, l.a_second.cols, l.a_second.ld);
+    if (e == HIPBLAS_STATUS_SUCCESS)
+      e = hipblasLtMatrixLayoutCreate(&g.c, HIP_R_32F, l.c.rows, l.c.cols, l.c.ld);
     hipblasLtMatmulPreference_t pref = nullptr;
     if (e == HIPBLAS_STATUS_SUCCESS) e = hipblasLtMatmulPreferenceCreate(&pref);
     const uint64_t no_workspace = 0;
@@ -100,6 +101,17 @@ struct Blas {
 };
 
 }  // namespace
+
+// Stored shapes (rows x cols, column-major): the caller's B as N x K (tb) or
+// K x N, its A as K x M or M x K (ta), C as N x M; leading dimensions are the
+// caller's row strides.
+GemmLayouts gemm_layouts(bool ta, bool tb, int M, int N, int K, int lda, int ldb, int ldc) {
+  GemmLayouts l;
+  l.b_first = GemmOperand{tb ? K : N, tb ? N : K, ldb};
+  l.a_second = GemmOperand{ta ? M : K, ta ? K : M, lda};
+  l.c = GemmOperand{N, M, ldc};
+  return l;
+}
 
 void* create_blas_handle() {
   Blas* b = new Blas;

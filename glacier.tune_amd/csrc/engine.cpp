@@ -523,25 +523,15 @@ class GpuAttentionEngine {
   // from the host targets (:53, :190), as in the reference; the loss comes
   // back as one float.  Synchronises the stream.
   void LmHead(LmHeadLaunch a, const int32_t* targets, float* loss, int32_t* n_valid) {
-    std::vector<int> rows, tgts, src_of(static_cast<size_t>(a.T), -1);
-    for (int t = 0; t < a.T; ++t) {
-      if (targets[t] >= 0 && targets[t] < a.V) {
-        src_of[t] = static_cast<int>(rows.size());
-        rows.push_back(t);
-        tgts.push_back(targets[t]);
-      }
-    }
+    std::vector<int> rows, tgts, src_of;
+    lmhead_rows(targets, a.T, a.V, rows, tgts, src_of);
     const int n = static_cast<int>(rows.size());
     if (n_valid != nullptr) *n_valid = n;
     *loss = 0.0f;
     if (a.T == 0 || (n == 0 && a.d_hidden == nullptr)) return;
-    a.n_valid = n;
-    a.ldl = (a.V + 7) / 8 * 8;
-    const size_t esz = a.io_bf16 ? 2 : 4;
-    const long per_row = (long)a.ldl * (4 + (a.io_bf16 ? 2 : 0));
-    a.chunk = static_cast<int>(std::max(1L, std::min<long>(n, kLmHeadChunkBytes / per_row)));
-    const size_t ints = 2 * static_cast<size_t>(n) + static_cast<size_t>(a.T);
-    int* idx = static_cast<int*>(lm_idx_.ensure(ints * sizeof(int), "LM-head row indices"));
+    lmhead_shape(a, n);
+    const LmHeadScratch need = lmhead_scratch(a);
+    int* idx = static_cast<int*>(lm_idx_.ensure(need.idx, "LM-head row indices"));
     hipStream_t st = stream();
     if (n > 0) {
       check_hip(hipMemcpyAsync(idx, rows.data(), n * sizeof(int), hipMemcpyHostToDevice, st),
@@ -555,15 +545,12 @@ class GpuAttentionEngine {
     a.targets = idx + n;
     a.src_of = idx + 2 * n;
     if (n > 0) {
-      a.hv = lm_hv_.ensure(static_cast<size_t>(a.chunk) * a.H * esz, "LM-head packed rows");
-      a.logits = static_cast<float*>(
-          lm_logits_.ensure(static_cast<size_t>(a.chunk) * a.ldl * 4, "LM-head logits"));
-      a.dl = a.io_bf16 ? lm_dl_.ensure(static_cast<size_t>(a.chunk) * a.ldl * 2, "LM-head dlogits")
-                       : static_cast<void*>(a.logits);
+      a.hv = lm_hv_.ensure(need.hv, "LM-head packed rows");
+      a.logits = static_cast<float*>(lm_logits_.ensure(need.logits, "LM-head logits"));
+      a.dl = a.io_bf16 ? lm_dl_.ensure(need.dl, "LM-head dlogits") : static_cast<void*>(a.logits);
       if (a.d_hidden != nullptr)
-        a.dhv = static_cast<float*>(
-            lm_dhv_.ensure(static_cast<size_t>(n) * a.H * 4, "LM-head packed gradient"));
-      a.row_loss = static_cast<float*>(lm_loss_.ensure((static_cast<size_t>(n) + 1) * 4, "LM-head losses"));
+        a.dhv = static_cast<float*>(lm_dhv_.ensure(need.dhv, "LM-head packed gradient"));
+      a.row_loss = static_cast<float*>(lm_loss_.ensure(need.row_loss, "LM-head losses"));
       a.loss = a.row_loss + n;
     }
     check_hip(launch_lmhead(a, st, blas()), "LM-head launch");

@@ -20,6 +20,7 @@
 //   ce_loss     the mean of the row terms (double, fixed order)
 // Every sum has a fixed order and hipBLASLt runs without workspace, so
 // results are bitwise repeatable.
+#include <algorithm>
 #include <cfloat>
 
 #include "attn_common.hpp"
@@ -29,19 +30,17 @@
 namespace glacier {
 namespace {
 
-constexpr int kCeThreads = 256;
-
 // hv[i] = hidden[rows[r0 + i]], 16-byte pieces (H % 8 == 0).
 template <typename IO>
 __global__ __launch_bounds__(256) void ce_gather_kernel(const IO* __restrict__ hidden,
                                                         const int* __restrict__ rows, int r0, int n,
                                                         int H, IO* __restrict__ hv) {
-  const int per_row = H * (int)sizeof(IO) / 16;
+  const int per_row = ce_gather_pieces(H, (int)sizeof(IO));
   const long idx = (long)blockIdx.x * 256 + threadIdx.x;
   if (idx >= (long)n * per_row) return;
-  const int i = (int)(idx / per_row), p = (int)(idx % per_row);
-  const int4* src = reinterpret_cast<const int4*>(hidden + (long)rows[r0 + i] * H);
-  reinterpret_cast<int4*>(hv + (long)i * H)[p] = src[p];
+  const CeGatherAt at = ce_gather_at(idx, per_row);
+  const int4* src = reinterpret_cast<const int4*>(hidden + (long)rows[r0 + at.i] * H);
+  reinterpret_cast<int4*>(hv + (long)at.i * H)[at.p] = src[at.p];
 }
 
 __device__ inline void merge(float& m, float& s, float m2, float s2) {
@@ -121,7 +120,8 @@ __global__ __launch_bounds__(256) void ce_scatter_kernel(const float* __restrict
   const long idx = (long)blockIdx.x * 256 + threadIdx.x;
   const int q4 = H / 4;
   if (idx >= (long)T * q4) return;
-  const int t = (int)(idx / q4), c = 4 * (int)(idx % q4);
+  const CeScatterAt at = ce_scatter_at(idx, q4);
+  const int t = at.t, c = at.c;
   const int src = src_of[t];
   f32x4 v = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   if (src >= 0) v = *reinterpret_cast<const f32x4*>(dhv + (long)src * H + c);
@@ -150,7 +150,7 @@ template <typename IO>
 hipError_t run(const LmHeadLaunch& a, hipStream_t st, void* blas) {
   constexpr bool BF = sizeof(IO) == 2;
   const bool grad = a.d_hidden != nullptr;
-  const int per_row = a.H * (int)sizeof(IO) / 16;
+  const int per_row = ce_gather_pieces(a.H, (int)sizeof(IO));
   for (int r0 = 0; r0 < a.n_valid; r0 += a.chunk) {
     const int n = std::min(a.chunk, a.n_valid - r0);
     hipLaunchKernelGGL(ce_gather_kernel<IO>, dim3(blocks((long)n * per_row, 256)), dim3(256), 0, st,
@@ -182,6 +182,122 @@ hipError_t run(const LmHeadLaunch& a, hipStream_t st, void* blas) {
 
 hipError_t launch_lmhead(const LmHeadLaunch& a, hipStream_t st, void* blas) {
   return a.io_bf16 ? run<bf16>(a, st, blas) : run<float>(a, st, blas);
+}
+
+void lmhead_rows(const int32_t* targets, int T, int V, std::vector<int>& rows,
+                 std::vector<int>& tgts, std::vector<int>& src_of) {
+  rows.clear();
+  tgts.clear();
+  src_of.assign(static_cast<size_t>(T), -1);
+  for (int t = 0; t < T; ++t) {
+    if (targets[t] >= 0 && targets[t] < V) {
+      src_of[t] = static_cast<int>(rows.size());
+      rows.push_back(t);
+      tgts.push_back(targets[t]);
+    }
+  }
+}
+
+void lmhead_shape(LmHeadLaunch& a, int n_valid) {
+  a.n_valid = n_valid;
+  a.ldl = (a.V + 7) / 8 * 8;
+  const long per_row = (long)a.ldl * (4 + (a.io_bf16 ? 2 : 0));
+  a.chunk = static_cast<int>(std::max(1L, std::min<long>(n_valid, kLmHeadChunkBytes / per_row)));
+}
+
+LmHeadScratch lmhead_scratch(const LmHeadLaunch& a) {
+  const size_t esz = a.io_bf16 ? 2 : 4, n = static_cast<size_t>(a.n_valid);
+  LmHeadScratch s{};
+  s.idx = (2 * n + static_cast<size_t>(a.T)) * sizeof(int);
+  if (n > 0) {
+    s.hv = static_cast<size_t>(a.chunk) * a.H * esz;
+    s.logits = static_cast<size_t>(a.chunk) * a.ldl * 4;
+    s.dl = a.io_bf16 ? static_cast<size_t>(a.chunk) * a.ldl * 2 : 0;
+    s.dhv = a.d_hidden != nullptr ? n * a.H * 4 : 0;
+    s.row_loss = (n + 1) * 4;
+  }
+  return s;
+}
+
+std::string lmhead_check_bounds(const LmHeadLaunch& a, const LmHeadScratch& s, const int* rows,
+                                const int* targets, const int* src_of, size_t hidden_elems,
+                                size_t weight_elems, size_t d_hidden_elems) {
+  const int esz = a.io_bf16 ? 2 : 4;
+  const bool grad = a.d_hidden != nullptr;
+  const long long hv_elems = s.hv / esz, logit_elems = s.logits / 4, dhv_elems = s.dhv / 4;
+  // dlogits: bf16 scratch, or the logits buffer itself in the fp32 mode
+  const long long dl_elems = a.io_bf16 ? (long long)(s.dl / 2) : logit_elems;
+  auto bad = [](const std::string& what, long long at, long long limit) {
+    return what + ": element " + std::to_string(at) + " of " + std::to_string(limit);
+  };
+  if (s.idx < (2 * (size_t)a.n_valid + (size_t)a.T) * sizeof(int)) return "index scratch too small";
+  for (int r = 0; r < a.n_valid; ++r) {
+    if (rows[r] < 0 || rows[r] >= a.T) return bad("rows[]", rows[r], a.T);
+    if (targets[r] < 0 || targets[r] >= a.V) return bad("targets[]", targets[r], a.V);
+  }
+  for (int t = 0; t < a.T; ++t)
+    if (src_of[t] < -1 || src_of[t] >= a.n_valid) return bad("src_of[]", src_of[t], a.n_valid);
+  const int per_row = ce_gather_pieces(a.H, esz), piece = 16 / esz;
+  for (int r0 = 0; r0 < a.n_valid; r0 += a.chunk) {
+    const int n = std::min(a.chunk, a.n_valid - r0);
+    // ce_gather: every thread of its grid
+    const long threads = (long)((n * (long)per_row + 255) / 256) * 256;
+    for (long idx = 0; idx < threads; ++idx) {
+      if (idx >= (long)n * per_row) continue;  // the kernel's early return
+      const CeGatherAt at = ce_gather_at(idx, per_row);
+      if (r0 + at.i >= a.n_valid) return bad("ce_gather rows[]", r0 + at.i, a.n_valid);
+      const long long src = (long long)rows[r0 + at.i] * a.H + (long long)at.p * piece + piece;
+      if (src > (long long)hidden_elems) return bad("ce_gather hidden", src, hidden_elems);
+      const long long dst = (long long)at.i * a.H + (long long)at.p * piece + piece;
+      if (dst > hv_elems) return bad("ce_gather hv", dst, hv_elems);
+    }
+    // logits GEMM: [n x V] = hv [n x H] . weight[V x H]^T
+    const GemmLayouts g1 = gemm_layouts(false, true, n, a.V, a.H, a.H, a.H, a.ldl);
+    if (g1.b_first.elements() > (long long)weight_elems)
+      return bad("logits GEMM weight", g1.b_first.elements(), weight_elems);
+    if (g1.a_second.elements() > hv_elems) return bad("logits GEMM hv", g1.a_second.elements(), hv_elems);
+    if (g1.c.elements() > logit_elems) return bad("logits GEMM logits", g1.c.elements(), logit_elems);
+    // ce_row: n workgroups of kCeThreads, each thread its quads tid, tid + 256, ...
+    const int nq = a.ldl / 4;
+    for (int r = 0; r < n; ++r) {
+      const long long base = (long long)r * a.ldl;
+      if (base + targets[r0 + r] >= logit_elems) return bad("ce_row target logit", base + targets[r0 + r], logit_elems);
+      if (r0 + r >= a.n_valid) return bad("ce_row row_loss", r0 + r, a.n_valid);
+      for (int tid = 0; tid < kCeThreads; ++tid)
+        for (int q = tid; q < nq; q += kCeThreads) {
+          const long long end = base + 4LL * q + 4;
+          if (end > logit_elems) return bad("ce_row logits", end, logit_elems);
+          if (grad && end > dl_elems) return bad("ce_row dlogits", end, dl_elems);
+        }
+    }
+    if (grad) {
+      // gradient GEMM: dhv[r0 ..][n x H] = dl [n x V] . weight [V x H]
+      const GemmLayouts g2 = gemm_layouts(false, false, n, a.H, a.V, a.ldl, a.H, a.H);
+      if (g2.b_first.elements() > (long long)weight_elems)
+        return bad("gradient GEMM weight", g2.b_first.elements(), weight_elems);
+      if (g2.a_second.elements() > dl_elems) return bad("gradient GEMM dlogits", g2.a_second.elements(), dl_elems);
+      const long long c_end = (long long)r0 * a.H + g2.c.elements();
+      if (c_end > dhv_elems) return bad("gradient GEMM dhv", c_end, dhv_elems);
+    }
+  }
+  if (grad) {
+    // ce_scatter: every thread of its grid
+    const int q4 = a.H / 4;
+    const long threads = ((long)a.T * q4 + 255) / 256 * 256;
+    for (long idx = 0; idx < threads; ++idx) {
+      if (idx >= (long)a.T * q4) continue;
+      const CeScatterAt at = ce_scatter_at(idx, q4);
+      const int src = src_of[at.t];
+      if (src >= 0 && (long long)src * a.H + at.c + 4 > dhv_elems)
+        return bad("ce_scatter dhv", (long long)src * a.H + at.c + 4, dhv_elems);
+      if ((long long)at.t * a.H + at.c + 4 > (long long)d_hidden_elems)
+        return bad("ce_scatter d_hidden", (long long)at.t * a.H + at.c + 4, d_hidden_elems);
+    }
+  }
+  // ce_loss reads n_valid row terms and writes the one after them
+  if (a.n_valid > 0 && (size_t)(a.n_valid + 1) * 4 > s.row_loss)
+    return bad("ce_loss", a.n_valid + 1, s.row_loss / 4);
+  return "";
 }
 
 }  // namespace glacier

@@ -9,7 +9,11 @@
 - the library's host code (every source of glacier.tune_amd/csrc, built with
   the sanitizers on hipcc's host pass only), driven by
   tests/sanitize/abi_asan_driver.cpp through the C ABI's argument checks,
-  which run before any device work and so need no GPU.
+  which run before any device work and so need no GPU, and by
+  tests/sanitize/lmhead_bounds_driver.cpp, which walks every access of the
+  LM-head launch plan (each kernel thread's indices, each GEMM operand's
+  stored extent) against its buffers at the shape whose first GPU run
+  faulted and four more.
 
 They are built into a temporary directory and run as child processes; any
 sanitizer report aborts the child (-fno-sanitize-recover) and fails the test.
@@ -105,20 +109,24 @@ def test_library_host_code_under_asan_and_ubsan(tmp_path):
         assert res.returncode == 0, res.stderr[-3000:]
         return obj
 
+    drivers = ("abi_asan_driver.cpp", "lmhead_bounds_driver.cpp")
     jobs = [(s, os.path.join(csrc, s), build.SOURCES[s]) for s in build.SOURCES]
-    jobs.append(("abi_asan_driver.cpp",
-                 os.path.join(ROOT, "tests", "sanitize", "abi_asan_driver.cpp"), ()))
+    jobs += [(d, os.path.join(ROOT, "tests", "sanitize", d), ()) for d in drivers]
     with cf.ThreadPoolExecutor(max_workers=min(8, len(jobs))) as ex:
-        objs = list(ex.map(lambda j: compile_one(*j), jobs))
+        objs = dict(zip([j[0] for j in jobs], ex.map(lambda j: compile_one(*j), jobs)))
+    lib_objs = [objs[s] for s in build.SOURCES]
     rocm_lib = os.path.join(os.path.dirname(os.path.dirname(os.path.realpath(hipcc))), "lib")
-    exe = str(tmp_path / "abi_asan")
-    res = subprocess.run([hipcc, "--offload-arch=gfx950", "-Xarch_host", "-fsanitize=address",
-                          "-Xarch_host", "-fsanitize=undefined", *objs, "-o", exe,
-                          "-L" + rocm_lib, "-Wl,-rpath," + rocm_lib, "-lhipblaslt"],
-                         capture_output=True, text=True)
-    assert res.returncode == 0, res.stderr[-3000:]
-    res = _run([exe], {"ASAN_OPTIONS": "detect_leaks=1:halt_on_error=1",
-                       "UBSAN_OPTIONS": "print_stacktrace=1:halt_on_error=1"}, 240)
-    assert res.returncode == 0, (res.stdout[-2000:], res.stderr[-4000:])
-    assert "ABI_SANITIZE_OK" in res.stdout
-    assert "runtime error" not in res.stderr, res.stderr[-4000:]
+    env = {"ASAN_OPTIONS": "detect_leaks=1:halt_on_error=1",
+           "UBSAN_OPTIONS": "print_stacktrace=1:halt_on_error=1"}
+    for driver, ok in zip(drivers, ("ABI_SANITIZE_OK", "LMHEAD_BOUNDS_OK")):
+        exe = str(tmp_path / driver.replace(".cpp", ""))
+        res = subprocess.run([hipcc, "--offload-arch=gfx950", "-Xarch_host", "-fsanitize=address",
+                              "-Xarch_host", "-fsanitize=undefined", objs[driver], *lib_objs,
+                              "-o", exe, "-L" + rocm_lib, "-Wl,-rpath," + rocm_lib, "-lhipblaslt"],
+                             capture_output=True, text=True)
+        assert res.returncode == 0, res.stderr[-3000:]
+        res = _run([exe], env, 400)
+        print(res.stdout)
+        assert res.returncode == 0, (res.stdout[-3000:], res.stderr[-4000:])
+        assert ok in res.stdout
+        assert "runtime error" not in res.stderr, res.stderr[-4000:]
