@@ -127,9 +127,14 @@ __device__ inline void store4(bf16* p, f32x4 v) {
 template <typename IO, int D, int NT = kThreads, int ROWS = kTile>
 struct TileRegs {
   static constexpr int CPR = D / 8;                  // chunks per row
-  static constexpr int N = ROWS * CPR / NT;          // chunks per thread
+  // Lanes per row: CPR rounded up to a power of two, so that a row's lanes
+  // never straddle a wave (D = 96: 12 chunks on 16 lanes, 4 of them idle
+  // and holding zeros).
+  static constexpr int LPR = CPR <= 4 ? 4 : CPR <= 8 ? 8 : CPR <= 16 ? 16 : 32;
+  static constexpr int N = ROWS * LPR / NT;          // chunks per thread
   static constexpr int W = 8 * sizeof(IO) / 16;      // 16-byte words per chunk
-  static_assert(N * NT == ROWS * CPR, "tile must split evenly");
+  static_assert(CPR <= LPR && D % 8 == 0, "head_dim a multiple of 8, at most 256");
+  static_assert(N * NT == ROWS * LPR, "tile must split evenly");
   i32x4 w[N][W];
 
   // Rows r >= nvalid read as zero (past the end of the sequence): the loads
@@ -154,8 +159,13 @@ struct TileRegs {
 #pragma unroll
     for (int i = 0; i < N; ++i) {
       const int idx = tid + i * NT;
-      const int r = idx / CPR, ch = idx % CPR;
+      const int r = idx / LPR, ch = idx % LPR;
       const int off = r * rowb + ch * 8 * static_cast<int>(sizeof(IO));
+      if (LPR != CPR && ch >= CPR) {
+#pragma unroll
+        for (int j = 0; j < W; ++j) w[i][j] = i32x4{0, 0, 0, 0};
+        continue;
+      }
 #pragma unroll
       for (int j = 0; j < W; ++j) w[i][j] = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16 * j, 0, 0);
     }
@@ -168,7 +178,8 @@ struct TileRegs {
 #pragma unroll
     for (int i = 0; i < N; ++i) {
       const int idx = tid + i * NT;
-      const int r = idx / CPR, ch = idx % CPR;
+      const int r = idx / LPR, ch = idx % LPR;
+      if (LPR != CPR && ch >= CPR) continue;
       T* dst = lds + r * S + ch * 8;
       if constexpr (sizeof(IO) == sizeof(T)) {
 #pragma unroll
@@ -343,16 +354,17 @@ __device__ inline int wave_id() {
 // loop's own prefetch loads.
 __device__ inline void wait_vmem_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
-// Sum over groups of N (8, 16 or 32) consecutive lanes: DPP lane moves
+// Sum over groups of N (4, 8, 16 or 32) consecutive lanes: DPP lane moves
 // (quad xor 1, quad xor 2, half-row mirror, row mirror) run at ALU speed;
 // only N = 32 needs one cross-row permute.  Every lane of a group ends with
 // the same bits (each step adds two equal-order partial sums).
 template <int N>
 __device__ inline float lanes_sum(float x) {
-  static_assert(N == 8 || N == 16 || N == 32, "8-, 16- or 32-lane groups");
+  static_assert(N == 4 || N == 8 || N == 16 || N == 32, "4-, 8-, 16- or 32-lane groups");
   // (the DPP control operand must be a literal)
   x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0xB1, 0xF, 0xF, false));
   x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x4E, 0xF, 0xF, false));
+  if constexpr (N == 4) return x;
   x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x141, 0xF, 0xF, false));
   if constexpr (N >= 16)
     x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x140, 0xF, 0xF, false));

@@ -85,9 +85,12 @@ __global__ __launch_bounds__(kThreads) void rope_k_kernel(
 // tiles == nullptr means one sequence of total_tokens tokens (the tile order
 // is then computed, longest first, instead of read).
 // ---------------------------------------------------------------------------
-template <typename T>
+// Two key groups need a 64-row tile to split evenly over 512 threads' 8-element
+// chunks (D a multiple of 64) and both groups' double buffers to fit the LDS
+// (D <= 128); other head sizes take one group.
+template <typename T, int D>
 constexpr int fwd_groups() {
-  return sizeof(T) == 2 ? 2 : 1;
+  return (sizeof(T) == 2 && D % 64 == 0 && D <= 128) ? 2 : 1;
 }
 
 // Lazy rescaling: the running max used for exp2 moves only when a tile's max
@@ -96,7 +99,7 @@ constexpr int fwd_groups() {
 constexpr float kRescaleTau = 8.0f;
 
 template <typename IO, typename T, int D>
-__global__ __launch_bounds__(kThreads * fwd_groups<T>()) void attn_fwd_kernel(
+__global__ __launch_bounds__((kThreads * fwd_groups<T, D>())) void attn_fwd_kernel(
     const IO* __restrict__ q, const T* __restrict__ kc, const IO* __restrict__ v,
     IO* __restrict__ out, float* __restrict__ lse, IO* __restrict__ q_rot,
     const TileDesc* __restrict__ tiles, int n_tiles, int n_heads_q, int n_heads_kv,
@@ -104,7 +107,7 @@ __global__ __launch_bounds__(kThreads * fwd_groups<T>()) void attn_fwd_kernel(
     const float* __restrict__ sin_t) {
   using M = Mfma<T>;
   using L = Lds<T, D>;
-  constexpr int G = fwd_groups<T>();
+  constexpr int G = fwd_groups<T, D>();
   constexpr int NKD = D / M::KSTEP;
   constexpr int H = D / 2;
   extern __shared__ __align__(16) unsigned char smem_raw[];
@@ -140,7 +143,44 @@ __global__ __launch_bounds__(kThreads * fwd_groups<T>()) void attn_fwd_kernel(
   // group 1 through LDS, lane for lane, so Q and the cos/sin rows are read
   // from memory once per workgroup.
   typename M::Frag qf[NKD];
-  if (grp == 0) {
+  if constexpr (H % M::KSTEP != 0) {
+    // Half the head is not a whole number of k-steps (bf16, D = 32 or 96):
+    // each fragment's 8 elements (all on one side of H, as H % 8 == 0) are
+    // rotated against their partner half on their own, with the same fp32
+    // operations as the paired path.
+    static_assert(sizeof(T) == 2 && H % 8 == 0 && G == 1, "per-fragment rotation layout");
+#pragma unroll
+    for (int kk = 0; kk < NKD; ++kk) {
+      const int d0 = kk * M::KSTEP + 8 * g;
+      const bool lo = d0 < H;
+      const int dp = lo ? d0 + H : d0 - H;  // the partner half
+      const int pi = lo ? d0 : d0 - H;      // the rotation pair
+      float x[8], xp[8], cs[8], sn[8], y[8];
+      if (qvalid) {
+        load8(q + qbase + d0, x);
+        load8(q + qbase + dp, xp);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = xp[e] = 0.0f;
+      }
+      const long ti = (long)(qvalid ? qrow : 0) * H + pi;
+      load8(cos_t + ti, cs);
+      load8(sin_t + ti, sn);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float y0, y1;
+        if (lo) {
+          rope_fwd(x[e], xp[e], cs[e], sn[e], y0, y1);
+          y[e] = y0;
+        } else {
+          rope_fwd(xp[e], x[e], cs[e], sn[e], y0, y1);
+          y[e] = y1;
+        }
+        qf[kk][e] = (bf16)y[e];
+      }
+      if (q_rot != nullptr && qvalid) store8(q_rot + qbase + d0, y);
+    }
+  } else if (grp == 0) {
 #pragma unroll
     for (int kk = 0; kk < NKD / 2; ++kk) {
       if constexpr (sizeof(T) == 2) {
@@ -335,9 +375,9 @@ __global__ __launch_bounds__(kThreads * fwd_groups<T>()) void attn_fwd_kernel(
 // G groups of 4 waves split a tile's loop (2 in the bf16 mode, 1 in fp32);
 // their partial sums are added in group order.
 // ---------------------------------------------------------------------------
-template <typename T>
+template <typename T, int D>
 constexpr int bwd_groups() {
-  return sizeof(T) == 2 ? 2 : 1;
+  return (sizeof(T) == 2 && D % 64 == 0 && D <= 128) ? 2 : 1;
 }
 
 // D_i = dO_i . O_i for register-staged dO/O tiles: the thread's chunk i (8
@@ -354,7 +394,7 @@ __device__ inline float row_term(const TileRegs<IO, D, NT>& dreg, const TileRegs
   float part = 0.0f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) part += xd[e] * xo[e];
-  return lanes_sum<TileRegs<IO, D, NT>::CPR>(part);
+  return lanes_sum<TileRegs<IO, D, NT>::LPR>(part);
 }
 
 // dQ of one (query head, query tile); z indexes the query tiles (longest
@@ -367,7 +407,7 @@ __device__ inline void bwd_dq_tile(
     float scale, const float* __restrict__ cos_t, const float* __restrict__ sin_t) {
   using M = Mfma<T>;
   using L = Lds<T, D>;
-  constexpr int G = bwd_groups<T>();
+  constexpr int G = bwd_groups<T, D>();
   constexpr int NKD = D / M::KSTEP;
   constexpr int H = D / 2;
   using Regs = TileRegs<IO, D, kThreads * G>;
@@ -454,7 +494,7 @@ __device__ inline void bwd_dq_tile(
   for (int i = 0; i < Regs::N; ++i) {
     const float part = row_term(dreg, oreg, i);
     const int idx = tid + i * kThreads * G;
-    if (idx % Regs::CPR == 0) dsm[idx / Regs::CPR] = part;
+    if (idx % Regs::LPR == 0) dsm[idx / Regs::LPR] = part;
   }
   wait_vmem_all();
   __syncthreads();
@@ -558,7 +598,7 @@ __device__ inline void bwd_dkdv_tile(
   using M = Mfma<T>;
   using L = Lds<T, D>;
   using Regs = TileRegs<IO, D>;
-  constexpr int G = bwd_groups<T>();
+  constexpr int G = bwd_groups<T, D>();
   constexpr int NKD = D / M::KSTEP;
   constexpr int BUF = 2 * L::TILE * sizeof(T) + 2 * kTile * sizeof(float);  // bytes
   extern __shared__ __align__(16) unsigned char smem_raw[];
@@ -605,7 +645,7 @@ __device__ inline void bwd_dkdv_tile(
     for (int i = 0; i < Regs::N; ++i) {
       const float part = row_term(dreg, oreg, i);
       const int idx = gtid + i * kThreads;
-      if (idx % Regs::CPR == 0) vec[kTile + idx / Regs::CPR] = part;
+      if (idx % Regs::LPR == 0) vec[kTile + idx / Regs::LPR] = part;
     }
   };
 
@@ -750,7 +790,7 @@ __device__ inline void bwd_dkdv_tile(
 // z indexes tiles_bwd, the dK/dV and dQ tiles in launch order.  The
 // table is read through the scalar cache (one uniform load per workgroup).
 template <typename IO, typename T, int D>
-__global__ __launch_bounds__(kThreads * bwd_groups<T>()) void attn_bwd_kernel(
+__global__ __launch_bounds__((kThreads * bwd_groups<T, D>())) void attn_bwd_kernel(
     const IO* __restrict__ q_rot, const IO* __restrict__ d_out, const IO* __restrict__ out,
     const IO* __restrict__ k_rot, const IO* __restrict__ v, const float* __restrict__ lse,
     IO* __restrict__ dq, IO* __restrict__ wk, IO* __restrict__ wv,
@@ -785,6 +825,7 @@ __global__ __launch_bounds__(kRedThreads) void attn_bwd_reduce_kernel(
   constexpr int CH = H / 4;  // 4-pair chunks per row
   constexpr int ROWS = kRedThreads / CH;
   GL_STAMP(kKernReduce, 0);
+  if ((int)threadIdx.x >= ROWS * CH) return;  // CH need not divide the workgroup
   const long row = (long)blockIdx.x * ROWS + threadIdx.x / CH;  // token * Hkv + kv head
   if (row >= (long)total_tokens * n_heads_kv) return;
   const int p0 = 4 * (threadIdx.x % CH);
@@ -852,16 +893,16 @@ namespace {
 template <typename T, int D>
 constexpr size_t fwd_lds() {
   // K/V double buffers per group, plus group 0's Q fragments for group 1
-  return sizeof(T) * 4 * Lds<T, D>::TILE * fwd_groups<T>() +
-         (fwd_groups<T>() == 2 ? sizeof(T) * kTile * D : 0);
+  return sizeof(T) * 4 * Lds<T, D>::TILE * fwd_groups<T, D>() +
+         (fwd_groups<T, D>() == 2 ? sizeof(T) * kTile * D : 0);
 }
 template <typename T, int D>
 constexpr size_t bwd_lds() {
   // dQ tiles: K/V double buffers per group plus the 64 row terms; dK/dV
   // tiles: Q/dO double buffers per group with the lse and D vectors.
-  constexpr size_t dq = sizeof(T) * 4 * Lds<T, D>::TILE * bwd_groups<T>() + kTile * sizeof(float);
+  constexpr size_t dq = sizeof(T) * 4 * Lds<T, D>::TILE * bwd_groups<T, D>() + kTile * sizeof(float);
   constexpr size_t dkdv =
-      2 * (sizeof(T) * 2 * Lds<T, D>::TILE + 2 * kTile * sizeof(float)) * bwd_groups<T>();
+      2 * (sizeof(T) * 2 * Lds<T, D>::TILE + 2 * kTile * sizeof(float)) * bwd_groups<T, D>();
   return dq > dkdv ? dq : dkdv;
 }
 
@@ -883,14 +924,14 @@ hipError_t forward_impl(const FwdLaunch& a, hipStream_t st, KernelTimer* tm) {
     GL_CHECK(hipGetLastError());
     t.launched();
   }
-  if constexpr (sizeof(T) == 2) {
+  if constexpr (sizeof(T) == 2 && (D == 64 || D == 128)) {
     GL_CHECK((launch_fwd_bf16<IO, D>(a, st, tm)));
   } else {
     auto fn = attn_fwd_kernel<IO, T, D>;
     constexpr size_t lds = fwd_lds<T, D>();
     GL_CHECK(allow_lds(fn, lds));
     LaunchTiming t(tm, kKernFwd);
-    GL_LAUNCH(t, fn, dim3(a.n_heads_q, a.n_tiles), dim3(kThreads * fwd_groups<T>()), lds,
+    GL_LAUNCH(t, fn, dim3(a.n_heads_q, a.n_tiles), dim3(kThreads * fwd_groups<T, D>()), lds,
                           st, static_cast<const IO*>(a.q),
                           static_cast<const T*>(kc), static_cast<const IO*>(a.v),
                           static_cast<IO*>(a.out), a.lse, static_cast<IO*>(a.q_rot),
@@ -906,21 +947,21 @@ template <typename IO, typename T, int D>
 hipError_t backward_impl(const BwdLaunch& a, hipStream_t st, KernelTimer* tm) {
   const int ratio = a.n_heads_q / a.n_heads_kv;
   bool rows32 = false;
-  if constexpr (std::is_same<IO, bf16>::value) {
+  if constexpr (std::is_same<IO, bf16>::value && (D == 64 || D == 128)) {
     const long long min_pairs = D == 128 ? kBwdRows32MinPairsD128 : kBwdRows32MinPairsD64;
     rows32 = a.variant == kBwdRows32 || (a.variant == kBwdAuto && a.pairs >= min_pairs);
   }
   if (rows32) {
     // bf16 tensors, long sequences: the 32-row-wave kernel fed by LDS DMA
-    // (attn_bwd.hip)
-    GL_CHECK(launch_bwd2<D>(a, st, tm));
+    // (attn_bwd.hip; head_dim 64 and 128)
+    if constexpr (D == 64 || D == 128) GL_CHECK(launch_bwd2<D>(a, st, tm));
   } else {
     auto fn = attn_bwd_kernel<IO, T, D>;
     constexpr size_t lds = bwd_lds<T, D>();
     GL_CHECK(allow_lds(fn, lds));
     LaunchTiming t(tm, kKernBwd);
     GL_LAUNCH(t, fn, dim3(ratio, a.n_heads_kv, 2 * a.n_tiles),
-                          dim3(kThreads * bwd_groups<T>()), lds, st,
+                          dim3(kThreads * bwd_groups<T, D>()), lds, st,
                           static_cast<const IO*>(a.q_rot), static_cast<const IO*>(a.d_out),
                           static_cast<const IO*>(a.out), static_cast<const IO*>(a.k_rot),
                           static_cast<const IO*>(a.v), a.lse, static_cast<IO*>(a.dq),
@@ -946,32 +987,49 @@ hipError_t backward_impl(const BwdLaunch& a, hipStream_t st, KernelTimer* tm) {
 
 }  // namespace
 
-hipError_t launch_forward(const FwdLaunch& a, hipStream_t st, KernelTimer* tm) {
+// One instantiation per (tensor dtype, compute dtype, head_dim); fp32
+// operands take head_dim up to 128 (a 256-wide fp32 K/V double buffer
+// exceeds the LDS), bf16 operands up to 256.
+template <template <typename, typename, int> class Impl, typename L>
+hipError_t dispatch_head_dim(const L& a, hipStream_t st, KernelTimer* tm) {
   const bool bf = a.precision == kPrecBf16;
-  if (a.io_bf16) {
-    if (a.head_dim == 64) return forward_impl<bf16, bf16, 64>(a, st, tm);
-    return forward_impl<bf16, bf16, 128>(a, st, tm);
+  switch (a.head_dim) {
+#define GL_HEAD_DIM(DIM)                                                   \
+  case DIM:                                                                \
+    if (a.io_bf16) return Impl<bf16, bf16, DIM>::run(a, st, tm);          \
+    if (bf) return Impl<float, bf16, DIM>::run(a, st, tm);                \
+    if constexpr (DIM <= 128) return Impl<float, float, DIM>::run(a, st, tm); \
+    return hipErrorInvalidValue;
+    GL_HEAD_DIM(32)
+    GL_HEAD_DIM(64)
+    GL_HEAD_DIM(96)
+    GL_HEAD_DIM(128)
+    GL_HEAD_DIM(256)
+#undef GL_HEAD_DIM
+    default:
+      return hipErrorInvalidValue;
   }
-  if (bf) {
-    if (a.head_dim == 64) return forward_impl<float, bf16, 64>(a, st, tm);
-    return forward_impl<float, bf16, 128>(a, st, tm);
+}
+
+template <typename IO, typename T, int D>
+struct ForwardImpl {
+  static hipError_t run(const FwdLaunch& a, hipStream_t st, KernelTimer* tm) {
+    return forward_impl<IO, T, D>(a, st, tm);
   }
-  if (a.head_dim == 64) return forward_impl<float, float, 64>(a, st, tm);
-  return forward_impl<float, float, 128>(a, st, tm);
+};
+template <typename IO, typename T, int D>
+struct BackwardImpl {
+  static hipError_t run(const BwdLaunch& a, hipStream_t st, KernelTimer* tm) {
+    return backward_impl<IO, T, D>(a, st, tm);
+  }
+};
+
+hipError_t launch_forward(const FwdLaunch& a, hipStream_t st, KernelTimer* tm) {
+  return dispatch_head_dim<ForwardImpl>(a, st, tm);
 }
 
 hipError_t launch_backward(const BwdLaunch& a, hipStream_t st, KernelTimer* tm) {
-  const bool bf = a.precision == kPrecBf16;
-  if (a.io_bf16) {
-    if (a.head_dim == 64) return backward_impl<bf16, bf16, 64>(a, st, tm);
-    return backward_impl<bf16, bf16, 128>(a, st, tm);
-  }
-  if (bf) {
-    if (a.head_dim == 64) return backward_impl<float, bf16, 64>(a, st, tm);
-    return backward_impl<float, bf16, 128>(a, st, tm);
-  }
-  if (a.head_dim == 64) return backward_impl<float, float, 64>(a, st, tm);
-  return backward_impl<float, float, 128>(a, st, tm);
+  return dispatch_head_dim<BackwardImpl>(a, st, tm);
 }
 
 size_t compute_elem_size(int precision, bool io_bf16) {

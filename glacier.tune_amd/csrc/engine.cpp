@@ -336,8 +336,10 @@ class GpuAttentionEngine {
   // GpuLoraEngine.SupportsAttention (GpuLoraEngine.cs:111-112): the shapes
   // the GPU kernels take; anything else stays on the CPU path.
   static bool SupportsAttention(int seq_len, int head_dim) {
-    return (head_dim == 64 || head_dim == 128) && seq_len >= 1 &&
-           seq_len <= GLACIER_ATTN_MAX_SEQ_LEN;
+    return SupportedHeadDim(head_dim) && seq_len >= 1 && seq_len <= GLACIER_ATTN_MAX_SEQ_LEN;
+  }
+  static bool SupportedHeadDim(int d) {
+    return d == 32 || d == 64 || d == 96 || d == 128 || d == 256;
   }
 
   std::mutex& lock() { return mutex_; }
@@ -793,9 +795,14 @@ ShapeArgs make_shape_args(int total_tokens, int n_seqs, const int32_t* cu, int h
   s.n_seqs = n_seqs;
   s.cu = cu;
   for (int b = 0; b < n_seqs; ++b) s.max_len = std::max(s.max_len, s.seq_start(b + 1) - s.seq_start(b));
-  if (d != 64 && d != 128)
+  if (!GpuAttentionEngine::SupportedHeadDim(d))
+    fail(GLACIER_ATTN_ERR_UNSUPPORTED, "head_dim " + std::to_string(d) +
+                                           " is not supported by the GPU kernels (32, 64, 96, "
+                                           "128 or 256)");
+  if (d > 128 && precision == GLACIER_ATTN_PREC_FP32)
     fail(GLACIER_ATTN_ERR_UNSUPPORTED,
-         "head_dim " + std::to_string(d) + " is not supported by the GPU kernels (64 or 128)");
+         "head_dim " + std::to_string(d) + " runs in GLACIER_ATTN_PREC_BF16 only (its fp32 "
+         "key/value tiles do not fit the LDS)");
   if (s.max_len > GLACIER_ATTN_MAX_SEQ_LEN)
     fail(GLACIER_ATTN_ERR_UNSUPPORTED, "sequence of " + std::to_string(s.max_len) +
                                            " tokens exceeds GLACIER_ATTN_MAX_SEQ_LEN");

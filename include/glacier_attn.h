@@ -41,9 +41,10 @@ extern "C" {
  * GpuLoraEngine throws ArgumentOutOfRangeException for these
  * (GpuLoraEngine.Forward.cs:437-438) */
 #define GLACIER_ATTN_ERR_INVALID_ARGUMENT 1
-/* valid, but outside what the GPU kernels cover (head_dim other than 64 or
- * 128, a sequence longer than GLACIER_ATTN_MAX_SEQ_LEN): the caller keeps its
- * CPU path, like the canUseGpuAttn gate (TransformerBlock.cs:428-434) */
+/* valid, but outside what the GPU kernels cover (head_dim other than 32, 64,
+ * 96, 128 or 256; 256 in GLACIER_ATTN_PREC_FP32; a sequence longer than
+ * GLACIER_ATTN_MAX_SEQ_LEN): the caller keeps its CPU path, like the
+ * canUseGpuAttn gate (TransformerBlock.cs:428-434) */
 #define GLACIER_ATTN_ERR_UNSUPPORTED 2
 /* a HIP runtime or launch failure (CuDriver.Check, GpuLoraEngine.Forward.cs:457-464) */
 #define GLACIER_ATTN_ERR_DEVICE 3
@@ -97,8 +98,11 @@ void glacier_attn_destroy(glacier_attn_ctx *ctx);
 /* Text of the last failure on the calling thread ("" if none). */
 const char *glacier_attn_last_error(void);
 
-/* 1 if the GPU kernels take this shape, else 0.  Replaces
- * GpuLoraEngine.SupportsAttention (GpuLoraEngine.cs:111-112). */
+/* 1 if the GPU kernels take this shape, else 0: head_dim 32, 64, 96, 128 or
+ * 256 (256 in GLACIER_ATTN_PREC_BF16 only, whose bf16 key/value tiles fit the
+ * LDS) and 1 <= seq_len <= GLACIER_ATTN_MAX_SEQ_LEN.  Replaces
+ * GpuLoraEngine.SupportsAttention (GpuLoraEngine.cs:111-112), which accepts
+ * head_dim 1..1024; the other sizes keep the CPU path. */
 int glacier_attn_supports(int seq_len, int head_dim);
 
 /* ---- drop-in entry points: host fp32 tensors ----------------------------- */

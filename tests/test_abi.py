@@ -32,7 +32,10 @@ def test_supports_attention_gate():
     assert ga.supports_attention(512, 128)
     assert ga.supports_attention(4096, 64)
     assert ga.supports_attention(1, 128)
-    assert not ga.supports_attention(512, 96)
+    for d in (32, 96, 256):
+        assert ga.supports_attention(512, d)
+    for d in (80, 160, 512, 1024):
+        assert not ga.supports_attention(512, d)
     assert not ga.supports_attention(0, 128)
     assert not ga.supports_attention(65537, 128)
 
@@ -51,8 +54,10 @@ def test_argument_errors_come_before_any_device_work():
     assert rc == ga.ERR_INVALID_ARGUMENT and "multiple" in msg
     rc, msg = _fwd_host_rc(8, 2, 2, 2000)
     assert rc == ga.ERR_INVALID_ARGUMENT and "headDim" in msg
-    rc, msg = _fwd_host_rc(8, 2, 2, 96)
-    assert rc == ga.ERR_UNSUPPORTED and "96" in msg
+    rc, msg = _fwd_host_rc(8, 2, 2, 80)
+    assert rc == ga.ERR_UNSUPPORTED and "80" in msg
+    rc, msg = _fwd_host_rc(8, 2, 2, 256)  # fp32 operands: 256 is bf16-only
+    assert rc == ga.ERR_UNSUPPORTED and "BF16" in msg
     rc, msg = _fwd_host_rc(8, 0, 2, 64)
     assert rc == ga.ERR_INVALID_ARGUMENT
     rc, msg = _fwd_host_rc(8, 2, 2, 64, base=-1.0)
@@ -87,7 +92,7 @@ def test_noalloc_backward_argument_errors_come_before_any_device_work():
     desc, _keep = ga.GpuAttentionEngine._desc(9, 4, 2, 64, 1e4, ga.PREC_BF16, ga.IO_BF16, cu)
     rc = L.glacier_attn_backward_noalloc(None, ctypes.byref(desc), *([None] * 9))
     assert rc == ga.ERR_INVALID_ARGUMENT and b"non-decreasing" in L.glacier_attn_last_error()
-    desc, _keep = ga.GpuAttentionEngine._desc(9, 4, 2, 96, 1e4, ga.PREC_BF16, ga.IO_BF16, None)
+    desc, _keep = ga.GpuAttentionEngine._desc(9, 4, 2, 80, 1e4, ga.PREC_BF16, ga.IO_BF16, None)
     rc = L.glacier_attn_backward_noalloc(None, ctypes.byref(desc), *([None] * 9))
     assert rc == ga.ERR_UNSUPPORTED
     desc, _keep = ga.GpuAttentionEngine._desc(9, 4, 2, 64, 1e4, ga.PREC_BF16, ga.IO_BF16, None)

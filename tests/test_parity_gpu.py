@@ -211,6 +211,54 @@ def test_small_and_ragged_shapes(engines, S, Hq, Hkv, D, prec):
     assert all(e <= gate for e in err.values()), err
 
 
+@pytest.mark.parametrize("mode", ["fp32", "bf16_host", "bf16_device"])
+@pytest.mark.parametrize("D", [32, 96, 256])
+def test_head_dims_match_oracle(engines, D, mode):
+    """head_dim 32, 96 and 256 (the generic 16-row kernels; 64 and 128 are
+    covered above): a ragged S=200 (three full tiles and a partial one),
+    GQA 4:1, in each mode.  fp32 operands stop at 128 (UNSUPPORTED above)."""
+    S, Hq, Hkv, base = 200, 8, 2, 1.0e4
+    bf = mode != "fp32"
+    _say(f"[head_dim] D={D} mode={mode}")
+    if D > 128 and not bf:
+        q = np.zeros((S, Hq, D), np.float32)
+        with pytest.raises(ga.Unsupported):
+            engines[ga.PREC_FP32].forward_attention(0, q, q[:, :Hkv].copy(), q[:, :Hkv].copy(),
+                                                    np.empty_like(q), None, S, Hq, Hkv, D, base)
+        return
+    (q, k, v, dO), ref = oracle_case(S, Hq, Hkv, D, base, 4, bf)
+    if mode == "bf16_device":
+        got = run_device(engines[ga.PREC_BF16], q, k, v, dO, base, torch.bfloat16)
+    else:
+        got = run_host(engines[ga.PREC_BF16 if bf else ga.PREC_FP32], q, k, v, dO, base)
+    err = errors(got, ref)
+    _say(f"  errors {err}")
+    gate = BF16_GATE if bf else FP32_GATE
+    assert all(e <= gate for e in err.values()), err
+    if mode == "fp32":
+        assert np.array_equal(got["q_rot"], ref["q_rot"])
+        assert np.array_equal(got["k_rot"], ref["k_rot"])
+    elif mode == "bf16_host":
+        assert np.array_equal(got["q_rot"], ref["q_rot"])
+
+
+@pytest.mark.parametrize("D", [32, 96, 256])
+def test_head_dims_packed_batch_matches_oracle(engines, D):
+    """Packed sequences (a one-token one among them) at the new head sizes,
+    bf16 device tensors, against the oracle per segment."""
+    Hq, Hkv, base = 6, 3, 1.0e6
+    lens = [70, 1, 129]
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    T = int(cu[-1])
+    _say(f"[head_dim varlen] D={D} lens={lens}")
+    q, k, v, dO = make_inputs(T, Hq, Hkv, D, 12, True)
+    ref = oracle.layer_fwd_bwd_varlen(q, k, v, dO, cu, base)
+    got = run_device(engines[ga.PREC_BF16], q, k, v, dO, base, torch.bfloat16, cu=cu)
+    err = errors(got, ref)
+    _say(f"  errors {err}")
+    assert all(e <= BF16_GATE for e in err.values()), err
+
+
 def test_forward_without_save_leaves_qk_and_matches_saving_forward(engines):
     S, Hq, Hkv, D, base = 96, 4, 2, 64, 1.0e6
     _say("[no-save forward]")
@@ -379,11 +427,11 @@ def test_invalid_arguments_raise(engines):
     out = np.empty_like(q)
     with pytest.raises(ga.InvalidArgument):
         eng.forward_attention(0, q, k, k, out, None, 8, 3, 2, 64, 1e4)  # Hq % Hkv != 0
-    q = np.zeros((8, 2, 96), np.float32)
+    q = np.zeros((8, 2, 80), np.float32)
     with pytest.raises(ga.Unsupported):
-        eng.forward_attention(0, q, q, q, np.empty_like(q), None, 8, 2, 2, 96, 1e4)
-    assert not ga.supports_attention(512, 96)
-    assert ga.supports_attention(512, 128)
+        eng.forward_attention(0, q, q, q, np.empty_like(q), None, 8, 2, 2, 80, 1e4)
+    assert not ga.supports_attention(512, 80)
+    assert ga.supports_attention(512, 128) and ga.supports_attention(512, 96)
 
 
 def test_empty_sequence_is_a_no_op(engines):
