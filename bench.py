@@ -455,7 +455,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; use --gpus 1 "
-                                   "(the path shards by KV-head group, see DESIGN.md)"}))
+                                   "(the path shards by KV-head group)"}))
         sys.exit(2)
     if args.copy_probe > 0:
         import torch
