@@ -35,6 +35,7 @@ SOURCES = {
     "attn_noalloc.hip": (),
     "blas_lt.cpp": (),
     "proj_lora.hip": (),
+    "proj_gemm.hip": (),
     "rmsnorm.hip": (),
     "lmhead.hip": (),
     "lora_file.cpp": (),

@@ -35,10 +35,48 @@ struct ProjLaunch {
   void* dx;       // [T][in] (backward; overwritten)
   // scratch (fp32), sized by proj_scratch_need
   float* yf;       // forward: [T][out_p] base products, one after another
-  float* dxf;      // backward: [T][in] sum_p dY_p W_p
+                   // ([nsplit][T][out_p] for a narrow projection of bf16 tensors)
+  float* dxf;      // backward: [T][in] sum_p dY_p W_p over the library-GEMM
+                   // projections, then [T][in] over the narrow ones
   float* lowrank;  // [slot][T][r] X A_p and dY_p B_p^T
   float* part;     // split sums of those products
 };
+
+// ---- the narrow base products on the library's own GEMM (proj_gemm.hip) ----
+// bf16 tensors, inputs a multiple of 64 and at most kNarrowMaxOut outputs,
+// also a multiple of 64 (the k and v projections of a GQA block).
+constexpr int kNarrowMaxOut = 1024;
+
+struct NarrowJob {
+  const void* w;   // W_p [n][in] (bf16)
+  const void* dy;  // backward: dY_p [T][n] (bf16)
+  float* c;        // forward: fp32 partials [nsplit][T][n]
+  int n;           // outputs of the projection
+  int first;       // forward: its first workgroup (set by launch_narrow_fwd)
+};
+
+// Yf_p[s] = X W_p^T over input slice s (kchunk inputs) for each job.
+struct NarrowFwd {
+  const void* x;  // [T][K] (bf16)
+  int T, K, nsplit, kchunk, n;
+  NarrowJob j[kMaxProj];
+};
+
+// dXf2 [T][K] = sum over the jobs of dY_p W_p (K = the input features).
+struct NarrowBwd {
+  int T, K;
+  float* c;
+  int n;
+  NarrowJob j[kMaxProj];
+};
+
+bool narrow_gemm_fits(int in_features, int out_features);
+// Input slices of a forward launch: 1, 2 or 4, so that the launch has about
+// a workgroup per CU when the tiles alone are fewer.
+int narrow_fwd_splits(int T, int total_feature_tiles);
+int narrow_feature_tiles(int out_features);
+hipError_t launch_narrow_fwd(NarrowFwd a, hipStream_t st);
+hipError_t launch_narrow_bwd(const NarrowBwd& a, hipStream_t st);
 
 // Floats of each ProjLaunch scratch buffer for a forward or backward call.
 struct ProjScratchNeed {

@@ -10,8 +10,10 @@
 //   backward  dX   = sum_p dY_p W_p + s_p (dY_p B_p^T) A_p^T
 //             dA_p += s_p X^T (dY_p B_p^T),  dB_p += s_p (X A_p)^T dY_p
 //
-// The base products X W_p^T and dY_p W_p are hipBLASLt GEMMs with fp32
-// results (blas_lt.cpp).  Everything low-rank is here, each kernel taking every
+// The base products X W_p^T and dY_p W_p are GEMMs with fp32 results:
+// hipBLASLt (blas_lt.cpp) for the wide ones, the library's own kernels
+// (proj_gemm.hip) for the narrow ones of bf16 tensors (the k and v
+// projections of a GQA block).  Everything low-rank is here, each kernel taking every
 // projection of the call in one launch:
 //   lowrank_rows    L = X A_p and dL = dY_p B_p^T (output r columns wide,
 //                   reduction over in / out): 16-row slabs, the reduction
@@ -307,6 +309,8 @@ struct OutJob {
   const float* l[kMaxProj];
   const float* v[kMaxProj];
   float s[kMaxProj];
+  int nbase = 1;      // base products summed in order: base + i * stride, i < nbase
+  long stride = 0;
 };
 struct OutJobs {
   OutJob j[kMaxProj];
@@ -336,6 +340,12 @@ __global__ __launch_bounds__(kOutThreads) void lowrank_out_kernel(OutJobs jobs, 
 #pragma unroll
   for (int c = 0; c < 4; ++c)
     base[c] = *reinterpret_cast<const f32x4*>(job.base + (long)min(t0 + 4 * q + c, T - 1) * n + colc);
+  for (int i = 1; i < job.nbase; ++i) {  // split partials, in order
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      base[c] += *reinterpret_cast<const f32x4*>(job.base + i * job.stride +
+                                                 (long)min(t0 + 4 * q + c, T - 1) * n + colc);
+  }
   f32x4 acc[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) acc[e] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -474,20 +484,48 @@ hipError_t run_out(const ProjLaunch& a, OutJobs& jobs, hipStream_t st) {
 
 const float* slot(const ProjLaunch& a, int z) { return a.lowrank + (long)z * a.T * a.rank; }
 
+// Which projections of a call take the library's own narrow GEMM.
+bool is_narrow(const ProjLaunch& a, int p) {
+  return a.io_bf16 && narrow_gemm_fits(a.in, a.p[p].out);
+}
+
+// Input slices of the narrow forward launch (1 when there is none).
+int fwd_splits(const ProjLaunch& a) {
+  int tiles = 0;
+  for (int p = 0; p < a.n_proj; ++p)
+    if (is_narrow(a, p)) tiles += narrow_feature_tiles(a.p[p].out);
+  return tiles == 0 ? 1 : narrow_fwd_splits(a.T, tiles);
+}
+
 template <typename IO>
 hipError_t forward_impl(const ProjLaunch& a, hipStream_t st, void* h) {
   constexpr bool BF = sizeof(IO) == 2;
   long off = 0;
   OutJobs out{};
   out.n = a.n_proj;
+  NarrowFwd nf{};
+  nf.x = a.x;
+  nf.T = a.T;
+  nf.K = a.in;
+  nf.nsplit = fwd_splits(a);
+  nf.kchunk = (a.in + 64 * nf.nsplit - 1) / (64 * nf.nsplit) * 64;
   for (int p = 0; p < a.n_proj; ++p) {
     const ProjSpec& s = a.p[p];
-    // Yf_p = X W_p^T
-    GL_CHECK(blas_gemm(h, BF, false, true, a.T, s.out, a.in, 1.0f, a.x, a.in, s.w, a.in, 0.0f,
-                           a.yf + off, s.out, st));
     out.j[p] = OutJob{a.yf + off, s.bias, s.y, s.out, 0, 0, {}, {}, {}};
-    off += (long)a.T * s.out;
+    if (is_narrow(a, p)) {
+      // Yf_p[i] = X W_p^T over input slice i, summed by lowrank_out
+      nf.j[nf.n++] = NarrowJob{s.w, nullptr, a.yf + off, s.out, 0};
+      out.j[p].nbase = nf.nsplit;
+      out.j[p].stride = (long)a.T * s.out;
+      off += (long)nf.nsplit * a.T * s.out;
+    } else {
+      // Yf_p = X W_p^T
+      GL_CHECK(blas_gemm(h, BF, false, true, a.T, s.out, a.in, 1.0f, a.x, a.in, s.w, a.in, 0.0f,
+                         a.yf + off, s.out, st));
+      off += (long)a.T * s.out;
+    }
   }
+  if (nf.n > 0) GL_CHECK(launch_narrow_fwd(nf, st));
   const RowsPlan plan = rows_plan(a, false);
   GL_CHECK(run_rows<IO>(a, plan, st));  // L_p = X A_p
   for (int p = 0; p < a.n_proj; ++p) {
@@ -504,12 +542,24 @@ hipError_t forward_impl(const ProjLaunch& a, hipStream_t st, void* h) {
 template <typename IO>
 hipError_t backward_impl(const ProjLaunch& a, hipStream_t st, void* h) {
   constexpr bool BF = sizeof(IO) == 2;
-  // dXf = sum_p dY_p W_p
+  // dXf = sum_p dY_p W_p: the library GEMM for the wide projections into
+  // dxf, the narrow ones into the buffer after it; lowrank_out adds the two
+  NarrowBwd nb{};
+  nb.T = a.T;
+  nb.K = a.in;
+  nb.c = a.dxf + (long)a.T * a.in;
+  int wide = 0;
   for (int p = 0; p < a.n_proj; ++p) {
     const ProjSpec& s = a.p[p];
+    if (is_narrow(a, p)) {
+      nb.j[nb.n++] = NarrowJob{s.w, s.dy, nullptr, s.out, 0};
+      continue;
+    }
     GL_CHECK(blas_gemm(h, BF, false, false, a.T, a.in, s.out, 1.0f, s.dy, s.out, s.w, a.in,
-                           p == 0 ? 0.0f : 1.0f, a.dxf, a.in, st));
+                       wide == 0 ? 0.0f : 1.0f, a.dxf, a.in, st));
+    ++wide;
   }
+  if (nb.n > 0) GL_CHECK(launch_narrow_bwd(nb, st));
   // dL_p = dY_p B_p^T, and L_p = X A_p where grad_B_p is wanted
   const RowsPlan plan = rows_plan(a, true);
   GL_CHECK(run_rows<IO>(a, plan, st));
@@ -545,7 +595,11 @@ hipError_t backward_impl(const ProjLaunch& a, hipStream_t st, void* h) {
   OutJobs out{};
   out.n = 1;
   OutJob& o = out.j[0];
-  o = OutJob{a.dxf, nullptr, a.dx, a.in, 0, 0, {}, {}, {}};
+  o = OutJob{wide > 0 ? a.dxf : nb.c, nullptr, a.dx, a.in, 0, 0, {}, {}, {}};
+  if (wide > 0 && nb.n > 0) {
+    o.nbase = 2;
+    o.stride = (long)a.T * a.in;
+  }
   for (int p = 0; p < a.n_proj; ++p) {
     if (plan.slot_dl[p] < 0) continue;
     o.l[o.n_terms] = slot(a, plan.slot_dl[p]);
@@ -560,10 +614,14 @@ hipError_t backward_impl(const ProjLaunch& a, hipStream_t st, void* h) {
 
 ProjScratchNeed proj_scratch_need(const ProjLaunch& a, bool backward) {
   ProjScratchNeed need{};
+  bool narrow = false;
+  for (int p = 0; p < a.n_proj; ++p) narrow = narrow || is_narrow(a, p);
   if (backward) {
-    need.dxf = (long)a.T * a.in;
+    need.dxf = (long)a.T * a.in * (narrow ? 2 : 1);
   } else {
-    for (int p = 0; p < a.n_proj; ++p) need.yf += (long)a.T * a.p[p].out;
+    const int splits = fwd_splits(a);
+    for (int p = 0; p < a.n_proj; ++p)
+      need.yf += (long)a.T * a.p[p].out * (is_narrow(a, p) ? splits : 1);
   }
   const RowsPlan plan = rows_plan(a, backward);
   if (plan.n > 0) {
