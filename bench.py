@@ -439,6 +439,56 @@ def run_norm(args):
     eng.close()
 
 
+def run_host(args):
+    """The drop-in host entry points (glacier_attn_forward_host /
+    backward_host, fp32 host arrays as the C# engine passes them): every call
+    copies its tensors host -> device and back, so this rate includes PCIe.
+    It is reported beside the device-resident headline, never as it."""
+    import time
+
+    import numpy as np
+
+    import glacier_attn as ga
+
+    lengths, Hq, Hkv, D, theta, _ = CONFIGS[args.config]
+    if len(lengths) != 1:
+        sys.exit("the host entry points take one sequence per call")
+    S = lengths[0]
+    rng = np.random.default_rng(0)
+    q0 = rng.standard_normal((S, Hq, D), dtype=np.float32)
+    k0 = rng.standard_normal((S, Hkv, D), dtype=np.float32)
+    v = rng.standard_normal((S, Hkv, D), dtype=np.float32)
+    dO = (0.01 * rng.standard_normal((S, Hq, D))).astype(np.float32)
+    q, k = np.empty_like(q0), np.empty_like(k0)
+    out = np.empty_like(q0)
+    lse = np.empty((Hq, S), np.float32)
+    dq, dk, dv = np.empty_like(q0), np.empty_like(k0), np.empty_like(v)
+    flops = 12 * D * Hq * pairs(lengths)  # the headline convention: 4 D fwd + 8 D bwd per pair
+    res = {}
+    for name, prec in (("bf16", ga.PREC_BF16), ("fp32", ga.PREC_FP32)):
+        eng = ga.GpuAttentionEngine(0, prec)
+        total = 0.0
+        for it in range(args.warmup + args.steps):
+            np.copyto(q, q0)  # the forward overwrites q, k with their post-RoPE values
+            np.copyto(k, k0)
+            t0 = time.perf_counter()
+            eng.forward_attention(0, q, k, v, out, lse, S, Hq, Hkv, D, theta)
+            eng.backward_attention(0, dO, q, k, v, out, lse, dq, dk, dv, S, Hq, Hkv, D, theta)
+            dt = time.perf_counter() - t0
+            if it >= args.warmup:
+                total += dt
+        eng.close()
+        ms = total / args.steps * 1e3
+        res[name] = {"ms_per_step": round(ms, 4), "tflops": round(flops / (ms * 1e-3) / 1e12, 3)}
+    print(json.dumps({
+        "metric": "PCIe-inclusive causal GQA attn fwd+bwd TFLOP/s through the host entry points "
+                  "(glacier_attn_forward_host + backward_host, fp32 host arrays)",
+        "unit": "TFLOP/s", "steps": args.steps, "warmup": args.warmup,
+        "config": {"workload": args.config, "seq_len": S, "n_heads_q": Hq, "n_heads_kv": Hkv,
+                   "head_dim": D, "host_memory": "pageable numpy arrays"},
+        "algorithmic_gflop_per_step": round(flops / 1e9, 4), "modes": res}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -446,9 +496,11 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="qwen7b_s512", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--component", default="attention", choices=["attention", "proj", "norm"],
-                    help="attention (the headline), the q/k/v projections with LoRA adapters, or "
-                         "the residual add + RMSNorm")
+    ap.add_argument("--component", default="attention",
+                    choices=["attention", "proj", "norm", "host"],
+                    help="attention (the headline), the q/k/v projections with LoRA adapters, "
+                         "the residual add + RMSNorm, or the attention's PCIe-inclusive host "
+                         "entry points")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run 5 plain device copies of MIB MiB (a known-size kernel that "
                          "calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE counters)")
@@ -471,6 +523,9 @@ def main():
         return
     if args.component == "norm":
         run_norm(args)
+        return
+    if args.component == "host":
+        run_host(args)
         return
 
     import numpy as np
