@@ -379,6 +379,32 @@ def test_large_shapes_match_torch_fp32_reference(engines, name, lens, Hq, Hkv, D
     assert all(e <= BF16_GATE for e in err.values()), err
 
 
+@pytest.mark.parametrize("S,D", [(16384, 128), (16384, 64)])
+def test_long_sequence_matches_torch_fp32_reference(engines, S, D):
+    """S=16384 (a quarter of GLACIER_ATTN_MAX_SEQ_LEN) through the 32-row
+    backward at D=128 and D=64, few heads so the float32 reference's S x S
+    scores fit: row indices, tile tables and causal masks far from the
+    shapes above."""
+    Hq, Hkv, base = 2, 1, 1.0e6
+    cu = np.array([0, S], np.int32)
+    _say(f"[long] S={S} D={D}")
+    g = torch.Generator(device="cuda").manual_seed(99)
+    q = torch.randn(S, Hq, D, device="cuda", generator=g).bfloat16()
+    k = torch.randn(S, Hkv, D, device="cuda", generator=g).bfloat16()
+    v = torch.randn(S, Hkv, D, device="cuda", generator=g).bfloat16()
+    dO = (0.01 * torch.randn(S, Hq, D, device="cuda", generator=g)).bfloat16()
+    eng = engines[ga.PREC_BF16]
+    out, lse, q_rot, k_rot = eng.forward(q, k, v, base)
+    dq, dk, dv = eng.backward(dO, q_rot, k_rot, v, out, lse, base)
+    torch.cuda.synchronize()
+    ref = torch_reference(q, k, v, dO, base, cu)
+    got = dict(out=out, lse=lse, dq=dq, dk=dk, dv=dv)
+    err = {key: float((got[key].float() - ref[key]).abs().max() / ref[key].abs().max())
+           for key in got}
+    _say(f"  errors {err}")
+    assert all(e <= BF16_GATE for e in err.values()), err
+
+
 LARGE_FP32 = [
     ("long_s4096", [4096], 28, 4, 1.0e6),
     ("llama3_b2_s2048", [2048, 2048], 32, 8, 5.0e5),
