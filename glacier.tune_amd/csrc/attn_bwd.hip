@@ -362,10 +362,9 @@ __device__ inline void b2_dkdv(const TileDesc td, const bf16* __restrict__ q_rot
       if (kk + 1 < NKD) cur = nxt;
     }
     __builtin_amdgcn_sched_barrier(0);
-    bf16x8 pB[2], dsB[2];
+    float pv[2][2][4], dsv[2][2][4];  // [query block][key block][row]
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
-      const int qi0 = q0 + 16 * qb + 4 * gq;  // the lane's first query of the block
+    for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -373,13 +372,33 @@ __device__ inline void b2_dkdv(const TileDesc td, const bf16* __restrict__ q_rot
           // (nlse2, D) of query 4 g + r: elements 2 (r % 2), 2 (r % 2) + 1 of
           // the block's stats vector r / 2
           const float nl = st2[qb][r >> 1][2 * (r & 1)], dr = st2[qb][r >> 1][2 * (r & 1) + 1];
-          float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qb][kb][r], scale_log2, nl));
-          float ds = p * (dp[qb][kb][r] - dr);
-          if (mask && !(kw + 16 * kb + cq <= qi0 + r && qi0 + r < td.len)) p = ds = 0.0f;
-          pB[kb][4 * qb + r] = (bf16)p;
-          dsB[kb][4 * qb + r] = (bf16)ds;
+          pv[qb][kb][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qb][kb][r], scale_log2, nl));
+          dsv[qb][kb][r] = pv[qb][kb][r] * (dp[qb][kb][r] - dr);
         }
+    // the mask's compares and selects only in the (few) stages that need it:
+    // a uniform branch, not a select in every stage
+    if (mask) {
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        const int qi0 = q0 + 16 * qb + 4 * gq;  // the lane's first query of the block
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (!(kw + 16 * kb + cq <= qi0 + r && qi0 + r < td.len))
+              pv[qb][kb][r] = dsv[qb][kb][r] = 0.0f;
+      }
     }
+    bf16x8 pB[2], dsB[2];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          pB[kb][4 * qb + r] = (bf16)pv[qb][kb][r];
+          dsB[kb][4 * qb + r] = (bf16)dsv[qb][kb][r];
+        }
     // dV^T += dO^T P and dK^T += Q^T dS: each transposed A fragment feeds
     // both key blocks; column block db + 1's reads are in flight during db's
     // MFMAs
@@ -630,17 +649,31 @@ __device__ inline void b2_dq(const TileDesc td, const bf16* __restrict__ q_rot,
       }
     }
     __builtin_amdgcn_sched_barrier(0);
+    float pv[2][2][4];  // [key block][query block][row]
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          pv[kb][qb][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][qb][r], scale_log2, nl[qb]));
+    if (mask) {  // a uniform branch: the compares only in the diagonal stage
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (kChunk * m + 16 * kb + 4 * gq + r > qw + 16 * qb + cq) pv[kb][qb][r] = 0.0f;
+    }
     bf16x8 dsB[2];
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][qb][r], scale_log2, nl[qb]));
-          if (mask && kChunk * m + 16 * kb + 4 * gq + r > qw + 16 * qb + cq) p = 0.0f;
-          dsB[qb][4 * kb + r] = (bf16)(p * (dp[kb][qb][r] - dr[qb]));
-        }
+        for (int r = 0; r < 4; ++r)
+          dsB[qb][4 * kb + r] = (bf16)(pv[kb][qb][r] * (dp[kb][qb][r] - dr[qb]));
     // dQ^T += K^T dS^T: each transposed K fragment feeds both query blocks;
     // column block db + 1's reads are in flight during db's MFMAs
     __builtin_amdgcn_sched_barrier(0);
