@@ -509,7 +509,7 @@ __device__ inline void bwd_dq_tile(
   GL_STAMP(kKernBwd, 2);
 
   const int nit = (td.tile + G) / G;
-  for (int it = 0; it < nit; ++it) {
+  auto iteration = [&](int it, auto diag) {
     const int kt = grp + G * it;
     const T* ks = glds + (it & 1) * 2 * L::TILE;
     const bool more = kt + G <= td.tile;
@@ -519,10 +519,7 @@ __device__ inline void bwd_dq_tile(
       kreg.load(kbase + roff, kvstride, nv, gtid);
       vreg.load(vbase + roff, kvstride, nv, gtid);
     }
-    if (kt < td.tile)
-      step(ks, ks + L::TILE, std::false_type{});
-    else if (kt == td.tile)
-      step(ks, ks + L::TILE, std::true_type{});
+    if (decltype(diag)::value || kt < td.tile) step(ks, ks + L::TILE, diag);
     if (it < 6) GL_STAMP(kKernBwd, 3 + 3 * it);
     if (more) {
       T* nxt = glds + ((it + 1) & 1) * 2 * L::TILE;
@@ -532,7 +529,16 @@ __device__ inline void bwd_dq_tile(
     if (it < 6) GL_STAMP(kKernBwd, 4 + 3 * it);
     __syncthreads();
     if (it < 6) GL_STAMP(kKernBwd, 5 + 3 * it);
-  }
+  };
+  // Every iteration but the last takes a key tile below the diagonal; the
+  // diagonal tile is the last iteration of one group.  Peeling it keeps a
+  // single step variant inside the loop (two variants in one loop body make
+  // the register allocator copy the loop-carried registers every iteration).
+  for (int it = 0; it + 1 < nit; ++it) iteration(it, std::false_type{});
+  if (grp + G * (nit - 1) == td.tile)
+    iteration(nit - 1, std::true_type{});
+  else
+    iteration(nit - 1, std::false_type{});
 
   GL_STAMP(kKernBwd, 21);
   if constexpr (G == 2) {
@@ -721,21 +727,27 @@ __device__ inline void bwd_dkdv_tile(
   GL_STAMP(kKernBwd, 2);
 
   const int nit = (ntq - td.tile + G - 1) / G;  // iterations of group 0 (the most)
-  for (int it = 0; it < nit; ++it) {
+  auto iteration = [&](int it, auto diag) {
     const int qt = first + G * it;
     const unsigned char* base = gsm + (it & 1) * BUF;
     const bool more = qt + G < ntq;
     if (more) load_tile(qt + G);
-    if (qt == td.tile)
-      step(base, std::true_type{});
-    else if (qt < ntq)
-      step(base, std::false_type{});
+    if (qt < ntq) step(base, diag);
     if (it < 6) GL_STAMP(kKernBwd, 3 + 3 * it);
     if (more) store_tile((it + 1) & 1, qt + G);
     if (it < 6) GL_STAMP(kKernBwd, 4 + 3 * it);
     __syncthreads();
     if (it < 6) GL_STAMP(kKernBwd, 5 + 3 * it);
+  };
+  // The diagonal query tile is group 0's first iteration; peeling it keeps a
+  // single step variant inside the loop (two variants in one loop body make
+  // the register allocator copy the accumulators every iteration).
+  int it0 = 0;
+  if (grp == 0 && nit > 0) {
+    iteration(0, std::true_type{});
+    it0 = 1;
   }
+  for (int it = it0; it < nit; ++it) iteration(it, std::false_type{});
 
   GL_STAMP(kKernBwd, 21);
   // Merge the groups and write whole rows: the [64 keys][D] fp32 dK and dV
