@@ -459,7 +459,7 @@ __device__ inline void bwd_dq_tile(
 
   float drow = 0.0f, nlse2 = 0.0f;  // set once the row terms are staged
   // One key tile: S, dP, P from lse, dS = P (dP - D), dQ^T += K^T dS^T.
-  auto step = [&](const T* ks, const T* vs, auto diag) {
+  auto step = [&](const T* ks, const T* vs, auto diag, auto after) {
     constexpr bool DIAG = decltype(diag)::value;
     const int nb = DIAG ? (wq + 1) : 4;
     float ds[4][4];
@@ -482,6 +482,7 @@ __device__ inline void bwd_dq_tile(
       }
     }
     acc_rows<T, D>(acc_dq, ks, ds, nb, lane);
+    after();
   };
 
   if (grp <= td.tile) {
@@ -513,13 +514,24 @@ __device__ inline void bwd_dq_tile(
     const int kt = grp + G * it;
     const T* ks = glds + (it & 1) * 2 * L::TILE;
     const bool more = kt + G <= td.tile;
-    if (more) {
-      const long roff = (long)kTile * (kt + G) * kvstride;
-      const int nv = td.len - kTile * (kt + G);
-      kreg.load(kbase + roff, kvstride, nv, gtid);
-      vreg.load(vbase + roff, kvstride, nv, gtid);
-    }
-    if (decltype(diag)::value || kt < td.tile) step(ks, ks + L::TILE, diag);
+    auto prefetch = [&] {
+      if (more) {
+        const long roff = (long)kTile * (kt + G) * kvstride;
+        const int nv = td.len - kTile * (kt + G);
+        kreg.load(kbase + roff, kvstride, nv, gtid);
+        vreg.load(vbase + roff, kvstride, nv, gtid);
+      }
+    };
+    // The next tile's loads: for bf16 tensors at the end of this tile's step
+    // (issued first, they stall the wave while the memory pipeline is full;
+    // more implies kt < td.tile, so the step runs whenever they are due),
+    // for fp32 tensors up front (the registers fp32 tile loads hold across
+    // the step would not fit beside its products).
+    if constexpr (sizeof(IO) == 4) prefetch();
+    if (decltype(diag)::value || kt < td.tile)
+      step(ks, ks + L::TILE, diag, [&] {
+        if constexpr (sizeof(IO) != 4) prefetch();
+      });
     if (it < 6) GL_STAMP(kKernBwd, 3 + 3 * it);
     if (more) {
       T* nxt = glds + ((it + 1) & 1) * 2 * L::TILE;
@@ -684,7 +696,7 @@ __device__ inline void bwd_dkdv_tile(
 
   // One query tile: S, dP (keys as columns), P, dS; dV^T += dO^T P,
   // dK^T += Q^T dS.  DIAG: the query tile that holds the keys themselves.
-  auto step = [&](const unsigned char* base, auto diag) {
+  auto step = [&](const unsigned char* base, auto diag, auto mid) {
     constexpr bool DIAG = decltype(diag)::value;
     const T* qs = reinterpret_cast<const T*>(base);
     const T* dos = qs + L::TILE;
@@ -712,6 +724,7 @@ __device__ inline void bwd_dkdv_tile(
       }
     }
     acc_rows<T, D>(acc_dv, dos, p, 4, lane);
+    mid();
     acc_rows<T, D>(acc_dk, qs, ds, 4, lane);
   };
 
@@ -731,8 +744,15 @@ __device__ inline void bwd_dkdv_tile(
     const int qt = first + G * it;
     const unsigned char* base = gsm + (it & 1) * BUF;
     const bool more = qt + G < ntq;
-    if (more) load_tile(qt + G);
-    if (qt < ntq) step(base, diag);
+    // The next tile's loads: for bf16 tensors between this tile's dV and dK
+    // products (issued first, they stall the wave while the memory pipeline
+    // is full; more implies qt < ntq, so the step runs whenever they are
+    // due), for fp32 tensors up front (the registers fp32 tile loads hold
+    // across the step would not fit beside its products).
+    if (sizeof(IO) == 4 && more) load_tile(qt + G);
+    if (qt < ntq) step(base, diag, [&] {
+      if (sizeof(IO) != 4 && more) load_tile(qt + G);
+    });
     if (it < 6) GL_STAMP(kKernBwd, 3 + 3 * it);
     if (more) store_tile((it + 1) & 1, qt + G);
     if (it < 6) GL_STAMP(kKernBwd, 4 + 3 * it);
