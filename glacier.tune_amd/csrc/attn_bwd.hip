@@ -75,6 +75,19 @@ __device__ inline void lgkm_wait() {
   static_assert(N >= 0 && N < 16, "lgkmcnt range");
   asm volatile("s_waitcnt lgkmcnt(%0)" ::"i"(N) : "memory");
 }
+// lgkm_wait with a count known only after unrolling (a multiple of 2, < 16)
+__device__ inline void lgkm_wait_n(int n) {
+  switch (n) {
+    case 0: lgkm_wait<0>(); break;
+    case 2: lgkm_wait<2>(); break;
+    case 4: lgkm_wait<4>(); break;
+    case 6: lgkm_wait<6>(); break;
+    case 8: lgkm_wait<8>(); break;
+    case 10: lgkm_wait<10>(); break;
+    case 12: lgkm_wait<12>(); break;
+    default: lgkm_wait<0>(); break;
+  }
+}
 template <typename T>
 __device__ inline void tie(T& x) {
   asm volatile("" : "+v"(x));
@@ -362,6 +375,21 @@ __device__ inline void b2_dkdv(const TileDesc td, const bf16* __restrict__ q_rot
       if (kk + 1 < NKD) cur = nxt;
     }
     __builtin_amdgcn_sched_barrier(0);
+    // dV^T += dO^T P and dK^T += Q^T dS (below): each transposed A fragment
+    // feeds both key blocks.  The reads of column blocks 0 .. TRD - 2 are
+    // issued here, so the exponentials hide their latency; in the loop,
+    // TRD - 1 blocks' reads stay in flight during each block's MFMAs.
+    constexpr int TRD = 3;
+    bf16x4 t[TRD][4];
+    auto issue_tr = [&](bf16x4 (&x)[4], unsigned to) {
+      x[0] = read_tr_async<0>(oa + to);
+      x[1] = read_tr_async<32 * D>(oa + to);
+      x[2] = read_tr_async<0>(qa + to);
+      x[3] = read_tr_async<32 * D>(qa + to);
+    };
+#pragma unroll
+    for (int db = 0; db + 1 < TRD; ++db) issue_tr(t[db], to0 ^ (32u * db));
+    __builtin_amdgcn_sched_barrier(0);
     float pv[2][2][4], dsv[2][2][4];  // [query block][key block][row]
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb)
@@ -399,27 +427,13 @@ __device__ inline void b2_dkdv(const TileDesc td, const bf16* __restrict__ q_rot
           pB[kb][4 * qb + r] = (bf16)pv[qb][kb][r];
           dsB[kb][4 * qb + r] = (bf16)dsv[qb][kb][r];
         }
-    // dV^T += dO^T P and dK^T += Q^T dS: each transposed A fragment feeds
-    // both key blocks; column block db + 1's reads are in flight during db's
-    // MFMAs
     __builtin_amdgcn_sched_barrier(0);
-    bf16x4 t[2][4];
-    auto issue_tr = [&](bf16x4 (&x)[4], unsigned to) {
-      x[0] = read_tr_async<0>(oa + to);
-      x[1] = read_tr_async<32 * D>(oa + to);
-      x[2] = read_tr_async<0>(qa + to);
-      x[3] = read_tr_async<32 * D>(qa + to);
-    };
-    issue_tr(t[0], to0);
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {
-      bf16x4 (&x)[4] = t[db & 1];
-      if (db + 1 < NDB) {
-        issue_tr(t[(db + 1) & 1], to0 ^ (32u * (db + 1)));
-        lgkm_wait<4>();
-      } else {
-        lgkm_wait0();
-      }
+      bf16x4 (&x)[4] = t[db % TRD];
+      const int ahead = db + TRD - 1;  // the block whose reads go out now
+      if (ahead < NDB) issue_tr(t[ahead % TRD], to0 ^ (32u * ahead));
+      lgkm_wait_n(4 * ((ahead < NDB ? ahead : NDB - 1) - db));
       tie(x[0]); tie(x[1]); tie(x[2]); tie(x[3]);
       const bf16x8 ao = join(x[0], x[1]), aq = join(x[2], x[3]);
 #pragma unroll
@@ -649,6 +663,18 @@ __device__ inline void b2_dq(const TileDesc td, const bf16* __restrict__ q_rot,
       }
     }
     __builtin_amdgcn_sched_barrier(0);
+    // dQ^T += K^T dS^T (below): each transposed K fragment feeds both query
+    // blocks.  The reads of column blocks 0 .. TRD - 2 are issued here, so
+    // the exponentials hide their latency; in the loop, TRD - 1 blocks'
+    // reads stay in flight during each block's MFMAs.
+    constexpr int TRD = 3;
+    bf16x4 t[TRD][2];
+#pragma unroll
+    for (int db = 0; db + 1 < TRD; ++db) {
+      t[db][0] = read_tr_async<0>(ka + (to0 ^ (32u * db)));
+      t[db][1] = read_tr_async<32 * D>(ka + (to0 ^ (32u * db)));
+    }
+    __builtin_amdgcn_sched_barrier(0);
     float pv[2][2][4];  // [key block][query block][row]
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb)
@@ -674,23 +700,17 @@ __device__ inline void b2_dq(const TileDesc td, const bf16* __restrict__ q_rot,
 #pragma unroll
         for (int r = 0; r < 4; ++r)
           dsB[qb][4 * kb + r] = (bf16)(pv[kb][qb][r] * (dp[kb][qb][r] - dr[qb]));
-    // dQ^T += K^T dS^T: each transposed K fragment feeds both query blocks;
-    // column block db + 1's reads are in flight during db's MFMAs
     __builtin_amdgcn_sched_barrier(0);
-    bf16x4 t[2][2];
-    t[0][0] = read_tr_async<0>(ka + to0);
-    t[0][1] = read_tr_async<32 * D>(ka + to0);
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {
-      bf16x4 (&x)[2] = t[db & 1];
-      if (db + 1 < NDB) {
-        const unsigned to = to0 ^ (32u * (db + 1));
-        t[(db + 1) & 1][0] = read_tr_async<0>(ka + to);
-        t[(db + 1) & 1][1] = read_tr_async<32 * D>(ka + to);
-        lgkm_wait<2>();
-      } else {
-        lgkm_wait0();
+      bf16x4 (&x)[2] = t[db % TRD];
+      const int ahead = db + TRD - 1;
+      if (ahead < NDB) {
+        const unsigned to = to0 ^ (32u * ahead);
+        t[ahead % TRD][0] = read_tr_async<0>(ka + to);
+        t[ahead % TRD][1] = read_tr_async<32 * D>(ka + to);
       }
+      lgkm_wait_n(2 * ((ahead < NDB ? ahead : NDB - 1) - db));
       tie(x[0]); tie(x[1]);
       const bf16x8 a = join(x[0], x[1]);
 #pragma unroll
