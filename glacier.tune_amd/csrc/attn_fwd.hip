@@ -211,7 +211,7 @@ __global__ __launch_bounds__(kFwdWaves * 64) void attn_fwd_kernel_ks(
   // O^T accumulators and per-query row sums (MFMA accumulators pinned in
   // AGPRs), the reference maxima the probabilities are taken against.
   f32x4 o[NDB][4], lsum[4];
-  float m_ref[4], m_seen[4], mt[4];
+  float m_ref[4], m_seen[4];
 #pragma unroll
   for (int qb = 0; qb < 4; ++qb) {
     // a wave without chunks merges as (kNegBig, 0, 0)
@@ -309,9 +309,12 @@ __global__ __launch_bounds__(kFwdWaves * 64) void attn_fwd_kernel_ks(
               sn[kb][qb][r] = (koff + 16 * kb + 4 * g + r <= 16 * qb + c) ? sn[kb][qb][r] : -INFINITY;
             mloc = fmaxf(mloc, sn[kb][qb][r]);
           }
-        mt[qb] = col_max_swap(mloc) * scale_log2;
-        grew = grew || (mt[qb] > m_ref[qb] + kRescale);
-        m_seen[qb] = fmaxf(m_seen[qb], mt[qb]);
+        // lane-local: a chunk exceeds a column's reference iff one of the
+        // column's four lanes does, and the maxima seen become the rescue
+        // pass's references only after one cross-lane reduction at the end
+        const float ml = mloc * scale_log2;
+        grew = grew || (ml > m_ref[qb] + kRescale);
+        m_seen[qb] = fmaxf(m_seen[qb], ml);
       }
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
@@ -421,6 +424,8 @@ __global__ __launch_bounds__(kFwdWaves * 64) void attn_fwd_kernel_ks(
     fence_acc(o, lsum);
     GL_STAMP(kKernFwd, 17);
     if (__builtin_amdgcn_ballot_w64(grew) == 0) break;
+#pragma unroll
+    for (int qb = 0; qb < 4; ++qb) m_seen[qb] = col_max_swap(m_seen[qb]);
 #pragma unroll
     for (int qb = 0; qb < 4; ++qb) m_ref[qb] = m_seen[qb];
   }

@@ -405,6 +405,61 @@ def test_long_sequence_matches_torch_fp32_reference(engines, S, D):
     assert all(e <= BF16_GATE for e in err.values()), err
 
 
+@pytest.mark.parametrize("prec,S,Hq,Hkv,D", [
+    (ga.PREC_BF16, 512, 28, 4, 128),
+    (ga.PREC_BF16, 512, 14, 2, 64),
+    (ga.PREC_BF16, 1536, 28, 4, 128),
+    (ga.PREC_FP32, 512, 28, 4, 128),
+])
+def test_scores_growing_far_past_the_first_chunk(engines, prec, S, Hq, Hkv, D):
+    """Keys from position 256 on score about 6.4e5 above the earlier ones
+    (value 800 in the lowest-frequency RoPE pair, which barely rotates: more
+    than 2^16 in the exponent at either head size), so every
+    query past 256 sees its maxima grow far beyond those of its first key
+    chunk: the bf16 forward's rescue pass (references re-taken from the
+    maxima seen; without it the probabilities overflow) and the fp32
+    forward's rescaling must give finite results that match the float32
+    reference.  At scores near 6.4e5, fp32 resolves about 0.06 and a bf16
+    operand of 800 about 4 (the big component's rotation, under 0.01, is
+    rounded away), so the bf16 mode is held to 5e-2 on O and 5e-5 on lse
+    (about 3 nats at lse ~ 5.7e4) and the fp32 mode to 5e-3 and 1e-6; the
+    backward is checked for finite values only (its row sums of P (dP - D)
+    cancel at that scale in every fp32 implementation, the reference's
+    included)."""
+    base = 1.0e6
+    dim = D // 2 - 1  # the pair (dim, dim + D/2) rotates by at most S * 1.2e-6 rad
+    cu = np.array([0, S], np.int32)
+    _say(f"[stress] prec={prec} S={S} Hq={Hq} D={D}")
+    g = torch.Generator(device="cuda").manual_seed(7)
+    q = torch.randn(S, Hq, D, device="cuda", generator=g)
+    k = torch.randn(S, Hkv, D, device="cuda", generator=g)
+    v = torch.randn(S, Hkv, D, device="cuda", generator=g)
+    dO = 0.01 * torch.randn(S, Hq, D, device="cuda", generator=g)
+    q[:, :, dim] = 800.0
+    k[:, :, dim] = 0.0
+    k[256:, :, dim] = 800.0
+    if prec == ga.PREC_BF16:
+        q, k, v, dO = (x.bfloat16() for x in (q, k, v, dO))
+    prev_tf32 = torch.backends.cuda.matmul.allow_tf32
+    torch.backends.cuda.matmul.allow_tf32 = False
+    try:
+        eng = engines[prec]
+        out, lse, q_rot, k_rot = eng.forward(q, k, v, base)
+        dq, dk, dv = eng.backward(dO, q_rot, k_rot, v, out, lse, base)
+        torch.cuda.synchronize()
+        ref = torch_reference(q, k, v, dO, base, cu)
+    finally:
+        torch.backends.cuda.matmul.allow_tf32 = prev_tf32
+    got = dict(out=out, lse=lse, dq=dq, dk=dk, dv=dv)
+    for key, t in got.items():
+        assert torch.isfinite(t.float()).all(), f"{key} has non-finite values"
+    err = {key: float((got[key].float() - ref[key]).abs().max() / ref[key].abs().max())
+           for key in ("out", "lse")}
+    _say(f"  errors {err}")
+    gate_out, gate_lse = (5e-2, 5e-5) if prec == ga.PREC_BF16 else (5e-3, 1e-6)
+    assert err["out"] <= gate_out and err["lse"] <= gate_lse, err
+
+
 LARGE_FP32 = [
     ("long_s4096", [4096], 28, 4, 1.0e6),
     ("llama3_b2_s2048", [2048, 2048], 32, 8, 5.0e5),
