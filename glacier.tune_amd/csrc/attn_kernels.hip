@@ -459,7 +459,7 @@ __device__ inline void bwd_dq_tile(
 
   float drow = 0.0f, nlse2 = 0.0f;  // set once the row terms are staged
   // One key tile: S, dP, P from lse, dS = P (dP - D), dQ^T += K^T dS^T.
-  auto step = [&](const T* ks, const T* vs, auto diag, auto after) {
+  auto step = [&](const T* ks, const T* vs, auto diag, auto mid, auto after) {
     constexpr bool DIAG = decltype(diag)::value;
     const int nb = DIAG ? (wq + 1) : 4;
     float ds[4][4];
@@ -481,6 +481,7 @@ __device__ inline void bwd_dq_tile(
         ds[b][r] = x;
       }
     }
+    mid();
     acc_rows<T, D>(acc_dq, ks, ds, nb, lane);
     after();
   };
@@ -510,7 +511,7 @@ __device__ inline void bwd_dq_tile(
   GL_STAMP(kKernBwd, 2);
 
   const int nit = (td.tile + G) / G;
-  auto iteration = [&](int it, auto diag) {
+  auto iteration = [&](int it, auto diag, auto mid) {
     const int kt = grp + G * it;
     const T* ks = glds + (it & 1) * 2 * L::TILE;
     const bool more = kt + G <= td.tile;
@@ -529,7 +530,7 @@ __device__ inline void bwd_dq_tile(
     // the step would not fit beside its products).
     if constexpr (sizeof(IO) == 4) prefetch();
     if (decltype(diag)::value || kt < td.tile)
-      step(ks, ks + L::TILE, diag, [&] {
+      step(ks, ks + L::TILE, diag, mid, [&] {
         if constexpr (sizeof(IO) != 4) prefetch();
       });
     if (it < 6) GL_STAMP(kKernBwd, 3 + 3 * it);
@@ -546,11 +547,30 @@ __device__ inline void bwd_dq_tile(
   // diagonal tile is the last iteration of one group.  Peeling it keeps a
   // single step variant inside the loop (two variants in one loop body make
   // the register allocator copy the loop-carried registers every iteration).
-  for (int it = 0; it + 1 < nit; ++it) iteration(it, std::false_type{});
+  for (int it = 0; it + 1 < nit; ++it) iteration(it, std::false_type{}, [] {});
+  // The inverse RoPE's cos/sin values (group 0 applies it).  For bf16
+  // tensors they are loaded inside the last iteration's step (between its
+  // dS block and its product; that iteration has no next tile to load), so
+  // the step hides their latency; fp32 tensors load them in the epilogue
+  // (held across the step, they would not fit beside the fp32 tile
+  // registers).
+  constexpr bool kEarlyRope = sizeof(IO) != 4;
+  f32x4 rc[D / 32], rs[D / 32];
+  const long ti0 = (long)(qvalid ? qrow : 0) * H;
+  auto load_rope = [&] {
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db) {
+      rc[db] = *reinterpret_cast<const f32x4*>(cos_t + ti0 + 16 * db + 4 * g);
+      rs[db] = *reinterpret_cast<const f32x4*>(sin_t + ti0 + 16 * db + 4 * g);
+    }
+  };
+  auto rope_mid = [&] {
+    if (kEarlyRope && grp == 0) load_rope();
+  };
   if (grp + G * (nit - 1) == td.tile)
-    iteration(nit - 1, std::true_type{});
+    iteration(nit - 1, std::true_type{}, rope_mid);
   else
-    iteration(nit - 1, std::false_type{});
+    iteration(nit - 1, std::false_type{}, rope_mid);
 
   GL_STAMP(kKernBwd, 21);
   if constexpr (G == 2) {
@@ -560,6 +580,7 @@ __device__ inline void bwd_dq_tile(
       for (int db = 0; db < D / 16; ++db) cmb[db * 64] = acc_dq[db];
     }
     __syncthreads();
+    GL_STAMP(kKernBwd, 23);
     if (grp == 0) {
 #pragma unroll
       for (int db = 0; db < D / 16; ++db) acc_dq[db] += cmb[db * 64];
@@ -573,18 +594,16 @@ __device__ inline void bwd_dq_tile(
   constexpr int SR = D + 8;
   IO* const stq = reinterpret_cast<IO*>(smem_raw);
   if (grp == 0) {
-    const long ti0 = (long)(qvalid ? qrow : 0) * H;
+    if (!kEarlyRope) load_rope();
 #pragma unroll
     for (int db = 0; db < D / 32; ++db) {
       const f32x4 lo = acc_dq[db] * scale, hi = acc_dq[db + D / 32] * scale;
       const int d0 = 16 * db + 4 * g;
-      const f32x4 cs = *reinterpret_cast<const f32x4*>(cos_t + ti0 + d0);
-      const f32x4 sn = *reinterpret_cast<const f32x4*>(sin_t + ti0 + d0);
       f32x4 y0, y1;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         float a, b;
-        rope_inv(lo[r], hi[r], cs[r], sn[r], a, b);
+        rope_inv(lo[r], hi[r], rc[db][r], rs[db][r], a, b);
         y0[r] = a;
         y1[r] = b;
       }
@@ -593,6 +612,7 @@ __device__ inline void bwd_dq_tile(
     }
   }
   __syncthreads();
+  GL_STAMP(kKernBwd, 24);
   constexpr int EPC = 16 / sizeof(IO);  // elements per 16-byte piece
   constexpr int PPR = D / EPC;          // pieces per row
 #pragma unroll
@@ -790,6 +810,7 @@ __device__ inline void bwd_dkdv_tile(
       }
     }
     __syncthreads();
+    GL_STAMP(kKernBwd, 23);
     if (grp == 0) {
 #pragma unroll
       for (int db = 0; db < D / 16; ++db) {
@@ -805,6 +826,7 @@ __device__ inline void bwd_dkdv_tile(
     }
   }
   __syncthreads();
+  GL_STAMP(kKernBwd, 24);
   constexpr int V4 = D / 4;  // 16-byte pieces per row
 #pragma unroll
   for (int i = tid; i < kTile * V4; i += kThreads * G) {
