@@ -790,52 +790,62 @@ __device__ inline void bwd_dkdv_tile(
   for (int it = it0; it < nit; ++it) iteration(it, std::false_type{});
 
   GL_STAMP(kKernBwd, 21);
-  // Merge the groups and write whole rows: the [64 keys][D] fp32 dK and dV
-  // tiles are staged in LDS (row stride D + 4 floats, so the 16 key rows of
-  // a wave's store fall in distinct banks), then every thread stores 16-byte
-  // pieces of consecutive rows.  Lane (g, c) holds d = 16 db + 4 g + 0..3 of
-  // key 16 wq + c.
+  // Merge the groups and write whole rows.  Group 0 hands its fp32 dK
+  // accumulators to group 1 through LDS and group 1 its dV to group 0 (row
+  // stride D + 4 floats, so the 16 key rows of a wave's store fall in
+  // distinct banks); each group adds the other's half to its own (group 0's
+  // sum first either way) and stages that tensor's [64 keys][D] rows in the
+  // partials' dtype, so the row stores read a quarter of the fp32 bytes
+  // back for bf16.  Then every thread stores 16-byte pieces of consecutive
+  // rows.  Lane (g, c) holds d = 16 db + 4 g + 0..3 of key 16 wq + c.
   constexpr int SR = D + 4;
-  static_assert(2 * kTile * SR * sizeof(float) <= 2 * BUF * G, "staging exceeds the LDS buffers");
+  constexpr int SRO = D + (sizeof(IO) == 4 ? 4 : 8);  // row stride of the staged rows
+  constexpr size_t MERGE = G == 2 ? 2 * kTile * SR * sizeof(float) : 0;
+  static_assert(MERGE + 2 * kTile * SRO * sizeof(IO) <= 2 * BUF * G, "staging exceeds the LDS buffers");
   float* const stk = reinterpret_cast<float*>(smem_raw);
   float* const stv = stk + kTile * SR;
-  f32x4* const pk = reinterpret_cast<f32x4*>(stk + (16 * wq + c) * SR + 4 * g);
-  f32x4* const pv = reinterpret_cast<f32x4*>(stv + (16 * wq + c) * SR + 4 * g);
+  IO* const sok = reinterpret_cast<IO*>(smem_raw + MERGE);
+  IO* const sov = sok + kTile * SRO;
+  IO* const ok = sok + (16 * wq + c) * SRO + 4 * g;
+  IO* const ov = sov + (16 * wq + c) * SRO + 4 * g;
   if constexpr (G == 2) {
-    if (grp == 1) {
+    f32x4* const pk = reinterpret_cast<f32x4*>(stk + (16 * wq + c) * SR + 4 * g);
+    f32x4* const pv = reinterpret_cast<f32x4*>(stv + (16 * wq + c) * SR + 4 * g);
+    if (grp == 0) {
 #pragma unroll
-      for (int db = 0; db < D / 16; ++db) {
-        pk[4 * db] = acc_dk[db];
-        pv[4 * db] = acc_dv[db];
-      }
+      for (int db = 0; db < D / 16; ++db) pk[4 * db] = acc_dk[db];
+    } else {
+#pragma unroll
+      for (int db = 0; db < D / 16; ++db) pv[4 * db] = acc_dv[db];
     }
     __syncthreads();
     GL_STAMP(kKernBwd, 23);
     if (grp == 0) {
 #pragma unroll
-      for (int db = 0; db < D / 16; ++db) {
-        pk[4 * db] = (acc_dk[db] + pk[4 * db]) * scale;
-        pv[4 * db] = acc_dv[db] + pv[4 * db];
-      }
+      for (int db = 0; db < D / 16; ++db) store4(ov + 16 * db, acc_dv[db] + pv[4 * db]);
+    } else {
+#pragma unroll
+      for (int db = 0; db < D / 16; ++db) store4(ok + 16 * db, (pk[4 * db] + acc_dk[db]) * scale);
     }
   } else {
 #pragma unroll
     for (int db = 0; db < D / 16; ++db) {
-      pk[4 * db] = acc_dk[db] * scale;
-      pv[4 * db] = acc_dv[db];
+      store4(ok + 16 * db, acc_dk[db] * scale);
+      store4(ov + 16 * db, acc_dv[db]);
     }
   }
   __syncthreads();
   GL_STAMP(kKernBwd, 24);
-  constexpr int V4 = D / 4;  // 16-byte pieces per row
+  constexpr int EPC = 16 / sizeof(IO);  // elements per 16-byte piece
+  constexpr int PPR = D / EPC;          // pieces per row
 #pragma unroll
-  for (int i = tid; i < kTile * V4; i += kThreads * G) {
-    const int r = i / V4, c4 = i % V4;
+  for (int i = tid; i < kTile * PPR; i += kThreads * G) {
+    const int r = i / PPR, pc = i % PPR;
     const int key = kTile * td.tile + r;
     if (key < td.len) {
-      const long wb = ((long)(td.tok0 + key) * n_heads_q + h) * D + 4 * c4;
-      store4(wk + wb, *reinterpret_cast<const f32x4*>(stk + r * SR + 4 * c4));
-      store4(wv + wb, *reinterpret_cast<const f32x4*>(stv + r * SR + 4 * c4));
+      const long wb = ((long)(td.tok0 + key) * n_heads_q + h) * D + pc * EPC;
+      *reinterpret_cast<uint4*>(wk + wb) = *reinterpret_cast<const uint4*>(sok + r * SRO + pc * EPC);
+      *reinterpret_cast<uint4*>(wv + wb) = *reinterpret_cast<const uint4*>(sov + r * SRO + pc * EPC);
     }
   }
   GL_STAMP(kKernBwd, 22);
