@@ -533,6 +533,8 @@ __device__ inline void bwd_dq_tile(
       step(ks, ks + L::TILE, diag, mid, [&] {
         if constexpr (sizeof(IO) != 4) prefetch();
       });
+    else
+      mid();  // a group with no tile left in this iteration
     if (it < 6) GL_STAMP(kKernBwd, 3 + 3 * it);
     if (more) {
       T* nxt = glds + ((it + 1) & 1) * 2 * L::TILE;
@@ -548,24 +550,30 @@ __device__ inline void bwd_dq_tile(
   // single step variant inside the loop (two variants in one loop body make
   // the register allocator copy the loop-carried registers every iteration).
   for (int it = 0; it + 1 < nit; ++it) iteration(it, std::false_type{}, [] {});
-  // The inverse RoPE's cos/sin values (group 0 applies it).  For bf16
-  // tensors they are loaded inside the last iteration's step (between its
-  // dS block and its product; that iteration has no next tile to load), so
-  // the step hides their latency; fp32 tensors load them in the epilogue
-  // (held across the step, they would not fit beside the fp32 tile
-  // registers).
+  // The epilogue scales dQ, applies the inverse RoPE at the query's
+  // position and stores whole rows.  Rotation block p holds the lane's
+  // d = 16 p + 4 g + 0..3 (acc_dq[p]) and d + D/2 (acc_dq[p + NP]); with
+  // two groups, each finishes half of the blocks (group 0 the first half)
+  // after adding the other group's accumulators for them, received through
+  // LDS (group 0's sum first either way).  The blocks' cos/sin values: for
+  // bf16 tensors loaded inside the last iteration's step (between its dS
+  // block and its product; that iteration has no next tile to load), so the
+  // step hides their latency; fp32 tensors load them in the epilogue (held
+  // across the step, they would not fit beside the fp32 tile registers).
+  constexpr int NP = D / 32;  // rotation blocks
+  constexpr int PB = NP / G;  // blocks each group finishes
   constexpr bool kEarlyRope = sizeof(IO) != 4;
-  f32x4 rc[D / 32], rs[D / 32];
-  const long ti0 = (long)(qvalid ? qrow : 0) * H;
+  f32x4 rc[PB], rs[PB];
+  const long ti0 = (long)(qvalid ? qrow : 0) * H + 16 * PB * grp + 4 * g;
   auto load_rope = [&] {
 #pragma unroll
-    for (int db = 0; db < D / 32; ++db) {
-      rc[db] = *reinterpret_cast<const f32x4*>(cos_t + ti0 + 16 * db + 4 * g);
-      rs[db] = *reinterpret_cast<const f32x4*>(sin_t + ti0 + 16 * db + 4 * g);
+    for (int j = 0; j < PB; ++j) {
+      rc[j] = *reinterpret_cast<const f32x4*>(cos_t + ti0 + 16 * j);
+      rs[j] = *reinterpret_cast<const f32x4*>(sin_t + ti0 + 16 * j);
     }
   };
   auto rope_mid = [&] {
-    if (kEarlyRope && grp == 0) load_rope();
+    if (kEarlyRope) load_rope();
   };
   if (grp + G * (nit - 1) == td.tile)
     iteration(nit - 1, std::true_type{}, rope_mid);
@@ -573,43 +581,62 @@ __device__ inline void bwd_dq_tile(
     iteration(nit - 1, std::false_type{}, rope_mid);
 
   GL_STAMP(kKernBwd, 21);
-  if constexpr (G == 2) {
-    f32x4* const cmb = reinterpret_cast<f32x4*>(lds + 4 * L::TILE) + wq * (D / 16) * 64 + lane;
-    if (grp == 1) {
+  // GR: the group as a constant (accumulators are indexed at compile time)
+  f32x4* const cx = reinterpret_cast<f32x4*>(lds + 4 * L::TILE);  // [G][4 waves][2 PB][64 lanes]
+  auto hand_over = [&](auto grc) {
+    constexpr int GR = decltype(grc)::value;
+    f32x4* const o = cx + (GR * 4 + wq) * 2 * PB * 64 + lane;
 #pragma unroll
-      for (int db = 0; db < D / 16; ++db) cmb[db * 64] = acc_dq[db];
+    for (int j = 0; j < PB; ++j) {
+      o[2 * j * 64] = acc_dq[(1 - GR) * PB + j];
+      o[(2 * j + 1) * 64] = acc_dq[(1 - GR) * PB + j + NP];
     }
-    __syncthreads();
-    GL_STAMP(kKernBwd, 23);
-    if (grp == 0) {
-#pragma unroll
-      for (int db = 0; db < D / 16; ++db) acc_dq[db] += cmb[db * 64];
-    }
-  }
-
-  // Scale, inverse RoPE at the query's position, and write whole rows: the
-  // [64][D] dQ tile is staged in LDS in the output dtype (row stride D + 8),
-  // then every thread stores 16-byte pieces of consecutive rows.  Lane
-  // (g, c) holds d = 16 db + 4 g + 0..3 (and d + D/2) of query 16 wq + c.
+  };
+  // The [64][D] dQ tile is staged in LDS in the output dtype (row stride
+  // D + 8), then every thread stores 16-byte pieces of consecutive rows.
   constexpr int SR = D + 8;
   IO* const stq = reinterpret_cast<IO*>(smem_raw);
-  if (grp == 0) {
+  auto finish = [&](auto grc) {
+    constexpr int GR = decltype(grc)::value;
+    if constexpr (G == 2) {
+      const f32x4* const in = cx + ((1 - GR) * 4 + wq) * 2 * PB * 64 + lane;
+#pragma unroll
+      for (int j = 0; j < PB; ++j) {
+        acc_dq[GR * PB + j] += in[2 * j * 64];
+        acc_dq[GR * PB + j + NP] += in[(2 * j + 1) * 64];
+      }
+    }
     if (!kEarlyRope) load_rope();
 #pragma unroll
-    for (int db = 0; db < D / 32; ++db) {
-      const f32x4 lo = acc_dq[db] * scale, hi = acc_dq[db + D / 32] * scale;
-      const int d0 = 16 * db + 4 * g;
+    for (int j = 0; j < PB; ++j) {
+      const int pb = GR * PB + j;
+      const f32x4 lo = acc_dq[pb] * scale, hi = acc_dq[pb + NP] * scale;
+      const int d0 = 16 * pb + 4 * g;
       f32x4 y0, y1;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         float a, b;
-        rope_inv(lo[r], hi[r], rc[db][r], rs[db][r], a, b);
+        rope_inv(lo[r], hi[r], rc[j][r], rs[j][r], a, b);
         y0[r] = a;
         y1[r] = b;
       }
       store4(stq + (16 * wq + c) * SR + d0, y0);
       store4(stq + (16 * wq + c) * SR + H + d0, y1);
     }
+  };
+  if constexpr (G == 2) {
+    if (grp == 0)
+      hand_over(std::integral_constant<int, 0>{});
+    else
+      hand_over(std::integral_constant<int, 1>{});
+    __syncthreads();
+    GL_STAMP(kKernBwd, 23);
+    if (grp == 0)
+      finish(std::integral_constant<int, 0>{});
+    else
+      finish(std::integral_constant<int, 1>{});
+  } else {
+    finish(std::integral_constant<int, 0>{});
   }
   __syncthreads();
   GL_STAMP(kKernBwd, 24);
