@@ -558,36 +558,31 @@ def main():
     net = [Layer() for _ in range(layers)]
     eng = ga.GpuAttentionEngine(0, ga.PREC_BF16)
 
-    def fwd(L, save):
-        if save:
-            eng.forward(L.q, L.k, L.v, theta, cu_seqlens=cu, out=L.out, lse=L.lse,
-                        q_rot=L.q_rot, k_rot=L.k_rot)
-        else:
-            eng.forward(L.q, L.k, L.v, theta, cu_seqlens=cu, out=L.out, save=False)
-
-    def bwd(L):
-        eng.backward(L.dO, L.q_rot, L.k_rot, L.v, L.out, L.lse, theta, cu_seqlens=cu,
-                     dq=L.dq, dk=L.dk, dv=L.dv)
-
-    # One layer: the forward + backward with their arguments checked and
-    # converted once (eng.bind_step), so each timed step is two C calls.
-    bound = None
+    # Every call with its arguments checked and converted once
+    # (eng.bind_forward / bind_backward / bind_step), so each timed call is
+    # one C call.  One layer: forward + backward.  Several layers: the
+    # checkpointed step (forward without saving through every layer, then
+    # per layer from the last: the recompute forward that saves, and the
+    # backward).
     if layers == 1:
         L0 = net[0]
         bound = eng.bind_step(dict(q=L0.q, k=L0.k, v=L0.v, out=L0.out, lse=L0.lse,
                                    q_rot=L0.q_rot, k_rot=L0.k_rot),
                               dict(d_out=L0.dO, dq=L0.dq, dk=L0.dk, dv=L0.dv), theta,
                               cu_seqlens=cu)
+        calls = [bound]
+    else:
+        fwd_plain = [eng.bind_forward(L.q, L.k, L.v, L.out, theta, cu_seqlens=cu) for L in net]
+        fwd_save = [eng.bind_forward(L.q, L.k, L.v, L.out, theta, cu_seqlens=cu, lse=L.lse,
+                                     q_rot=L.q_rot, k_rot=L.k_rot) for L in net]
+        bwd = [eng.bind_backward(L.dO, L.q_rot, L.k_rot, L.v, L.out, L.lse, L.dq, L.dk, L.dv,
+                                 theta, cu_seqlens=cu) for L in net]
+        calls = fwd_plain + [c for i in reversed(range(layers)) for c in (fwd_save[i], bwd[i])]
+        bound = calls[0]  # rebind() binds the engine's stream for every bound call
 
     def step():
-        if layers == 1:
-            bound()
-            return
-        for L in net:
-            fwd(L, False)
-        for L in reversed(net):
-            fwd(L, True)
-            bwd(L)
+        for c in calls:
+            c()
 
     for _ in range(args.warmup):
         step()
@@ -613,11 +608,9 @@ def main():
     try:
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
-            if bound is not None:
-                bound.rebind()  # enqueue on the capture stream
+            bound.rebind()  # enqueue on the capture stream
             step()
-        if bound is not None:
-            bound.rebind()
+        bound.rebind()
         for _ in range(3):
             graph.replay()
         torch.cuda.synchronize()
@@ -630,11 +623,12 @@ def main():
     except Exception as e:  # capture unsupported: report the eager rate
         graph_error = f"{type(e).__name__}: {e}"
         torch.cuda.synchronize()
-    # The eager rate is the measured one when the host enqueues faster than
-    # the device runs (host_bound false); otherwise the graph replay, which
-    # the host cannot bound, is.
+    # The measured rate is the eager one unless the graph replay of the same
+    # step is faster: the eager loop is then bound by the host (the enqueue
+    # itself, or the device idling between bursts of it), which the replay
+    # cannot be.
     host_bound = host_ms >= ms_eager
-    use_graph = host_bound and ms_graph is not None
+    use_graph = ms_graph is not None and ms_graph < ms_eager
     ms = ms_graph if use_graph else ms_eager
 
     # 12 D flop per unmasked (query, key, head) per layer, plus 4 D for the
@@ -692,10 +686,11 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "timing": {
-            "method": ("hipGraph replay of one captured step (the eager loop is host-bound)"
+            "method": ("hipGraph replay of one captured step (faster than the eager loop, "
+                       "which the host bounds)"
                        if use_graph else
-                       "eager: K steps enqueued back to back between two events; the host "
-                       "enqueues faster than the device runs (host_bound false)"),
+                       "eager: K steps enqueued back to back between two events (faster than "
+                       "the graph replay of the same step)"),
             "graph_error": graph_error,
             "ms_per_step_graph": None if ms_graph is None else round(ms_graph, 6),
             "ms_per_step_eager": round(ms_eager, 6),

@@ -484,6 +484,52 @@ class GpuAttentionEngine:
                                             self._ptr(dk), self._ptr(dv)))
         return dq, dk, dv
 
+    def _bound(self, fn, args, desc, keep):
+        """A callable that enqueues fn(*args) on the stream bound last."""
+        def call():
+            rc = fn(*args)
+            if rc != OK:
+                _check(rc)
+
+        call._keep = (desc, keep)  # the descriptor and cu_seqlens outlive the calls
+        call.rebind = self._bind_stream
+        return call
+
+    def bind_forward(self, q, k, v, out, rope_freq_base, precision=None, cu_seqlens=None,
+                     lse=None, q_rot=None, k_rot=None):
+        """forward() on fixed tensors with every argument checked and
+        converted once: returns call(), which enqueues glacier_attn_forward on
+        torch's current stream (bound now; call.rebind() binds it again).
+        Saves lse/q_rot/k_rot when all three are given, none of them
+        otherwise.  The tensors must stay alive and in place while it is used."""
+        save = lse is not None or q_rot is not None or k_rot is not None
+        if save and (lse is None or q_rot is None or k_rot is None):
+            raise ValueError("bind_forward saves lse, q_rot and k_rot together")
+        check_forward_args(q, k, v, out, lse, q_rot, k_rot)
+        prec = self.precision if precision is None else precision
+        T, hq, d = q.shape
+        desc, keep = self._desc(T, hq, k.shape[1], d, rope_freq_base, prec, self._io_of(q),
+                                cu_seqlens)
+        self._bind_stream()
+        p = self._ptr
+        args = (self._h, ctypes.byref(desc), p(q), p(k), p(v), p(out), p(lse), p(q_rot), p(k_rot))
+        return self._bound(load().glacier_attn_forward, args, desc, keep)
+
+    def bind_backward(self, d_out, q_rot, k_rot, v, out, lse, dq, dk, dv, rope_freq_base,
+                      precision=None, cu_seqlens=None):
+        """backward() on fixed tensors with every argument checked and
+        converted once (see bind_forward)."""
+        check_backward_args(d_out, q_rot, k_rot, v, out, lse, dq, dk, dv)
+        prec = self.precision if precision is None else precision
+        T, hq, d = q_rot.shape
+        desc, keep = self._desc(T, hq, k_rot.shape[1], d, rope_freq_base, prec,
+                                self._io_of(q_rot), cu_seqlens)
+        self._bind_stream()
+        p = self._ptr
+        args = (self._h, ctypes.byref(desc), p(d_out), p(q_rot), p(k_rot), p(v), p(out), p(lse),
+                p(dq), p(dk), p(dv))
+        return self._bound(load().glacier_attn_backward, args, desc, keep)
+
     def bind_step(self, fwd, bwd, rope_freq_base, precision=None, cu_seqlens=None):
         """A forward + backward on fixed tensors with every argument checked
         and converted once: returns step(), which enqueues glacier_attn_forward

@@ -288,6 +288,45 @@ def test_recompute_and_backward_are_bitwise_repeatable(engines, prec):
         assert np.array_equal(a[key], b[key]), key
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "fp32"])
+def test_bound_calls_match_unbound_calls(engines, dtype):
+    """bind_forward / bind_backward / bind_step (arguments checked once) give
+    the bits of forward() / backward() on the same tensors: with and without
+    saving, on a packed batch."""
+    Hq, Hkv, D, base = 14, 2, 64, 1.0e6
+    lens = [100, 37, 200]
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    T = int(cu[-1])
+    _say(f"[bound calls] {dtype} lens={lens}")
+    eng = engines[ga.PREC_BF16]
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    q, k, v, dO = (_dev(x, tdt) for x in make_inputs(T, Hq, Hkv, D, 11, dtype == "bf16"))
+    out, lse, q_rot, k_rot = eng.forward(q, k, v, base, cu_seqlens=cu)
+    dq, dk, dv = eng.backward(dO, q_rot, k_rot, v, out, lse, base, cu_seqlens=cu)
+    out_ns, _, _, _ = eng.forward(q, k, v, base, cu_seqlens=cu, save=False)
+
+    e = torch.empty_like
+    b_out_ns = e(out)
+    eng.bind_forward(q, k, v, b_out_ns, base, cu_seqlens=cu)()
+    b = dict(out=e(out), lse=e(lse), q_rot=e(q_rot), k_rot=e(k_rot), dq=e(dq), dk=e(dk), dv=e(dv))
+    eng.bind_forward(q, k, v, b["out"], base, cu_seqlens=cu, lse=b["lse"], q_rot=b["q_rot"],
+                     k_rot=b["k_rot"])()
+    eng.bind_backward(dO, b["q_rot"], b["k_rot"], v, b["out"], b["lse"], b["dq"], b["dk"],
+                      b["dv"], base, cu_seqlens=cu)()
+    s = dict(out=e(out), lse=e(lse), q_rot=e(q_rot), k_rot=e(k_rot), dq=e(dq), dk=e(dk), dv=e(dv))
+    eng.bind_step(dict(q=q, k=k, v=v, out=s["out"], lse=s["lse"], q_rot=s["q_rot"],
+                       k_rot=s["k_rot"]),
+                  dict(d_out=dO, dq=s["dq"], dk=s["dk"], dv=s["dv"]), base, cu_seqlens=cu)()
+    torch.cuda.synchronize()
+    ref = dict(out=out, lse=lse, q_rot=q_rot, k_rot=k_rot, dq=dq, dk=dk, dv=dv)
+    assert torch.equal(b_out_ns, out_ns)
+    for name, t in ref.items():
+        assert torch.equal(b[name], t), name
+        assert torch.equal(s[name], t), name
+    with pytest.raises(ValueError):
+        eng.bind_forward(q, k, v, e(out), base, cu_seqlens=cu, lse=e(lse))
+
+
 def test_varlen_packed_batch_matches_oracle_per_segment(engines, bf16_kernels):
     """BASELINE configs[2] shape: 4 packed sequences, lengths U[64,512] (seed 5),
     block-diagonal causal mask, 7B heads, bf16."""
