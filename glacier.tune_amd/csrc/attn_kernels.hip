@@ -31,10 +31,12 @@
 namespace glacier {
 
 // ---------------------------------------------------------------------------
-// rope_k: one thread per (token, kv head, 8 rotation pairs).  Writes the
-// rotated K to k_rot (caller dtype) and/or kc (compute dtype), and, when vc
-// is given, a compute-dtype copy of V.  pos_of == nullptr: one sequence, the
-// token index is the position (no table load before the cos/sin loads).
+// rope_k: grid (tokens * 8-pair chunks / 256, kv heads), one thread per
+// (token, kv head, 8 rotation pairs); no division by a runtime value before
+// the loads.  Writes the rotated K to k_rot (caller dtype) and/or kc
+// (compute dtype), and, when vc is given, a compute-dtype copy of V.
+// pos_of == nullptr: one sequence, the token index is the position (no table
+// load before the cos/sin loads).
 // ---------------------------------------------------------------------------
 template <typename IO, typename T, int D>
 __global__ __launch_bounds__(kThreads) void rope_k_kernel(
@@ -44,13 +46,11 @@ __global__ __launch_bounds__(kThreads) void rope_k_kernel(
     const float* __restrict__ cos_t, const float* __restrict__ sin_t) {
   constexpr int H = D / 2;
   constexpr int CH = H / 8;  // 8-pair chunks per head
-  const long idx = (long)blockIdx.x * kThreads + threadIdx.x;
-  if (idx >= (long)total_tokens * n_heads_kv * CH) return;
-  const int p0 = 8 * (int)(idx % CH);
-  const long th = idx / CH;  // token * Hkv + head
-  const long tok = th / n_heads_kv;
-  const long base = th * D + p0;
-  const long ti = (pos_of != nullptr ? (long)pos_of[tok] : tok) * H + p0;
+  const int idx = blockIdx.x * kThreads + threadIdx.x;
+  if (idx >= total_tokens * CH) return;
+  const int tok = idx / CH, p0 = 8 * (idx % CH);
+  const long base = ((long)tok * n_heads_kv + blockIdx.y) * D + p0;
+  const long ti = (long)(pos_of != nullptr ? pos_of[tok] : tok) * H + p0;
   float x0[8], x1[8], c[8], s[8], y0[8], y1[8];
   load8(k + base, x0);
   load8(k + base + H, x1);
@@ -917,17 +917,18 @@ __global__ __launch_bounds__(kRedThreads) void attn_bwd_reduce_kernel(
   constexpr int ROWS = kRedThreads / CH;
   GL_STAMP(kKernReduce, 0);
   if ((int)threadIdx.x >= ROWS * CH) return;  // CH need not divide the workgroup
-  const long row = (long)blockIdx.x * ROWS + threadIdx.x / CH;  // token * Hkv + kv head
-  if (row >= (long)total_tokens * n_heads_kv) return;
+  // grid (tokens / ROWS, kv heads): no division by a runtime value
+  const int tok = blockIdx.x * ROWS + threadIdx.x / CH;
+  if (tok >= total_tokens) return;
   const int p0 = 4 * (threadIdx.x % CH);
-  const long tok = row / n_heads_kv;
-  const int j = (int)(row % n_heads_kv);
+  const int j = blockIdx.y;  // kv head
+  const long row = (long)tok * n_heads_kv + j;
   const int n_heads_q = ratio * n_heads_kv;
   const long pos = pos_of != nullptr ? pos_of[tok] : tok;
   const f32x4 cs = *reinterpret_cast<const f32x4*>(cos_t + pos * H + p0);
   const f32x4 sn = *reinterpret_cast<const f32x4*>(sin_t + pos * H + p0);
-  const IO* wkr = wk + (tok * n_heads_q + (long)j * ratio) * D + p0;
-  const IO* wvr = wv + (tok * n_heads_q + (long)j * ratio) * D + p0;
+  const IO* wkr = wk + ((long)tok * n_heads_q + (long)j * ratio) * D + p0;
+  const IO* wvr = wv + ((long)tok * n_heads_q + (long)j * ratio) * D + p0;
   f32x4 k0 = {0.0f, 0.0f, 0.0f, 0.0f}, k1 = k0, v0 = k0, v1 = k0;
   constexpr int RMAX = 8;
   if (ratio <= RMAX) {
@@ -1002,11 +1003,11 @@ hipError_t forward_impl(const FwdLaunch& a, hipStream_t st, KernelTimer* tm) {
   const dim3 blk(kThreads);
   T* kc = static_cast<T*>(a.kc);
   {
-    const long n = (long)a.total_tokens * a.n_heads_kv * (D / 16);
-    const unsigned grid = static_cast<unsigned>((n + kThreads - 1) / kThreads);
+    const long n = (long)a.total_tokens * (D / 16);
+    const dim3 grid(static_cast<unsigned>((n + kThreads - 1) / kThreads), a.n_heads_kv);
     IO* k_rot = static_cast<IO*>(a.k_rot);
     LaunchTiming t(tm, kKernRopeK);
-    GL_LAUNCH(t, (rope_k_kernel<IO, T, D>), dim3(grid), blk, 0, st,
+    GL_LAUNCH(t, (rope_k_kernel<IO, T, D>), grid, blk, 0, st,
                           static_cast<const IO*>(a.k), k_rot,
                           (static_cast<void*>(kc) == static_cast<void*>(k_rot)) ? nullptr : kc,
                           static_cast<const IO*>(a.v), static_cast<T*>(a.vc),
@@ -1062,10 +1063,10 @@ hipError_t backward_impl(const BwdLaunch& a, hipStream_t st, KernelTimer* tm) {
   }
   {
     constexpr int rows_per_wg = kRedThreads / (D / 8);
-    const long rows = (long)a.total_tokens * a.n_heads_kv;
-    const unsigned grid = static_cast<unsigned>((rows + rows_per_wg - 1) / rows_per_wg);
+    const dim3 grid(static_cast<unsigned>((a.total_tokens + rows_per_wg - 1) / rows_per_wg),
+                    a.n_heads_kv);
     LaunchTiming t(tm, kKernReduce);
-    GL_LAUNCH(t, (attn_bwd_reduce_kernel<IO, T, D>), dim3(grid), dim3(kRedThreads), 0, st,
+    GL_LAUNCH(t, (attn_bwd_reduce_kernel<IO, T, D>), grid, dim3(kRedThreads), 0, st,
                           static_cast<const IO*>(a.wk),
                           static_cast<const IO*>(a.wv), static_cast<IO*>(a.dk),
                           static_cast<IO*>(a.dv), a.single_seq ? nullptr : a.pos_of, a.total_tokens,
