@@ -229,9 +229,11 @@ __device__ inline bf16x8 join(bf16x4 lo, bf16x4 hi) {
 }
 
 // ---------------------------------------------------------------------------
-// bwd_stats: one 16-lane (D=128) or 8-lane (D=64) group per (token, head)
-// row; each lane multiplies 8 elements of dO and O in order, the group adds
-// the partials in a fixed order.
+// bwd_stats: grid (tokens / rows per workgroup, query heads), one 16-lane
+// (D=128) or 8-lane (D=64) group per (token, head) row; each lane multiplies
+// 8 elements of dO and O in order, the group adds the partials in a fixed
+// order.  The row's lse is loaded with its dO and O (no division by a
+// runtime value before any load).
 // ---------------------------------------------------------------------------
 template <int D>
 __global__ __launch_bounds__(256) void bwd_stats_kernel(const bf16* __restrict__ d_out,
@@ -239,11 +241,15 @@ __global__ __launch_bounds__(256) void bwd_stats_kernel(const bf16* __restrict__
                                                         const float* __restrict__ lse,
                                                         float2* __restrict__ stats,
                                                         int total_tokens, int n_heads_q) {
-  constexpr int LPR = D / 8;  // lanes per row
-  const long row = ((long)blockIdx.x * 256 + threadIdx.x) / LPR;  // token * Hq + head
+  constexpr int LPR = D / 8;      // lanes per row
+  constexpr int RPW = 256 / LPR;  // rows (tokens) per workgroup
+  const int tok = blockIdx.x * RPW + threadIdx.x / LPR;
+  const int h = blockIdx.y;
   const int part = threadIdx.x % LPR;
-  const long rows = (long)total_tokens * n_heads_q;
-  const long rr = row < rows ? row : rows - 1;  // every lane of a row group stays active
+  const int tt = tok < total_tokens ? tok : total_tokens - 1;  // every lane of a row group stays active
+  const long rr = (long)tt * n_heads_q + h;
+  const long si = (long)h * total_tokens + tt;
+  const float l = lse[si];
   float xd[8], xo[8];
   load8(d_out + rr * D + 8 * part, xd);
   load8(out + rr * D + 8 * part, xo);
@@ -251,12 +257,7 @@ __global__ __launch_bounds__(256) void bwd_stats_kernel(const bf16* __restrict__
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc += xd[e] * xo[e];
   const float drow = lanes_sum<LPR>(acc);
-  if (row < rows && part == 0) {
-    const long tok = row / n_heads_q;
-    const int h = static_cast<int>(row % n_heads_q);
-    const long si = (long)h * total_tokens + tok;
-    stats[si] = make_float2(-lse[si] * kLog2e, drow);
-  }
+  if (tok < total_tokens && part == 0) stats[si] = make_float2(-l * kLog2e, drow);
 }
 
 // ---------------------------------------------------------------------------
@@ -823,10 +824,10 @@ hipError_t launch_bwd2(const BwdLaunch& a, hipStream_t st, KernelTimer* tm) {
   float2* stats = static_cast<float2*>(a.stats);
   {
     constexpr int rows_per_wg = 256 / (D / 8);
-    const long rows = (long)a.total_tokens * a.n_heads_q;
-    const unsigned grid = static_cast<unsigned>((rows + rows_per_wg - 1) / rows_per_wg);
+    const dim3 grid(static_cast<unsigned>((a.total_tokens + rows_per_wg - 1) / rows_per_wg),
+                    a.n_heads_q);
     LaunchTiming t(tm, kKernBwdStats);
-    GL_LAUNCH(t, (bwd_stats_kernel<D>), dim3(grid), dim3(256), 0, st,
+    GL_LAUNCH(t, (bwd_stats_kernel<D>), grid, dim3(256), 0, st,
               static_cast<const bf16*>(a.d_out), static_cast<const bf16*>(a.out), a.lse, stats,
               a.total_tokens, a.n_heads_q);
     GL_CHECK(hipGetLastError());
