@@ -143,7 +143,7 @@ struct FwdLaunch {
 // 32-row kernel's extra row-stats launch and larger per-workgroup fixed
 // costs only pay off on long sequences.
 enum BwdVariant : int { kBwdAuto = 0, kBwdRows16 = 1, kBwdRows32 = 2 };
-constexpr long long kBwdRows32MinPairsD128 = 1024LL * 1025 / 2;  // one S=1024 sequence
+constexpr long long kBwdRows32MinPairsD128 = 1664LL * 1665 / 2;  // one S=1664 sequence
 constexpr long long kBwdRows32MinPairsD64 = 2048LL * 2049 / 2;   // one S=2048 sequence
 
 struct BwdLaunch {
