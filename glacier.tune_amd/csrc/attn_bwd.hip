@@ -808,7 +808,7 @@ __global__ __launch_bounds__(kB2Threads) void attn_bwd2_kernel(
   const int ratio = gridDim.x, n_heads_kv = gridDim.y, n_heads_q = ratio * n_heads_kv;
   const int kvh = blockIdx.y, h = kvh * ratio + blockIdx.x;
   const TileDesc td = tiles_bwd[blockIdx.z];
-  if (td.kind == 0)
+  if (td.kind == kTileDkDv)
     b2_dkdv<D>(td, q_rot, d_out, k_rot, v, stats, wk, wv, total_tokens, n_heads_q, n_heads_kv, h,
                kvh, scale_log2, scale, smem_raw);
   else

@@ -678,6 +678,8 @@ __device__ inline void bwd_dkdv_tile(
   unsigned char* const gsm = smem_raw + grp * 2 * BUF;
 
   const int ntq = (td.len + kTile - 1) / kTile;
+  // the query tiles this entry visits: all from the diagonal one, or one half
+  const QueryRange qr = dkdv_query_range(td.tile, ntq, td.kind);
   const long qstride = (long)n_heads_q * D;
   const IO* qb = q_rot + ((long)td.tok0 * n_heads_q + h) * D;
   const IO* dob = d_out + ((long)td.tok0 * n_heads_q + h) * D;
@@ -726,8 +728,8 @@ __device__ inline void bwd_dkdv_tile(
     kst.load(k_rot + krow0, kvstride, td.len - kTile * td.tile, tid);
     vst.load(v + krow0, kvstride, td.len - kTile * td.tile, tid);
   }
-  const int first = td.tile + grp;
-  if (first < ntq) load_tile(first);
+  const int first = qr.first + grp;
+  if (first < qr.end) load_tile(first);
   GL_STAMP(kKernBwd, 1);
   T* const kvs = reinterpret_cast<T*>(smem_raw + BUF);
   kst.store(kvs, tid);
@@ -775,7 +777,7 @@ __device__ inline void bwd_dkdv_tile(
     acc_rows<T, D>(acc_dk, qs, ds, 4, lane);
   };
 
-  if (first < ntq) store_tile(0, first);
+  if (first < qr.end) store_tile(0, first);
   wait_vmem_all();
   __syncthreads();
 #pragma unroll
@@ -786,18 +788,18 @@ __device__ inline void bwd_dkdv_tile(
   __syncthreads();  // the staging area is free again
   GL_STAMP(kKernBwd, 2);
 
-  const int nit = (ntq - td.tile + G - 1) / G;  // iterations of group 0 (the most)
+  const int nit = (qr.end - qr.first + G - 1) / G;  // iterations of group 0 (the most)
   auto iteration = [&](int it, auto diag) {
     const int qt = first + G * it;
     const unsigned char* base = gsm + (it & 1) * BUF;
-    const bool more = qt + G < ntq;
+    const bool more = qt + G < qr.end;
     // The next tile's loads: for bf16 tensors between this tile's dV and dK
     // products (issued first, they stall the wave while the memory pipeline
-    // is full; more implies qt < ntq, so the step runs whenever they are
+    // is full; more implies qt < qr.end, so the step runs whenever they are
     // due), for fp32 tensors up front (the registers fp32 tile loads hold
     // across the step would not fit beside its products).
     if (sizeof(IO) == 4 && more) load_tile(qt + G);
-    if (qt < ntq) step(base, diag, [&] {
+    if (qt < qr.end) step(base, diag, [&] {
       if (sizeof(IO) != 4 && more) load_tile(qt + G);
     });
     if (it < 6) GL_STAMP(kKernBwd, 3 + 3 * it);
@@ -806,11 +808,12 @@ __device__ inline void bwd_dkdv_tile(
     __syncthreads();
     if (it < 6) GL_STAMP(kKernBwd, 5 + 3 * it);
   };
-  // The diagonal query tile is group 0's first iteration; peeling it keeps a
-  // single step variant inside the loop (two variants in one loop body make
-  // the register allocator copy the accumulators every iteration).
+  // The diagonal query tile (when this entry visits it) is group 0's first
+  // iteration; peeling it keeps a single step variant inside the loop (two
+  // variants in one loop body make the register allocator copy the
+  // accumulators every iteration).
   int it0 = 0;
-  if (grp == 0 && nit > 0) {
+  if (grp == 0 && nit > 0 && qr.first == td.tile) {
     iteration(0, std::true_type{});
     it0 = 1;
   }
@@ -878,22 +881,26 @@ __device__ inline void bwd_dkdv_tile(
   GL_STAMP(kKernBwd, 22);
 }
 
-// z indexes tiles_bwd, the dK/dV and dQ tiles in launch order.  The
+// z indexes tiles_bwd, the dK/dV (whole or half) and dQ tiles in launch order.  The
 // table is read through the scalar cache (one uniform load per workgroup).
 template <typename IO, typename T, int D>
 __global__ __launch_bounds__((kThreads * bwd_groups<T, D>())) void attn_bwd_kernel(
     const IO* __restrict__ q_rot, const IO* __restrict__ d_out, const IO* __restrict__ out,
     const IO* __restrict__ k_rot, const IO* __restrict__ v, const float* __restrict__ lse,
-    IO* __restrict__ dq, IO* __restrict__ wk, IO* __restrict__ wv,
-    const TileDesc* __restrict__ tiles_bwd, int total_tokens, float scale_log2, float scale,
-    const float* __restrict__ cos_t, const float* __restrict__ sin_t) {
+    IO* __restrict__ dq, IO* __restrict__ wk, IO* __restrict__ wv, IO* __restrict__ wk2,
+    IO* __restrict__ wv2, const TileDesc* __restrict__ tiles_bwd, int total_tokens,
+    float scale_log2, float scale, const float* __restrict__ cos_t,
+    const float* __restrict__ sin_t) {
   const TileDesc td = tiles_bwd[blockIdx.z];
-  if (td.kind == 0)
-    bwd_dkdv_tile<IO, T, D>(td, q_rot, d_out, out, k_rot, v, lse, wk, wv, total_tokens,
-                            scale_log2, scale);
-  else
+  if (td.kind == kTileDq) {
     bwd_dq_tile<IO, T, D>(td, q_rot, d_out, out, k_rot, v, lse, dq, total_tokens, scale_log2,
                           scale, cos_t, sin_t);
+  } else {
+    // the second half of a split tile writes the second partials
+    const bool second = td.kind == kTileDkDvSecondHalf;
+    bwd_dkdv_tile<IO, T, D>(td, q_rot, d_out, out, k_rot, v, lse, second ? wk2 : wk,
+                            second ? wv2 : wv, total_tokens, scale_log2, scale);
+  }
 }
 
 // Threads of a reduction workgroup; each finishes 4 rotation pairs of one
@@ -907,10 +914,13 @@ __device__ inline f32x4 load_partial4(const bf16* p) {
   return f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
 }
 
-template <typename IO, typename T, int D>
+// SPLIT: the call split dK/dV tiles (bf16 partials), so rows below
+// split_rows have second partials.
+template <typename IO, typename T, int D, bool SPLIT>
 __global__ __launch_bounds__(kRedThreads) void attn_bwd_reduce_kernel(
     const IO* __restrict__ wk, const IO* __restrict__ wv, IO* __restrict__ dk,
-    IO* __restrict__ dv, const int32_t* __restrict__ pos_of, int total_tokens, int ratio,
+    IO* __restrict__ dv, const IO* __restrict__ wk2, const IO* __restrict__ wv2,
+    int split_rows, const int32_t* __restrict__ pos_of, int total_tokens, int ratio,
     int n_heads_kv, const float* __restrict__ cos_t, const float* __restrict__ sin_t) {
   constexpr int H = D / 2;
   constexpr int CH = H / 4;  // 4-pair chunks per row
@@ -929,13 +939,20 @@ __global__ __launch_bounds__(kRedThreads) void attn_bwd_reduce_kernel(
   const f32x4 sn = *reinterpret_cast<const f32x4*>(sin_t + pos * H + p0);
   const IO* wkr = wk + ((long)tok * n_heads_q + (long)j * ratio) * D + p0;
   const IO* wvr = wv + ((long)tok * n_heads_q + (long)j * ratio) * D + p0;
+  // A row of a split dK/dV tile (bf16 partials only) has a second partial
+  // per head, added right after the head's first.
+  const bool two = SPLIT && pos < split_rows;
+  const IO* wkr2 = wk2 + ((long)tok * n_heads_q + (long)j * ratio) * D + p0;
+  const IO* wvr2 = wv2 + ((long)tok * n_heads_q + (long)j * ratio) * D + p0;
   f32x4 k0 = {0.0f, 0.0f, 0.0f, 0.0f}, k1 = k0, v0 = k0, v1 = k0;
   constexpr int RMAX = 8;
+  constexpr int RMAX2 = SPLIT ? RMAX : 1;
   if (ratio <= RMAX) {
     // Every head's partial in flight at once (a load per head that the sum
     // waits on would cost one memory round trip per head), then the sum in
     // ascending head order; heads past the group add nothing.
     f32x4 pk0[RMAX], pk1[RMAX], pv0[RMAX], pv1[RMAX];
+    f32x4 qk0[RMAX2], qk1[RMAX2], qv0[RMAX2], qv1[RMAX2];
 #pragma unroll
     for (int hh = 0; hh < RMAX; ++hh) {
       const long o = (long)(hh < ratio ? hh : 0) * D;
@@ -944,6 +961,18 @@ __global__ __launch_bounds__(kRedThreads) void attn_bwd_reduce_kernel(
       pv0[hh] = load_partial4(wvr + o);
       pv1[hh] = load_partial4(wvr + o + H);
     }
+    if constexpr (RMAX2 == RMAX) {
+      if (two) {
+#pragma unroll
+        for (int hh = 0; hh < RMAX; ++hh) {
+          const long o = (long)(hh < ratio ? hh : 0) * D;
+          qk0[hh] = load_partial4(wkr2 + o);
+          qk1[hh] = load_partial4(wkr2 + o + H);
+          qv0[hh] = load_partial4(wvr2 + o);
+          qv1[hh] = load_partial4(wvr2 + o + H);
+        }
+      }
+    }
 #pragma unroll
     for (int hh = 0; hh < RMAX; ++hh) {
       if (hh < ratio) {
@@ -951,6 +980,14 @@ __global__ __launch_bounds__(kRedThreads) void attn_bwd_reduce_kernel(
         k1 += pk1[hh];
         v0 += pv0[hh];
         v1 += pv1[hh];
+        if constexpr (RMAX2 == RMAX) {
+          if (two) {
+            k0 += qk0[hh];
+            k1 += qk1[hh];
+            v0 += qv0[hh];
+            v1 += qv1[hh];
+          }
+        }
       }
     }
   } else {
@@ -959,6 +996,12 @@ __global__ __launch_bounds__(kRedThreads) void attn_bwd_reduce_kernel(
       k1 += load_partial4(wkr + (long)hh * D + H);
       v0 += load_partial4(wvr + (long)hh * D);
       v1 += load_partial4(wvr + (long)hh * D + H);
+      if (two) {
+        k0 += load_partial4(wkr2 + (long)hh * D);
+        k1 += load_partial4(wkr2 + (long)hh * D + H);
+        v0 += load_partial4(wvr2 + (long)hh * D);
+        v1 += load_partial4(wvr2 + (long)hh * D + H);
+      }
     }
   }
   f32x4 y0, y1;
@@ -1047,17 +1090,24 @@ hipError_t backward_impl(const BwdLaunch& a, hipStream_t st, KernelTimer* tm) {
     // bf16 tensors, long sequences: the 32-row-wave kernel fed by LDS DMA
     // (attn_bwd.hip; head_dim 64 and 128)
     if constexpr (D == 64 || D == 128) GL_CHECK(launch_bwd2<D>(a, st, tm));
-  } else {
+  }
+  // dK/dV tiles split in query halves: 16-row kernel, bf16 partials
+  const bool split = !rows32 && sizeof(IO) == 2 && a.split > 0;
+  if (!rows32) {
     auto fn = attn_bwd_kernel<IO, T, D>;
     constexpr size_t lds = bwd_lds<T, D>();
     GL_CHECK(allow_lds(fn, lds));
     LaunchTiming t(tm, kKernBwd);
-    GL_LAUNCH(t, fn, dim3(ratio, a.n_heads_kv, 2 * a.n_tiles),
+    GL_LAUNCH(t, fn, dim3(ratio, a.n_heads_kv, split ? a.n_split_entries : 2 * a.n_tiles),
                           dim3(kThreads * bwd_groups<T, D>()), lds, st,
                           static_cast<const IO*>(a.q_rot), static_cast<const IO*>(a.d_out),
                           static_cast<const IO*>(a.out), static_cast<const IO*>(a.k_rot),
                           static_cast<const IO*>(a.v), a.lse, static_cast<IO*>(a.dq),
-                          static_cast<IO*>(a.wk), static_cast<IO*>(a.wv), a.tiles_bwd, a.total_tokens, a.scale_log2, a.scale, a.cos_t, a.sin_t);
+                          static_cast<IO*>(a.wk), static_cast<IO*>(a.wv),
+                          static_cast<IO*>(split ? a.wk2 : nullptr),
+                          static_cast<IO*>(split ? a.wv2 : nullptr),
+                          split ? a.tiles_split : a.tiles_bwd, a.total_tokens, a.scale_log2,
+                          a.scale, a.cos_t, a.sin_t);
     GL_CHECK(hipGetLastError());
     t.launched();
   }
@@ -1066,11 +1116,17 @@ hipError_t backward_impl(const BwdLaunch& a, hipStream_t st, KernelTimer* tm) {
     const dim3 grid(static_cast<unsigned>((a.total_tokens + rows_per_wg - 1) / rows_per_wg),
                     a.n_heads_kv);
     LaunchTiming t(tm, kKernReduce);
-    GL_LAUNCH(t, (attn_bwd_reduce_kernel<IO, T, D>), grid, dim3(kRedThreads), 0, st,
+    auto fn = attn_bwd_reduce_kernel<IO, T, D, false>;
+    if constexpr (sizeof(IO) == 2) {
+      if (split) fn = attn_bwd_reduce_kernel<IO, T, D, true>;
+    }
+    GL_LAUNCH(t, fn, grid, dim3(kRedThreads), 0, st,
                           static_cast<const IO*>(a.wk),
                           static_cast<const IO*>(a.wv), static_cast<IO*>(a.dk),
-                          static_cast<IO*>(a.dv), a.single_seq ? nullptr : a.pos_of, a.total_tokens,
-                          ratio, a.n_heads_kv, a.cos_t, a.sin_t);
+                          static_cast<IO*>(a.dv), static_cast<const IO*>(split ? a.wk2 : nullptr),
+                          static_cast<const IO*>(split ? a.wv2 : nullptr),
+                          split ? kTile * a.split : 0, a.single_seq ? nullptr : a.pos_of,
+                          a.total_tokens, ratio, a.n_heads_kv, a.cos_t, a.sin_t);
     GL_CHECK(hipGetLastError());
     t.launched();
   }

@@ -5,6 +5,7 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <algorithm>
 #include <type_traits>
 #include <utility>
 #include <vector>
@@ -23,8 +24,21 @@ struct TileDesc {
   int32_t tok0;   // first token of the sequence in the [T][H][D] tensors
   int32_t len;    // tokens in the sequence
   int32_t tile;   // tile index inside the sequence (rows 64*tile ..)
-  int32_t kind;   // backward table: 0 = dK/dV tile, 1 = dQ tile (unused elsewhere)
+  int32_t kind;   // backward table: a TileKind (unused elsewhere)
 };
+
+// Backward tile kinds.  A split dK/dV tile runs as two workgroups, each over
+// half of the tile's query tiles (the first half holds the diagonal one); the
+// second half writes its own partials, which the head reduction adds.
+enum TileKind : int {
+  kTileDkDv = 0,
+  kTileDq = 1,
+  kTileDkDvFirstHalf = 2,
+  kTileDkDvSecondHalf = 3,
+};
+// dK/dV tiles 0 .. split - 1 of each sequence may be split (16-row backward,
+// bf16 tensors, only while the launch still fits one workgroup per CU).
+constexpr int kBwdMaxSplit = 3;
 
 constexpr int kPrecFp32 = 0;
 constexpr int kPrecBf16 = 1;
@@ -161,9 +175,46 @@ struct BwdLaunch {
   void *wk, *wv;                 // per-query-head dK/dV partials [T][Hq][D], tensors' dtype
   void* stats;                   // bf16 tensors: [Hq][T] float2 (-lse log2 e, dO . O)
   const TileDesc* tiles_bwd;     // [2 n_tiles] dK/dV and dQ tiles, longest expected first
+  // Split dK/dV tiles (16-row backward only; split == 0: none): the table
+  // with dK/dV tiles 0 .. split - 1 of every sequence in halves, its length,
+  // and the second halves' partials [T][Hq][D] (rows of split tiles only).
+  int split;
+  int n_split_entries;
+  const TileDesc* tiles_split;
+  void *wk2, *wv2;
   const int32_t* pos_of;
   const float *cos_t, *sin_t;
 };
+
+// How many dK/dV tiles per sequence the backward splits (see TileKind): the
+// largest split <= kBwdMaxSplit for which Hq workgroups per table entry still
+// fit n_cu, for bf16 tensors; 0 for fp32 tensors.  tiles_of(b) gives the
+// tile count of sequence b of n_seqs.
+template <typename F>
+int bwd_split_of(bool io_bf16, int n_heads_q, int n_seqs, int n_cu, F tiles_of) {
+  if (!io_bf16) return 0;
+  long long base = 0;
+  for (int b = 0; b < n_seqs; ++b) base += 2LL * tiles_of(b);
+  int best = 0;
+  for (int s = 1; s <= kBwdMaxSplit; ++s) {
+    long long entries = base;
+    for (int b = 0; b < n_seqs; ++b) entries += std::min(s, tiles_of(b));
+    if ((long long)n_heads_q * entries <= n_cu) best = s;
+  }
+  return best;
+}
+
+// Queries of a dK/dV tile entry: query tiles [first, end) of a sequence with
+// ntq tiles.
+struct QueryRange {
+  int first, end;
+};
+__host__ __device__ inline QueryRange dkdv_query_range(int tile, int ntq, int kind) {
+  const int mid = tile + (ntq - tile + 1) / 2;
+  if (kind == kTileDkDvFirstHalf) return QueryRange{tile, mid};
+  if (kind == kTileDkDvSecondHalf) return QueryRange{mid, ntq};
+  return QueryRange{tile, ntq};
+}
 
 hipError_t launch_forward(const FwdLaunch& a, hipStream_t st, KernelTimer* tm);
 hipError_t launch_backward(const BwdLaunch& a, hipStream_t st, KernelTimer* tm);

@@ -127,7 +127,24 @@ inline float rope_freq(int i, int head_dim, float base) {
 // tile visits, with constants fitted to measured workgroup durations (D = 128,
 // units of 0.1 us); it only orders the launch.
 inline int bwd_tile_cost(int n_tiles_in_seq, int tile, int kind) {
-  return kind == 0 ? 63 + 16 * (n_tiles_in_seq - tile) : 53 + 12 * (tile + 1);
+  if (kind == kTileDq) return 53 + 12 * (tile + 1);
+  const QueryRange r = dkdv_query_range(tile, n_tiles_in_seq, kind);
+  return 63 + 16 * (r.end - r.first);
+}
+
+// The backward entries of one sequence of nt tiles in natural order (tile by
+// tile, dK/dV before dQ); the dK/dV tiles below `split` come as two halves.
+template <typename F>
+void bwd_entries(int nt, int split, F emit) {
+  for (int t = 0; t < nt; ++t) {
+    if (t < split) {
+      emit(t, static_cast<int>(kTileDkDvFirstHalf));
+      emit(t, static_cast<int>(kTileDkDvSecondHalf));
+    } else {
+      emit(t, static_cast<int>(kTileDkDv));
+    }
+    emit(t, static_cast<int>(kTileDq));
+  }
 }
 
 // ---- allocation-free backward: its buffers inside the fixed scratch -------
@@ -135,6 +152,7 @@ constexpr int kNoAllocMaxSeqs = 1024;
 constexpr int kNoAllocMaxTokens = GLACIER_ATTN_MAX_SEQ_LEN;
 constexpr int kNoAllocMaxTiles = kNoAllocMaxTokens / kTile + kNoAllocMaxSeqs;
 constexpr int kNoAllocMaxCost = 63 + 16 * (kNoAllocMaxTokens / kTile);
+constexpr int kNoAllocMaxSplitEntries = 4096;  // a split table fits the CUs: far fewer
 constexpr int kNoAllocRopeChunk = 16384;  // floats staged per table upload
 
 // What one device's scratch holds across calls: the RoPE tables and the tile
@@ -143,13 +161,13 @@ struct NoAllocResident {
   int rope_cap = 0, rope_dim = 0;
   float rope_base = 0.0f;
   size_t tiles_off = 0;  // 0: no tile table resident
-  int n_seqs = 0, total_tokens = 0;
+  int n_seqs = 0, total_tokens = 0, split = 0;
   int32_t cu[kNoAllocMaxSeqs + 1] = {};
 };
 
 std::mutex g_noalloc_mutex;  // guards the records and host staging below
 NoAllocResident g_noalloc[kNoAllocMaxDevices];
-TileDesc g_noalloc_tiles[2 * kNoAllocMaxTiles];
+TileDesc g_noalloc_tiles[2 * kNoAllocMaxTiles + kNoAllocMaxSplitEntries];
 int32_t g_noalloc_pos[kNoAllocMaxTokens];
 int32_t g_noalloc_count[kNoAllocMaxCost + 2];
 float g_noalloc_freq[512];  // head_dim / 2 (head_dim <= 1024, make_shape_args)
@@ -160,6 +178,9 @@ size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 struct NoAllocBwd {
   void *wk, *wv, *stats;
   const TileDesc* tiles_bwd;
+  int split, n_split_entries;  // split dK/dV tiles (split > 0): their table and partials
+  const TileDesc* tiles_split;
+  void *wk2, *wv2;
   const int32_t* pos_of;
   const float *cos_t, *sin_t;
   int n_tiles;
@@ -167,13 +188,17 @@ struct NoAllocBwd {
 };
 
 // Lays out one backward call inside the scratch at `base` on `device`:
-//   [cos table][sin table][dK/dV + dQ tile table][positions][row stats][dK partials][dV partials]
-// (each region 256-byte aligned).  The RoPE tables and the tile/position
+//   [cos table][sin table][dK/dV + dQ tile table, then the split table][positions][row stats]
+//   [dK partials][dV partials][second-half dK partials][second-half dV partials]
+// (each region 256-byte aligned; the split regions only when the call splits
+// dK/dV tiles, by the rule of the allocating backward: bwd_split_of with the
+// device's n_cu, unless split_ok is false).  The RoPE tables and the tile/position
 // tables are uploaded only when the call's head_dim, theta, longest sequence
 // or sequence layout differ from what the scratch holds; the upload first
 // waits for the whole device, since any earlier call may still read them.
 // Every other region is written by the call's own kernels before it is read.
-NoAllocBwd noalloc_bwd_workspace(int device, void* base, const ShapeArgs& s) {
+NoAllocBwd noalloc_bwd_workspace(int device, void* base, const ShapeArgs& s, int n_cu,
+                                 bool split_ok) {
   if (s.n_seqs > kNoAllocMaxSeqs)
     fail(GLACIER_ATTN_ERR_UNSUPPORTED, "the allocation-free backward takes at most " +
                                            std::to_string(kNoAllocMaxSeqs) + " sequences per call");
@@ -189,6 +214,14 @@ NoAllocBwd noalloc_bwd_workspace(int device, void* base, const ShapeArgs& s) {
     n_tiles += (len + kTile - 1) / kTile;
     pairs += static_cast<long long>(len) * (len + 1) / 2;
   }
+  auto tiles_of = [&](int b) { return (s.seq_start(b + 1) - s.seq_start(b) + kTile - 1) / kTile; };
+  int split = split_ok ? bwd_split_of(s.io_bf16, s.n_heads_q, s.n_seqs, n_cu, tiles_of) : 0;
+  int n_split_entries = 0;
+  if (split > 0) {
+    n_split_entries = 2 * n_tiles;
+    for (int b = 0; b < s.n_seqs; ++b) n_split_entries += std::min(split, tiles_of(b));
+    if (n_split_entries > kNoAllocMaxSplitEntries) split = n_split_entries = 0;
+  }
   std::lock_guard<std::mutex> g(g_noalloc_mutex);
   NoAllocResident& r = g_noalloc[device];
   const bool rope_ok = r.rope_cap >= s.max_len && r.rope_dim == s.head_dim &&
@@ -196,19 +229,21 @@ NoAllocBwd noalloc_bwd_workspace(int device, void* base, const ShapeArgs& s) {
   const int rope_cap = rope_ok ? r.rope_cap : (std::max(s.max_len, 1) + 255) / 256 * 256;
   const size_t rope_bytes = align256(static_cast<size_t>(rope_cap) * half * sizeof(float));
   const size_t off_tiles = 2 * rope_bytes;
-  const size_t off_pos = off_tiles + align256(2 * static_cast<size_t>(n_tiles) * sizeof(TileDesc));
+  const size_t n_entries = 2 * static_cast<size_t>(n_tiles) + n_split_entries;
+  const size_t off_pos = off_tiles + align256(n_entries * sizeof(TileDesc));
   const size_t off_stats = off_pos + align256(T * sizeof(int32_t));
   const size_t stats_bytes = s.io_bf16 ? align256((T * Hq + 64) * 2 * sizeof(float)) : 0;
   const size_t part = align256(T * Hq * D * (s.io_bf16 ? 2 : 4));
   const size_t off_wk = off_stats + stats_bytes, off_wv = off_wk + part;
-  const size_t need = off_wv + part;
+  const size_t off_wk2 = off_wv + part, off_wv2 = off_wk2 + (split > 0 ? part : 0);
+  const size_t need = off_wv2 + (split > 0 ? part : 0);
   if (need > kNoAllocScratchBytes)
     fail(GLACIER_ATTN_ERR_UNSUPPORTED,
          "the allocation-free backward needs " + std::to_string(need) +
              " bytes of scratch for this call; its fixed scratch holds " +
              std::to_string(kNoAllocScratchBytes) + " (GLACIER_ATTN_NOALLOC_SCRATCH_BYTES)");
   bool tiles_ok = r.tiles_off == off_tiles && r.n_seqs == s.n_seqs &&
-                  r.total_tokens == s.total_tokens;
+                  r.total_tokens == s.total_tokens && r.split == split;
   for (int b = 0; tiles_ok && b <= s.n_seqs; ++b) tiles_ok = r.cu[b] == s.seq_start(b);
   char* const sb = static_cast<char*>(base);
   if (!rope_ok || !tiles_ok) {
@@ -261,13 +296,36 @@ NoAllocBwd noalloc_bwd_workspace(int device, void* base, const ShapeArgs& s) {
                 TileDesc{tok0, len, t, kind};
         for (int i = 0; i < len; ++i) g_noalloc_pos[tok0 + i] = i;
       }
-      check_hip(hipMemcpy(sb + off_tiles, g_noalloc_tiles, 2 * static_cast<size_t>(n_tiles) * sizeof(TileDesc),
+      if (split > 0) {
+        // the split table: the same stable counting sort over the entries
+        // with dK/dV tiles 0 .. split - 1 in halves
+        TileDesc* const out = g_noalloc_tiles + 2 * n_tiles;
+        std::fill(g_noalloc_count, g_noalloc_count + kNoAllocMaxCost + 2, 0);
+        for (int b = 0; b < s.n_seqs; ++b) {
+          const int nt = tiles_of(b);
+          bwd_entries(nt, split, [&](int t, int kind) { ++g_noalloc_count[bwd_tile_cost(nt, t, kind)]; });
+        }
+        int at = 0;
+        for (int c = kNoAllocMaxCost; c >= 0; --c) {
+          const int n = g_noalloc_count[c];
+          g_noalloc_count[c] = at;
+          at += n;
+        }
+        for (int b = 0; b < s.n_seqs; ++b) {
+          const int tok0 = s.seq_start(b), len = s.seq_start(b + 1) - tok0, nt = tiles_of(b);
+          bwd_entries(nt, split, [&](int t, int kind) {
+            out[g_noalloc_count[bwd_tile_cost(nt, t, kind)]++] = TileDesc{tok0, len, t, kind};
+          });
+        }
+      }
+      check_hip(hipMemcpy(sb + off_tiles, g_noalloc_tiles, n_entries * sizeof(TileDesc),
                           hipMemcpyHostToDevice),
                 "allocation-free backward: tile table upload");
       check_hip(hipMemcpy(sb + off_pos, g_noalloc_pos, T * sizeof(int32_t), hipMemcpyHostToDevice),
                 "allocation-free backward: position table upload");
       r.n_seqs = s.n_seqs;
       r.total_tokens = s.total_tokens;
+      r.split = split;
       for (int b = 0; b <= s.n_seqs; ++b) r.cu[b] = s.seq_start(b);
       r.tiles_off = off_tiles;
     }
@@ -280,6 +338,11 @@ NoAllocBwd noalloc_bwd_workspace(int device, void* base, const ShapeArgs& s) {
   w.stats = s.io_bf16 ? sb + off_stats : nullptr;
   w.wk = sb + off_wk;
   w.wv = sb + off_wv;
+  w.split = split;
+  w.n_split_entries = n_split_entries;
+  w.tiles_split = split > 0 ? w.tiles_bwd + 2 * n_tiles : nullptr;
+  w.wk2 = split > 0 ? sb + off_wk2 : nullptr;
+  w.wv2 = split > 0 ? sb + off_wv2 : nullptr;
   w.n_tiles = n_tiles;
   w.pairs = pairs;
   return w;
@@ -289,7 +352,12 @@ NoAllocBwd noalloc_bwd_workspace(int device, void* base, const ShapeArgs& s) {
 struct TileSet {
   int n_tiles = 0, max_len = 0;
   long long pairs = 0;  // causal (query, key) pairs per head
-  DeviceBuffer tiles;  // [3 n_tiles] TileDesc: fwd order, then the backward order
+  // [3 n_tiles] TileDesc: fwd order, then the backward order; then, for
+  // layouts small enough to split, the backward tables with split 1, 2, ...
+  DeviceBuffer tiles;
+  int split_at[kBwdMaxSplit + 1] = {};       // entry offset of each split table (0: none)
+  int split_entries[kBwdMaxSplit + 1] = {};  // and its length
+  std::vector<int> seq_tiles;                // tiles of each sequence
   DeviceBuffer pos;    // [T] int32
 };
 
@@ -306,6 +374,8 @@ class GpuAttentionEngine {
            "device ordinal " + std::to_string(device_ordinal) + " out of range (" +
                std::to_string(n) + " devices)");
     check_hip(hipSetDevice(device_), "hipSetDevice");
+    check_hip(hipDeviceGetAttribute(&n_cu_, hipDeviceAttributeMultiprocessorCount, device_),
+              "hipDeviceGetAttribute");
     check_hip(hipStreamCreateWithFlags(&own_stream_, hipStreamNonBlocking), "hipStreamCreate");
     // the allocation-free backward's scratch address on this device; a
     // failure here only disables that entry point (it retries and reports)
@@ -319,6 +389,15 @@ class GpuAttentionEngine {
       else if (m != "auto" && !m.empty())
         fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT,
              "GLACIER_ATTN_BWD must be auto, rows16 or rows32, not " + m);
+    }
+    // GLACIER_ATTN_BWD_SPLIT=0 keeps every dK/dV tile whole (comparisons and
+    // A/B runs); unset or "auto" splits the longest ones when the CUs allow.
+    if (const char* v = std::getenv("GLACIER_ATTN_BWD_SPLIT")) {
+      const std::string m(v);
+      if (m == "0") split_ok_ = false;
+      else if (m != "auto" && !m.empty())
+        fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT,
+             "GLACIER_ATTN_BWD_SPLIT must be auto or 0, not " + m);
     }
   }
 
@@ -434,6 +513,18 @@ class GpuAttentionEngine {
     if (s.io_bf16) a.stats = stats_.ensure((T * Hq + 64) * 2 * sizeof(float), "row stats");
     const TileDesc* t = static_cast<const TileDesc*>(ts.tiles.ptr);
     a.tiles_bwd = t + ts.n_tiles;
+    // the longest dK/dV tiles in query halves while the launch fits the CUs
+    const int split =
+        split_ok_ ? bwd_split_of(s.io_bf16, s.n_heads_q, static_cast<int>(ts.seq_tiles.size()),
+                                 n_cu_, [&](int b) { return ts.seq_tiles[b]; })
+                  : 0;
+    if (split > 0 && ts.split_entries[split] > 0) {
+      a.split = split;
+      a.n_split_entries = ts.split_entries[split];
+      a.tiles_split = t + ts.split_at[split];
+      a.wk2 = wk2_.ensure(T * Hq * D * wsz, "second-half dK partials");
+      a.wv2 = wv2_.ensure(T * Hq * D * wsz, "second-half dV partials");
+    }
     a.pos_of = static_cast<const int32_t*>(ts.pos.ptr);
     a.cos_t = static_cast<const float*>(rope_cos_.ptr);
     a.sin_t = static_cast<const float*>(rope_sin_.ptr);
@@ -459,7 +550,7 @@ class GpuAttentionEngine {
       }
       base = noalloc_scratch(device_);
     }
-    NoAllocBwd w = noalloc_bwd_workspace(device_, base, s);
+    NoAllocBwd w = noalloc_bwd_workspace(device_, base, s, n_cu_, split_ok_);
     BwdLaunch a = bwd_launch_of(BwdCall{s.total_tokens, s.n_heads_q, s.n_heads_kv, s.head_dim,
                                         s.precision, s.io_bf16, s.n_seqs == 1, w.n_tiles,
                                         w.pairs});
@@ -469,6 +560,11 @@ class GpuAttentionEngine {
     a.wv = w.wv;
     a.stats = w.stats;
     a.tiles_bwd = w.tiles_bwd;
+    a.split = w.split;
+    a.n_split_entries = w.n_split_entries;
+    a.tiles_split = w.tiles_split;
+    a.wk2 = w.wk2;
+    a.wv2 = w.wv2;
     a.pos_of = w.pos_of;
     a.cos_t = w.cos_t;
     a.sin_t = w.sin_t;
@@ -684,20 +780,36 @@ class GpuAttentionEngine {
       return remaining(x) > remaining(y);
     });
     // Backward: dK/dV and dQ tiles share one launch, longest expected first
-    // (bwd_tile_cost).
-    std::vector<std::pair<int, TileDesc>> bw;
-    for (const TileDesc& t : nat) {
-      const int nt = (t.len + kTile - 1) / kTile;
-      for (int kind = 0; kind < 2; ++kind)
-        bw.push_back({bwd_tile_cost(nt, t.tile, kind), TileDesc{t.tok0, t.len, t.tile, kind}});
-    }
-    std::stable_sort(bw.begin(), bw.end(),
-                     [](const std::pair<int, TileDesc>& x, const std::pair<int, TileDesc>& y) {
-                       return x.first > y.first;
-                     });
+    // (bwd_tile_cost); the split tables likewise, with dK/dV tiles 0 ..
+    // split - 1 of every sequence in query halves.
+    auto backward_table = [&](int split, std::vector<TileDesc>& all) {
+      std::vector<std::pair<int, TileDesc>> bw;
+      for (int b = 0; b < n; ++b) {
+        const int tok0 = s.cu[b], len = s.cu[b + 1] - s.cu[b];
+        if (len <= 0) continue;
+        const int nt = (len + kTile - 1) / kTile;
+        bwd_entries(nt, split, [&](int t, int kind) {
+          bw.push_back({bwd_tile_cost(nt, t, kind), TileDesc{tok0, len, t, kind}});
+        });
+      }
+      std::stable_sort(bw.begin(), bw.end(),
+                       [](const std::pair<int, TileDesc>& x, const std::pair<int, TileDesc>& y) {
+                         return x.first > y.first;
+                       });
+      for (const auto& e : bw) all.push_back(e.second);
+      return static_cast<int>(bw.size());
+    };
+    for (int b = 0; b < n; ++b) ts->seq_tiles.push_back((std::max(s.cu[b + 1] - s.cu[b], 0) + kTile - 1) / kTile);
     std::vector<TileDesc> all;
     all.insert(all.end(), fwd.begin(), fwd.end());
-    for (const auto& e : bw) all.push_back(e.second);
+    backward_table(0, all);
+    // only a layout of fewer backward entries than CUs can ever be split
+    if (2 * static_cast<long long>(ts->n_tiles) < n_cu_) {
+      for (int split = 1; split <= kBwdMaxSplit; ++split) {
+        ts->split_at[split] = static_cast<int>(all.size());
+        ts->split_entries[split] = backward_table(split, all);
+      }
+    }
     ts->tiles.ensure(all.size() * sizeof(TileDesc), "tile table");
     ts->pos.ensure(pos.size() * sizeof(int32_t), "position table");
     check_hip(hipStreamSynchronize(stream()), "tile table");
@@ -742,8 +854,10 @@ class GpuAttentionEngine {
   int rope_len_ = 0, rope_dim_ = 0;
   float rope_base_ = 0.0f;
   // device-path scratch
-  DeviceBuffer kc_, vc_, wk_, wv_, stats_;
+  DeviceBuffer kc_, vc_, wk_, wv_, wk2_, wv2_, stats_;
   int bwd_variant_ = kBwdAuto;
+  int n_cu_ = 0;          // compute units of the device
+  bool split_ok_ = true;  // dK/dV tiles may be split (GLACIER_ATTN_BWD_SPLIT)
   // projection scratch and the hipBLASLt handle (created on first use)
   DeviceBuffer yf_, dxf_, lowrank_, part_;
   DeviceBuffer rstd_, dyw_;  // RMSNorm backward row scales, dy copy (weight gradient)

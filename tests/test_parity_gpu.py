@@ -187,6 +187,48 @@ def test_bf16_device_ragged_shapes_each_backward_kernel(bf16_kernels, S, Hq, Hkv
     assert all(e <= BF16_GATE for e in err.values()), err
 
 
+@pytest.mark.parametrize("case", ["qwen05b_s512", "short_packed"])
+def test_split_dkdv_tiles_match_whole_tiles(engines, case):
+    """When the 16-row backward's grid leaves CUs idle (bf16 tensors, e.g. 14
+    query heads at S=512) its longest dK/dV tiles run as two query halves
+    whose partials the head reduction adds.  Against an engine with
+    GLACIER_ATTN_BWD_SPLIT=0 (every tile whole): dq bit-identical (dQ tiles
+    do not change), dk and dv within the bf16 gate of each other, both runs
+    within the gate of the oracle.  The packed case has sequences of one tile
+    or less, whose second halves visit no query tile and write zeros."""
+    if case == "qwen05b_s512":
+        S, Hq, Hkv, D, base = CONFIGS["qwen05b_s512"]
+        (q, k, v, dO), ref = oracle_case(S, Hq, Hkv, D, base, 1, True)
+        cu = None
+    else:
+        Hq, Hkv, D, base = 4, 2, 128, 1.0e4
+        cu = np.array([0, 30, 94, 95, 195], np.int32)
+        q, k, v, dO = make_inputs(int(cu[-1]), Hq, Hkv, D, 6, True)
+        ref = oracle.layer_fwd_bwd_varlen(q, k, v, dO, cu, base)
+    _say(f"[split dK/dV] {case}")
+    old = os.environ.get("GLACIER_ATTN_BWD_SPLIT")
+    os.environ["GLACIER_ATTN_BWD_SPLIT"] = "0"
+    try:
+        whole = ga.GpuAttentionEngine(0, ga.PREC_BF16)
+    finally:
+        if old is None:
+            os.environ.pop("GLACIER_ATTN_BWD_SPLIT", None)
+        else:
+            os.environ["GLACIER_ATTN_BWD_SPLIT"] = old
+    try:
+        got_w = run_device(whole, q, k, v, dO, base, torch.bfloat16, cu=cu)
+    finally:
+        whole.close()
+    got_s = run_device(engines[ga.PREC_BF16], q, k, v, dO, base, torch.bfloat16, cu=cu)
+    err_s, err_w = errors(got_s, ref), errors(got_w, ref)
+    _say(f"  split {err_s}\n  whole {err_w}")
+    assert all(e <= BF16_GATE for e in err_s.values()), err_s
+    assert all(e <= BF16_GATE for e in err_w.values()), err_w
+    assert np.array_equal(got_s["dq"], got_w["dq"])
+    for key in ("dk", "dv"):
+        assert oracle.max_rel_err(got_s[key], got_w[key]) <= BF16_GATE, key
+
+
 @pytest.mark.parametrize("kernel", BWD_KERNELS)
 def test_bf16_device_backward_is_bitwise_repeatable(bf16_kernels, kernel):
     S, Hq, Hkv, D, base = 300, 14, 2, 128, 1.0e6
