@@ -37,7 +37,7 @@ enum TileKind : int {
   kTileDkDvSecondHalf = 3,
 };
 // dK/dV tiles 0 .. split - 1 of each sequence may be split (16-row backward,
-// bf16 tensors, only while the launch still fits one workgroup per CU).
+// bf16 tensors, only while the launch about fits one workgroup per CU).
 constexpr int kBwdMaxSplit = 3;
 
 constexpr int kPrecFp32 = 0;
@@ -187,9 +187,11 @@ struct BwdLaunch {
 };
 
 // How many dK/dV tiles per sequence the backward splits (see TileKind): the
-// largest split <= kBwdMaxSplit for which Hq workgroups per table entry still
-// fit n_cu, for bf16 tensors; 0 for fp32 tensors.  tiles_of(b) gives the
-// tile count of sequence b of n_seqs.
+// largest split <= kBwdMaxSplit for which Hq workgroups per table entry
+// still fit n_cu with an eighth to spare (a few more workgroups than CUs
+// still shorten the span: the short tiles fill in behind), for bf16 tensors;
+// 0 for fp32 tensors.  tiles_of(b) gives the tile count of sequence b of
+// n_seqs.
 template <typename F>
 int bwd_split_of(bool io_bf16, int n_heads_q, int n_seqs, int n_cu, F tiles_of) {
   if (!io_bf16) return 0;
@@ -199,7 +201,7 @@ int bwd_split_of(bool io_bf16, int n_heads_q, int n_seqs, int n_cu, F tiles_of) 
   for (int s = 1; s <= kBwdMaxSplit; ++s) {
     long long entries = base;
     for (int b = 0; b < n_seqs; ++b) entries += std::min(s, tiles_of(b));
-    if ((long long)n_heads_q * entries <= n_cu) best = s;
+    if ((long long)n_heads_q * entries <= n_cu + n_cu / 8) best = s;
   }
   return best;
 }

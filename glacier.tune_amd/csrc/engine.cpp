@@ -803,8 +803,9 @@ class GpuAttentionEngine {
     std::vector<TileDesc> all;
     all.insert(all.end(), fwd.begin(), fwd.end());
     backward_table(0, all);
-    // only a layout of fewer backward entries than CUs can ever be split
-    if (2 * static_cast<long long>(ts->n_tiles) < n_cu_) {
+    // only a layout of fewer backward entries than CUs (and an eighth) can
+    // ever be split
+    if (2 * static_cast<long long>(ts->n_tiles) < n_cu_ + n_cu_ / 8) {
       for (int split = 1; split <= kBwdMaxSplit; ++split) {
         ts->split_at[split] = static_cast<int>(all.size());
         ts->split_entries[split] = backward_table(split, all);
