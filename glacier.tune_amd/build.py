@@ -34,6 +34,7 @@ SOURCES = {
     "attn_kernels.hip": ("-Wno-pass-failed",),
     "attn_fwd.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form"),
     "attn_bwd.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form"),
+    "attn_bwd3.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form"),
     "attn_noalloc.hip": (),
     "blas_lt.cpp": (),
     "proj_lora.hip": (),

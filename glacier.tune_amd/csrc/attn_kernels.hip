@@ -1081,12 +1081,18 @@ hipError_t forward_impl(const FwdLaunch& a, hipStream_t st, KernelTimer* tm) {
 template <typename IO, typename T, int D>
 hipError_t backward_impl(const BwdLaunch& a, hipStream_t st, KernelTimer* tm) {
   const int ratio = a.n_heads_q / a.n_heads_kv;
-  bool rows32 = false;
+  bool rows32 = false, mfma32 = false;
   if constexpr (std::is_same<IO, bf16>::value && (D == 64 || D == 128)) {
     const long long min_pairs = D == 128 ? kBwdRows32MinPairsD128 : kBwdRows32MinPairsD64;
-    rows32 = a.variant == kBwdRows32 || (a.variant == kBwdAuto && a.pairs >= min_pairs);
+    mfma32 = a.variant == kBwdMfma32 && a.tiles_wide != nullptr;
+    rows32 = !mfma32 &&
+             (a.variant == kBwdRows32 || (a.variant == kBwdAuto && a.pairs >= min_pairs));
   }
-  if (rows32) {
+  if (mfma32) {
+    // bf16 tensors: the 32x32x16-MFMA kernel (attn_bwd3.hip)
+    if constexpr (D == 64 || D == 128) GL_CHECK(launch_bwd3<D>(a, st, tm));
+    rows32 = true;  // no split tiles, whole-tile reduction
+  } else if (rows32) {
     // bf16 tensors, long sequences: the 32-row-wave kernel fed by LDS DMA
     // (attn_bwd.hip; head_dim 64 and 128)
     if constexpr (D == 64 || D == 128) GL_CHECK(launch_bwd2<D>(a, st, tm));

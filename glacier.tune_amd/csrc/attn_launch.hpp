@@ -13,6 +13,7 @@
 namespace glacier {
 
 constexpr int kTile = 64;      // queries or keys per workgroup tile
+constexpr int kWideTile = 128; // rows per tile of the 32x32x16-MFMA backward
 constexpr int kWaves = 4;      // waves per workgroup, 16 rows each
 constexpr int kThreads = 256;  // kWaves * 64
 constexpr float kLog2e = 1.4426950408889634f;
@@ -156,7 +157,7 @@ struct FwdLaunch {
 // break-even below, the 16-row-wave kernel (attn_kernels.hip) under it: the
 // 32-row kernel's extra row-stats launch and larger per-workgroup fixed
 // costs only pay off on long sequences.
-enum BwdVariant : int { kBwdAuto = 0, kBwdRows16 = 1, kBwdRows32 = 2 };
+enum BwdVariant : int { kBwdAuto = 0, kBwdRows16 = 1, kBwdRows32 = 2, kBwdMfma32 = 3 };
 constexpr long long kBwdRows32MinPairsD128 = 1664LL * 1665 / 2;  // one S=1664 sequence
 constexpr long long kBwdRows32MinPairsD64 = 2048LL * 2049 / 2;   // one S=2048 sequence
 
@@ -182,6 +183,10 @@ struct BwdLaunch {
   int n_split_entries;
   const TileDesc* tiles_split;
   void *wk2, *wv2;
+  // The 128-row tile table of the 32x32x16-MFMA backward (null: not built;
+  // that kernel is then not used) and its length.
+  const TileDesc* tiles_wide;
+  int n_wide_entries;
   const int32_t* pos_of;
   const float *cos_t, *sin_t;
 };
@@ -232,6 +237,12 @@ hipError_t launch_fwd_bf16(const FwdLaunch& a, hipStream_t st, KernelTimer* tm);
 // dK/dV + dQ kernel, writing dq and the per-head dK/dV partials; D: 64 or 128.
 template <int D>
 hipError_t launch_bwd2(const BwdLaunch& a, hipStream_t st, KernelTimer* tm);
+
+// The bf16-tensor backward on 32x32x16 MFMAs (attn_bwd3.hip): its row-stats
+// kernel and the dK/dV + dQ kernel, writing dq and the per-head dK/dV
+// partials; D: 64 or 128.
+template <int D>
+hipError_t launch_bwd3(const BwdLaunch& a, hipStream_t st, KernelTimer* tm);
 
 // Kernels whose dynamic LDS exceeds 64 KB must say so before their launch.
 template <typename F>

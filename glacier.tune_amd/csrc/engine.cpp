@@ -132,6 +132,18 @@ inline int bwd_tile_cost(int n_tiles_in_seq, int tile, int kind) {
   return 63 + 16 * (r.end - r.first);
 }
 
+// Expected cost of a 128-row backward tile (attn_bwd3.hip) of a sequence of
+// len tokens: its step count (one per 32-row chunk it visits, plus one),
+// weighted by the step time of its kind, plus a fixed part; it only orders
+// the launch.
+inline int bwd_wide_cost(int len, int tile, int kind) {
+  if (kind == kTileDq) {
+    const int keys = std::min(len, kWideTile * (tile + 1));
+    return 50 + 18 * (((keys + 31) / 32 + 1) / 2 + 1);
+  }
+  return 50 + 12 * ((len - kWideTile * tile + 31) / 32 + 1);
+}
+
 // The backward entries of one sequence of nt tiles in natural order (tile by
 // tile, dK/dV before dQ); the dK/dV tiles below `split` come as two halves.
 template <typename F>
@@ -357,6 +369,7 @@ struct TileSet {
   DeviceBuffer tiles;
   int split_at[kBwdMaxSplit + 1] = {};       // entry offset of each split table (0: none)
   int split_entries[kBwdMaxSplit + 1] = {};  // and its length
+  int wide_at = 0, wide_entries = 0;         // the 128-row backward table (attn_bwd3.hip)
   std::vector<int> seq_tiles;                // tiles of each sequence
   DeviceBuffer pos;    // [T] int32
 };
@@ -380,15 +393,17 @@ class GpuAttentionEngine {
     // the allocation-free backward's scratch address on this device; a
     // failure here only disables that entry point (it retries and reports)
     if (noalloc_scratch_init(device_) != hipSuccess) (void)hipGetLastError();
-    // GLACIER_ATTN_BWD=rows16|rows32 pins the bf16 backward kernel (tests
-    // cover both on every shape); unset or "auto" picks by sequence length.
+    // GLACIER_ATTN_BWD=rows16|rows32|mfma32 pins the bf16 backward kernel
+    // (tests cover each on every shape); unset or "auto" picks by sequence
+    // length.
     if (const char* v = std::getenv("GLACIER_ATTN_BWD")) {
       const std::string m(v);
       if (m == "rows16") bwd_variant_ = kBwdRows16;
       else if (m == "rows32") bwd_variant_ = kBwdRows32;
+      else if (m == "mfma32") bwd_variant_ = kBwdMfma32;
       else if (m != "auto" && !m.empty())
         fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT,
-             "GLACIER_ATTN_BWD must be auto, rows16 or rows32, not " + m);
+             "GLACIER_ATTN_BWD must be auto, rows16, rows32 or mfma32, not " + m);
     }
     // GLACIER_ATTN_BWD_SPLIT=0 keeps every dK/dV tile whole (comparisons and
     // A/B runs); unset or "auto" splits the longest ones when the CUs allow.
@@ -513,6 +528,8 @@ class GpuAttentionEngine {
     if (s.io_bf16) a.stats = stats_.ensure((T * Hq + 64) * 2 * sizeof(float), "row stats");
     const TileDesc* t = static_cast<const TileDesc*>(ts.tiles.ptr);
     a.tiles_bwd = t + ts.n_tiles;
+    a.tiles_wide = t + ts.wide_at;
+    a.n_wide_entries = ts.wide_entries;
     // the longest dK/dV tiles in query halves while the launch fits the CUs
     const int split =
         split_ok_ ? bwd_split_of(s.io_bf16, s.n_heads_q, static_cast<int>(ts.seq_tiles.size()),
@@ -810,6 +827,26 @@ class GpuAttentionEngine {
         ts->split_at[split] = static_cast<int>(all.size());
         ts->split_entries[split] = backward_table(split, all);
       }
+    }
+    // the 128-row backward table: dK/dV tiles of 128 keys and dQ tiles of 128
+    // queries, longest expected first (bwd_wide_cost)
+    {
+      std::vector<std::pair<int, TileDesc>> bw;
+      for (int b = 0; b < n; ++b) {
+        const int tok0 = s.cu[b], len = s.cu[b + 1] - s.cu[b];
+        if (len <= 0) continue;
+        const int nt = (len + kWideTile - 1) / kWideTile;
+        for (int t = 0; t < nt; ++t)
+          for (int kind = 0; kind < 2; ++kind)
+            bw.push_back({bwd_wide_cost(len, t, kind), TileDesc{tok0, len, t, kind}});
+      }
+      std::stable_sort(bw.begin(), bw.end(),
+                       [](const std::pair<int, TileDesc>& x, const std::pair<int, TileDesc>& y) {
+                         return x.first > y.first;
+                       });
+      ts->wide_at = static_cast<int>(all.size());
+      ts->wide_entries = static_cast<int>(bw.size());
+      for (const auto& e : bw) all.push_back(e.second);
     }
     ts->tiles.ensure(all.size() * sizeof(TileDesc), "tile table");
     ts->pos.ensure(pos.size() * sizeof(int32_t), "position table");
