@@ -8,8 +8,10 @@ max|gpu - ref| / max|ref| per tensor:
 Configs: BASELINE.json configs[0] (Qwen2.5-0.5B, S=512, 14/2, D=64) and
 configs[1] (Qwen2.5-7B, S=512, 28/4, D=128) against the oracle; configs[2]
 (packed varlen) against the oracle per segment; configs[3] (S=4096) and
-configs[4] (Llama-3-8B B=2 S=2048) against a float32 torch reference on the
-GPU (the oracle would take minutes there), plus edge cases.
+configs[4] (Llama-3-8B B=2 S=2048) against the oracle on the same seeded
+SplitMix inputs in both modes (about 7-15 s of oracle time each on 8-16
+host threads), and again, with other large shapes, against a float32 torch
+reference on the GPU; plus edge cases.
 """
 import functools
 import os
@@ -43,7 +45,7 @@ def engines():
     e16.close()
 
 
-BWD_KERNELS = ("rows16", "rows32")
+BWD_KERNELS = ("rows16", "rows32", "mfma32")
 
 
 @pytest.fixture(scope="module")
@@ -391,6 +393,56 @@ def test_varlen_packed_batch_matches_oracle_per_segment(engines, bf16_kernels):
     got = run_device(engines[ga.PREC_FP32], q, k, v, dO, base, torch.float32, cu=cu)
     err = errors(got, ref)
     assert all(e <= FP32_GATE for e in err.values()), err
+
+
+# ---------------------------------------------------------------------------
+# BASELINE configs[3] and [4] against the oracle.
+# ---------------------------------------------------------------------------
+
+LONG_ORACLE = {
+    "qwen7b_s4096": ([4096], 28, 4, 128, 1.0e6),            # configs[3]
+    "llama3_b2_s2048": ([2048, 2048], 32, 8, 128, 5.0e5),   # configs[4]
+}
+
+
+@functools.lru_cache(maxsize=2)
+def long_oracle_case(name, bf16):
+    lens, Hq, Hkv, D, base = LONG_ORACLE[name]
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    q, k, v, dO = make_inputs(int(cu[-1]), Hq, Hkv, D, 5, bf16)
+    return (q, k, v, dO), cu, oracle.layer_fwd_bwd_varlen(q, k, v, dO, cu, base)
+
+
+@pytest.mark.parametrize("name", list(LONG_ORACLE))
+def test_long_configs_fp32_mode_match_oracle(engines, name):
+    """fp32 tensors, fp32 math: 1e-4 on O, lse, dQ, dK, dV; the post-RoPE q
+    and k bit-exact."""
+    lens, Hq, Hkv, D, base = LONG_ORACLE[name]
+    _say(f"[long oracle fp32] {name}")
+    (q, k, v, dO), cu, ref = long_oracle_case(name, False)
+    got = run_device(engines[ga.PREC_FP32], q, k, v, dO, base, torch.float32,
+                     cu=None if len(lens) == 1 else cu)
+    err = errors(got, ref)
+    _say(f"  errors {err}")
+    assert all(e <= FP32_GATE for e in err.values()), err
+    assert np.array_equal(got["q_rot"], ref["q_rot"])
+    assert np.array_equal(got["k_rot"], ref["k_rot"])
+
+
+@pytest.mark.parametrize("kernel", ("auto",) + BWD_KERNELS)
+@pytest.mark.parametrize("name", list(LONG_ORACLE))
+def test_long_configs_bf16_mode_match_oracle(engines, bf16_kernels, name, kernel):
+    """bf16 tensors (inputs rounded to bf16 for the oracle too), bf16 MFMA
+    math, through the automatic backward choice and each pinned one: 2e-2
+    on O, lse, dQ, dK, dV."""
+    lens, Hq, Hkv, D, base = LONG_ORACLE[name]
+    _say(f"[long oracle bf16, {kernel} backward] {name}")
+    (q, k, v, dO), cu, ref = long_oracle_case(name, True)
+    eng = engines[ga.PREC_BF16] if kernel == "auto" else bf16_kernels[kernel]
+    got = run_device(eng, q, k, v, dO, base, torch.bfloat16, cu=None if len(lens) == 1 else cu)
+    err = errors(got, ref)
+    _say(f"  errors {err}")
+    assert all(e <= BF16_GATE for e in err.values()), err
 
 
 # ---------------------------------------------------------------------------
