@@ -2,6 +2,7 @@
 """Benchmark: causal GQA attention forward + backward on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config qwen7b_s512]
+    python bench.py --precision fp32      # the fp32-operand mode (fp32 tensors and MFMAs)
     python bench.py --component proj      # the q/k/v projections with LoRA adapters
     python bench.py --component norm      # the residual add + RMSNorm
 
@@ -19,9 +20,13 @@ roofline = the dominant kernel (largest share of device time), its average
          duration from events that its own launches timestamp (on the stream
          it runs on), against the 2.5 PFLOP/s dense bf16 MFMA peak of MI355X;
          traffic = its HBM bytes per launch measured with rocprofv3 counters
-         (profiles/attn_kernels_qwen7b_s512_pmc.md).
+         (profiles/attn_kernels_<config>[_fp32]_pmc.md).
 cpu_baseline = the C restatement of the reference CPU path (oracle/), fp32,
          on this host's cores, over a bounded sample.
+
+--precision fp32 runs the same step in the fp32-operand mode (fp32 device
+tensors, v_mfma_f32_16x16x4f32 with fp32 accumulation) and prices it against
+the 157.3 TFLOP/s dense fp32 MFMA peak.
 
 --component proj measures the projection step instead (include/glacier_qkv.h):
 one step = glacier_proj_forward + glacier_proj_backward of the q, k and v
@@ -44,7 +49,27 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "glacier.tune_amd"))
 
 PEAK_BF16_TFLOPS = 2500.0
+PEAK_FP32_TFLOPS = 157.3
 METRIC = "causal GQA attn fwd+bwd TFLOP/s + % bf16 MFMA peak, Qwen2.5-7B shape S=512"
+
+# The shape each config is (BASELINE.json's configs index where it is one).
+CONFIG_LABEL = {
+    "qwen7b_s512": ("Qwen2.5-7B shape S=512", "BASELINE.json configs[1]"),
+    "qwen05b_s512": ("Qwen2.5-0.5B shape S=512", "BASELINE.json configs[0]'s shape"),
+    "qwen7b_s4096": ("Qwen2.5-7B shape S=4096", "BASELINE.json configs[3]"),
+    "llama3_b2_s2048": ("Llama-3-8B shape B=2 S=2048", "BASELINE.json configs[4]"),
+    "qwen7b_ckpt28_varlen": ("Qwen2.5-7B 28-layer checkpointed step, 4 packed sequences",
+                             "BASELINE.json configs[2]"),
+}
+
+
+def metric_name(config, precision):
+    """BASELINE.json's metric for its own config and mode; the same form,
+    naming the shape and the peak priced against, for the others."""
+    if config == "qwen7b_s512" and precision == "bf16":
+        return METRIC
+    return (f"causal GQA attn fwd+bwd TFLOP/s + % {precision} MFMA peak, "
+            f"{CONFIG_LABEL[config][0]}")
 
 CONFIGS = {
     # name: (lengths, Hq, Hkv, D, theta, layers).  layers == 1: one attention
@@ -68,16 +93,16 @@ FLOPS_PER_PAIR = {"attn_fwd": 4, "attn_bwd": 8, "rope_k": 0, "attn_bwd_reduce": 
                   "attn_bwd_stats": 0}
 
 
-# HBM bytes per launch of each kernel at qwen7b_s512, from two rocprofv3 --pmc
-# runs (FETCH_SIZE, WRITE_SIZE) scaled by a plain copy of known size; the file
-# gives the commands and the calibration.
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "attn_kernels_qwen7b_s512_pmc.md")
-
-
-def measured_traffic(config, kernel):
-    if config != "qwen7b_s512" or not os.path.exists(TRAFFIC_FILE):
+# HBM bytes per launch of each kernel, per config and mode, from two
+# rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) scaled by a plain copy of
+# known size; profiles/attn_kernels_<config>[_fp32]_pmc.md gives the commands
+# and the calibration.
+def measured_traffic(config, kernel, precision="bf16"):
+    path = os.path.join(ROOT, "profiles", f"attn_kernels_{config}"
+                        f"{'_fp32' if precision == 'fp32' else ''}_pmc.md")
+    if not os.path.exists(path):
         return None
-    for line in open(TRAFFIC_FILE):
+    for line in open(path):
         f = line.split()
         if len(f) == 3 and f[0] == "traffic_bytes" and f[1] == kernel:
             return int(f[2])
@@ -496,6 +521,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="qwen7b_s512", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--precision", default="bf16", choices=["bf16", "fp32"],
+                    help="attention: bf16 tensors on bf16 MFMAs (the headline) or the "
+                         "fp32-operand mode (fp32 tensors and MFMAs)")
     ap.add_argument("--component", default="attention",
                     choices=["attention", "proj", "norm", "host"],
                     help="attention (the headline), the q/k/v projections with LoRA adapters, "
@@ -534,6 +562,9 @@ def main():
     import glacier_attn as ga
 
     lengths, Hq, Hkv, D, theta, layers = CONFIGS[args.config]
+    fp32 = args.precision == "fp32"
+    tdt = torch.float32 if fp32 else torch.bfloat16
+    peak = PEAK_FP32_TFLOPS if fp32 else PEAK_BF16_TFLOPS
     T = sum(lengths)
     cu = None if len(lengths) == 1 else np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
     dev = torch.device("cuda:0")
@@ -543,10 +574,10 @@ def main():
         """One layer's device tensors (each layer has its own activations)."""
 
         def __init__(self):
-            self.q = torch.randn(T, Hq, D, device=dev, generator=g).bfloat16()
-            self.k = torch.randn(T, Hkv, D, device=dev, generator=g).bfloat16()
-            self.v = torch.randn(T, Hkv, D, device=dev, generator=g).bfloat16()
-            self.dO = (0.01 * torch.randn(T, Hq, D, device=dev, generator=g)).bfloat16()
+            self.q = torch.randn(T, Hq, D, device=dev, generator=g).to(tdt)
+            self.k = torch.randn(T, Hkv, D, device=dev, generator=g).to(tdt)
+            self.v = torch.randn(T, Hkv, D, device=dev, generator=g).to(tdt)
+            self.dO = (0.01 * torch.randn(T, Hq, D, device=dev, generator=g)).to(tdt)
             self.out = torch.empty_like(self.q)
             self.lse = torch.empty(Hq, T, device=dev, dtype=torch.float32)
             self.q_rot = torch.empty_like(self.q)
@@ -556,7 +587,7 @@ def main():
             self.dv = torch.empty_like(self.v)
 
     net = [Layer() for _ in range(layers)]
-    eng = ga.GpuAttentionEngine(0, ga.PREC_BF16)
+    eng = ga.GpuAttentionEngine(0, ga.PREC_FP32 if fp32 else ga.PREC_BF16)
 
     # Every call with its arguments checked and converted once
     # (eng.bind_forward / bind_backward / bind_step), so each timed call is
@@ -651,10 +682,10 @@ def main():
         "bound": "mfma",
         "kernel": dom,
         "achieved": round(achieved, 3),
-        "peak": PEAK_BF16_TFLOPS,
+        "peak": peak,
         "unit": "TFLOP/s",
-        "frac": round(achieved / PEAK_BF16_TFLOPS, 5),
-        "traffic": measured_traffic(args.config, dom),
+        "frac": round(achieved / peak, 5),
+        "traffic": measured_traffic(args.config, dom, args.precision),
         "kernel_avg_us": {n: round(avg[n] * 1e3, 3) for n in FLOPS_PER_PAIR},
     }
 
@@ -663,10 +694,10 @@ def main():
         cpu = cpu_baseline(lengths, Hq, Hkv, D, theta)
 
     res = {
-        "metric": METRIC,
+        "metric": metric_name(args.config, args.precision),
         "value": round(tflops, 3),
         "unit": "TFLOP/s",
-        "pct_bf16_peak": round(100.0 * tflops / PEAK_BF16_TFLOPS, 3),
+        f"pct_{args.precision}_peak": round(100.0 * tflops / peak, 3),
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
@@ -674,13 +705,16 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": "f32" if fp32 else "bf16",
         "data": "synthetic (seeded normal q/k/v, dO*0.01; device-resident)",
         "config": {
-            "workload": f"{args.config}: causal GQA attention layer fwd+bwd (BASELINE.json configs[1])"
-            if args.config == "qwen7b_s512" else f"{args.config}: causal GQA attention layer fwd+bwd",
+            "workload": f"{args.config}: {CONFIG_LABEL[args.config][0]}, causal GQA attention "
+                        f"{'layer fwd+bwd' if layers == 1 else 'fwd, recompute fwd, bwd per layer'} "
+                        f"({CONFIG_LABEL[args.config][1]})",
             "seq_lens": lengths, "n_heads_q": Hq, "n_heads_kv": Hkv, "head_dim": D,
-            "rope_theta": theta, "io": "bf16 device tensors, fp32 lse", "parallelism": "1 GPU",
+            "rope_theta": theta, "parallelism": "1 GPU",
+            "io": ("fp32 device tensors, fp32 MFMAs (fp32-operand mode), fp32 lse" if fp32 else
+                   "bf16 device tensors, bf16 MFMAs with fp32 accumulation, fp32 lse"),
             "algorithmic_gflop_per_step": round(flops / 1e9, 4),
         },
         "roofline": roofline,
