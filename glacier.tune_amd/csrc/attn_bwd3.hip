@@ -1,23 +1,28 @@
 // attn_bwd3.hip -- the bf16-tensor attention backward on 32x32x16 MFMAs
-// (gfx950, wave64): GpuLoraEngine.Backward.cs:354-412 (the dq/ds and dk/dv
-// kernels of tune_bwd.cu:598-717) and the inverse rope_batch of :452, on
-// device tensors; the arithmetic of CausalAttentionKernel.cs:79-213.
+// (gfx950, wave64) for long sequences: GpuLoraEngine.Backward.cs:354-412
+// (the dq/ds and dk/dv kernels of tune_bwd.cu:598-717) and the inverse
+// rope_batch of :452, on device tensors; the arithmetic of
+// CausalAttentionKernel.cs:79-213.
 //
 // Two launches before the GQA head reduction (attn_bwd_reduce):
-//   bwd3_stats  per (query head, token) the pair (-lse / scale, -D_i), with
+//   bwd3_stats  per (query head, token) the pair (-lse log2 e, D_i), with
 //               D_i = dO_i . O_i (the softmax-gradient row term), [Hq][T].
-//   attn_bwd3   one workgroup of 8 waves per tile of the tile table (both
-//               kinds, longest expected first):
-//     dK/dV tile  64 keys of one query head.  Waves = 2 key halves x 4 query
-//                 groups; a wave owns 32 keys, whose K rows it keeps in
-//                 registers for the whole tile (the B operand of S = Q K^T);
-//                 V rows sit in LDS.  Group g takes the 32-query chunks
-//                 g, g + 4, ... of the causal range, streamed into LDS by DMA.
-//                 dV^T += dO^T P and dK^T += Q^T dS accumulate in AGPRs.
-//     dQ tile     64 queries of one query head.  Waves = 2 query halves x 4
-//                 key groups; a wave keeps its 32 queries' Q and dO rows in
-//                 registers (B operands of S^T = K Q^T, dP^T = V dO^T) and
-//                 streams 32-key chunks of K and V; dQ^T += K^T dS^T.
+//   attn_bwd3   one workgroup of 8 waves per entry of the 128-row tile table
+//               (both kinds, longest expected first):
+//     dK/dV tile  128 keys of one query head.  Waves = 4 key quarters x 2
+//                 roles, the two waves of a quarter on one SIMD.  The P wave
+//                 keeps its 32 keys' K fragments and dV^T in AGPRs and forms
+//                 S = Q K^T, P (masked) and dV^T += dO^T P; the dS wave keeps
+//                 V and dK^T, forms dP = dO V^T, dS = P (dP - D) and
+//                 dK^T += Q^T dS.  P crosses to the dS wave through LDS.
+//                 32-query chunks of Q, dO and the row stats stream through
+//                 a 4-slot ring by DMA, two chunks ahead.
+//     dQ tile     128 queries of one query head.  Waves = 4 query quarters x
+//                 2 key groups (even and odd 32-key chunks, each group with
+//                 its own 4-slot ring of K and V).  A wave keeps its queries'
+//                 Q and dO fragments and dQ^T in AGPRs, forms S^T and dP^T,
+//                 then dQ^T += K^T dS^T; the groups' sums are added in group
+//                 order on the store, with the scale and the inverse RoPE.
 //
 // Matrix-core layout, v_mfma_f32_32x32x16_bf16 (lane l, c = l % 32,
 // h = l / 32): A[row c][k = 8h .. 8h + 7], B[k = 8h ..][col c], and the
@@ -28,41 +33,32 @@
 // 16 s + 8 + 4 h + 0..3), whose A operand comes from two ds_read_b64_tr_b16
 // reads of the row-major LDS tile (4 consecutive rows of one column each).
 //
-// Row statistics enter as the accumulators' initial values: S starts at
-// -lse / scale, so that P = exp2(S * scale * log2 e); dP starts at -D_i, so
-// that dS = P * dP.  No per-row value is held in registers across a chunk.
-//
 // LDS tiles are [32][D] bf16 rows, unpadded, with 16-byte piece p of row r
-// in slot p ^ sw3(r).  sw3 makes both access patterns conflict-free: a
+// in slot p ^ lds_sw(r), which keeps both access patterns conflict-free: a
 // 16-lane quarter of a fragment read (16 rows, one piece each) and a 32-lane
 // half of a transposing read (4 rows x 4 pieces).
 //
-// Scheduling: the two waves on each SIMD (w and w + 4) work half an
-// iteration out of phase.  Waves 0-3 (groups 0, 1) form S and dP of a chunk
-// in the first half and finish it (exponentials, dV/dK or dQ products) in
-// the second; waves 4-7 finish their previous chunk in the first half and
-// form the next one's S and dP in the second.  One wave's exponentials and
-// LDS reads then run beside its SIMD partner's MFMAs.  Two workgroup barriers
-// per iteration order the DMA refills of each group's two-slot ring.
+// Steps: every wave takes every step with one workgroup barrier.  Step c
+// forms chunk c's first products (a dependent chain) and issues chunk
+// c - 1's last products (independent MFMAs) between the chain's links; the
+// ring slot of every LDS read is an immediate offset (the steady loop is
+// unrolled over the four slots).
 //
 // All sums have a fixed order and no atomics are used: results are bitwise
 // repeatable.
 #include "attn_common.hpp"
 #include "attn_ks.hpp"
 #include "attn_launch.hpp"
+#include "lds_mfma.hpp"
 
 #include <hip/hip_ext.h>
-
-#include <utility>
 
 namespace glacier {
 namespace {
 
-typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kW3 = 8;
 constexpr int kNT3 = kW3 * 64;
-constexpr int kG3 = 4;   // stage groups (2 waves each)
 constexpr int kC3 = 32;  // rows per chunk
 
 template <int D>
@@ -90,102 +86,13 @@ struct L3 {
   static_assert(KV_STATS + 3 * SLOT + CB + 16 * RB < 65536, "ring offsets");
 };
 
-// Slot of piece p of row r: p ^ sw3(r) (16 pieces per row at D = 128, 8 at
-// D = 64, where two rows share one 256-byte line of the 64 banks).
-template <int D>
-__device__ inline int sw3(int r) {
-  if constexpr (D == 128)
-    return ((r & 3) << 2) | ((r >> 2) & 3);
-  else
-    return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
-}
 
-// ---- inline-assembly pieces ---------------------------------------------
-__device__ inline f32x4 lds4(unsigned addr) {
-  f32x4 r;
-  asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(addr));
-  return r;
-}
-template <int OFF>
-__device__ inline bf16x8 rd128(unsigned addr) {
-  bf16x8 r;
-  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
-  return r;
-}
-template <int OFF>
-__device__ inline bf16x4 rdtr(unsigned addr) {
-  bf16x4 r;
-  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
-  return r;
-}
-template <int N>
-__device__ inline void lgkm() {
-  static_assert(N >= 0 && N < 16, "lgkmcnt range");
-  asm volatile("s_waitcnt lgkmcnt(%0)" ::"i"(N) : "memory");
-}
-// lgkm<n> with n known only after unrolling (constant-folded there),
-// saturated at the counter's maximum (a larger count waits for nothing)
-__device__ inline void lgkm_v(int n) {
-  switch (n < 15 ? n : 15) {
-    case 0: lgkm<0>(); break;
-    case 1: lgkm<1>(); break;
-    case 2: lgkm<2>(); break;
-    case 3: lgkm<3>(); break;
-    case 4: lgkm<4>(); break;
-    case 5: lgkm<5>(); break;
-    case 6: lgkm<6>(); break;
-    case 7: lgkm<7>(); break;
-    case 8: lgkm<8>(); break;
-    case 9: lgkm<9>(); break;
-    case 10: lgkm<10>(); break;
-    case 11: lgkm<11>(); break;
-    case 12: lgkm<12>(); break;
-    case 13: lgkm<13>(); break;
-    case 14: lgkm<14>(); break;
-    default: lgkm<15>(); break;
-  }
-}
-template <int N>
-__device__ inline void vmw() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  asm volatile("s_waitcnt vmcnt(%0)" ::"i"(N) : "memory");
-}
-// vmcnt(n) for n known only after the call's arguments are (0 .. 63)
-__device__ inline void vm_wait_v(int n) {
-  switch (n) {
-#define GL_VMW_CASE(N) \
-  case N:              \
-    vmw<N>();          \
-    break;
-    GL_VMW_CASE(0) GL_VMW_CASE(1) GL_VMW_CASE(2) GL_VMW_CASE(3) GL_VMW_CASE(4) GL_VMW_CASE(5)
-    GL_VMW_CASE(6) GL_VMW_CASE(7) GL_VMW_CASE(8) GL_VMW_CASE(9) GL_VMW_CASE(10) GL_VMW_CASE(11)
-    GL_VMW_CASE(12) GL_VMW_CASE(13) GL_VMW_CASE(14) GL_VMW_CASE(15) GL_VMW_CASE(16)
-    GL_VMW_CASE(17) GL_VMW_CASE(18) GL_VMW_CASE(19) GL_VMW_CASE(20) GL_VMW_CASE(21)
-    GL_VMW_CASE(22) GL_VMW_CASE(23) GL_VMW_CASE(24) GL_VMW_CASE(25) GL_VMW_CASE(26)
-    GL_VMW_CASE(27) GL_VMW_CASE(28) GL_VMW_CASE(29) GL_VMW_CASE(30) GL_VMW_CASE(31)
-    GL_VMW_CASE(32) GL_VMW_CASE(33) GL_VMW_CASE(34) GL_VMW_CASE(35) GL_VMW_CASE(36)
-#undef GL_VMW_CASE
-    default: vmw<0>(); break;
-  }
-}
-template <typename T>
-__device__ inline void tie3(T& x) {
-  asm volatile("" : "+v"(x));
-}
-template <typename T>
-__device__ inline T fresh3(T x) {
-  asm volatile("" : "+v"(x));
-  return x;
-}
 
 // x += A B, x in VGPRs (read by VALU code after the chain), B resident in
-// AGPRs.  The compiler sees no MFMA here: the first MFMA of a chain waits the
-// two states a VALU-written x needs (s_nop 1); later ones accumulate into
-// the same registers back to back, which needs none; xdl_to_valu() must
+// AGPRs.  The compiler sees no MFMA here; a chain's first product is
+// mma32_zero (no accumulator input), later ones accumulate into the same
+// registers back to back, which needs no wait states; xdl_to_valu() must
 // separate the chain's last MFMA from any VALU read of x.
-__device__ inline void mma32_first(f32x16& x, const bf16x8& a, const bf16x8& b) {
-  asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(x) : "v"(a), "a"(b));
-}
 __device__ inline void mma32(f32x16& x, const bf16x8& a, const bf16x8& b) {
   asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(x) : "v"(a), "a"(b));
 }
@@ -235,43 +142,12 @@ __device__ inline void write_accs(unsigned base, const f32x16 (&acc)[N]) {
       lds_w4(base + 1024u * (4 * db + q), f32x4{y[4 * q], y[4 * q + 1], y[4 * q + 2], y[4 * q + 3]});
   }
 }
-__device__ inline bf16x8 join8(bf16x4 lo, bf16x4 hi) {
-  bf16x8 r;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    r[i] = lo[i];
-    r[4 + i] = hi[i];
-  }
-  return r;
-}
-
-// f(integral_constant<int, i>) for i = 0 .. N - 1, in order
-template <int N, typename F, int... I>
-__device__ inline void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
-  (f(std::integral_constant<int, I>{}), ...);
-}
-template <int N, typename F>
-__device__ inline void static_for(F&& f) {
-  static_for_impl<N>(f, std::make_integer_sequence<int, N>{});
-}
-
-// A buffer resource over [base, base + bytes) with base made wave-uniform.
-#if defined(__HIP_DEVICE_COMPILE__)
-__device__ inline __amdgpu_buffer_rsrc_t rsrc3(const void* base, int bytes) {
-  const unsigned long long a = reinterpret_cast<unsigned long long>(base);
-  const unsigned long long au =
-      (static_cast<unsigned long long>(__builtin_amdgcn_readfirstlane(static_cast<int>(a >> 32))) << 32) |
-      static_cast<unsigned>(__builtin_amdgcn_readfirstlane(static_cast<int>(a & 0xffffffffu)));
-  return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(au), (short)0,
-                                           __builtin_amdgcn_readfirstlane(bytes), kBufferWord3);
-}
-#endif
 
 // ---- DMA into swizzled [32][D] tiles --------------------------------------
 // Instruction n of a 32-row chunk fills LDS bytes 1024 n .. of the tile;
 // lane l writes the 16 bytes at 16 l, i.e. slot l % PPR of row
-// n RPI + l / PPR, and loads the global piece slot ^ sw3(row) of that row.
-// sw3 depends on the row only modulo 16 = RPI P, so the per-lane part of
+// n RPI + l / PPR, and loads the global piece slot ^ lds_sw(row) of that row.
+// lds_sw depends on the row only modulo 16 = RPI P, so the per-lane part of
 // the offset repeats every P instructions: it is computed once per tile
 // (off[]), and the row block n RPI goes into the scalar offset.
 template <int D>
@@ -288,7 +164,7 @@ __device__ inline Dma3<D> dma3_setup(int rowb, int lane) {
   d.rowb = rowb;
   const int rl = lane / M::PPR, slot = lane % M::PPR;
 #pragma unroll
-  for (int j = 0; j < M::P; ++j) d.off[j] = rl * rowb + 16 * (slot ^ sw3<D>(j * M::RPI + rl));
+  for (int j = 0; j < M::P; ++j) d.off[j] = rl * rowb + 16 * (slot ^ lds_sw<D>(j * M::RPI + rl));
   d.stat = 8 * (lane & 31) + 4 * (lane >> 5);
   return d;
 }
@@ -303,21 +179,21 @@ __device__ inline void dma3(const Dma3<D>& d, const bf16* src, int nvalid, unsig
 #if defined(__HIP_DEVICE_COMPILE__)
   using M = Dma3<D>;
   if (nvalid >= kC3) {
-    const __amdgpu_buffer_rsrc_t rs = rsrc3(src, kC3 * d.rowb);
+    const __amdgpu_buffer_rsrc_t rs = wave_rsrc(src, kC3 * d.rowb);
 #pragma unroll
     for (int n = 0; n < M::NI; ++n)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (GLACIER_LDS void*)(dst + 1024 * n), 16,
                                                d.off[n % M::P], n * M::RPI * d.rowb, 0, 0);
   } else {
     const int nv = nvalid < 0 ? 0 : nvalid;
-    const __amdgpu_buffer_rsrc_t rs = rsrc3(src, nv * d.rowb);
-    const int ln = fresh3(lane);
+    const __amdgpu_buffer_rsrc_t rs = wave_rsrc(src, nv * d.rowb);
+    const int ln = fresh_v(lane);
     const int rl = ln / M::PPR, slot = ln % M::PPR;
 #pragma unroll
     for (int n = 0; n < M::NI; ++n) {
       const int r = n * M::RPI + rl;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (GLACIER_LDS void*)(dst + 1024 * n), 16,
-                                               r * d.rowb + 16 * (slot ^ sw3<D>(r)), 0, 0, 0);
+                                               r * d.rowb + 16 * (slot ^ lds_sw<D>(r)), 0, 0, 0);
     }
   }
 #endif
@@ -331,7 +207,7 @@ __device__ inline void dma_stats3(const Dma3<D>& d, const float2* src, int nvali
                                   unsigned char* dst) {
 #if defined(__HIP_DEVICE_COMPILE__)
   const int nv = nvalid < 0 ? 0 : nvalid < kC3 ? nvalid : kC3;
-  const __amdgpu_buffer_rsrc_t rs = rsrc3(src, nv * 8);
+  const __amdgpu_buffer_rsrc_t rs = wave_rsrc(src, nv * 8);
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (GLACIER_LDS void*)dst, 4, d.stat, 0, 0, 0);
 #endif
 }
@@ -344,7 +220,7 @@ __device__ inline void load_rows3(const bf16* src, int rowb, int nvalid, bf16x8 
                                   int lane) {
 #if defined(__HIP_DEVICE_COMPILE__)
   const int nv = nvalid < 0 ? 0 : nvalid < kC3 ? nvalid : kC3;
-  const __amdgpu_buffer_rsrc_t rs = rsrc3(src, nv * rowb);
+  const __amdgpu_buffer_rsrc_t rs = wave_rsrc(src, nv * rowb);
   const int off = (lane & 31) * rowb + 16 * (lane >> 5);
 #pragma unroll
   for (int kk = 0; kk < D / 16; ++kk)
@@ -357,7 +233,7 @@ __device__ inline void load_rows3(const bf16* src, int rowb, int nvalid, bf16x8 
 template <int D>
 __device__ inline unsigned frag3(int lane) {
   const int r = lane & 31, h = lane >> 5;
-  return static_cast<unsigned>(r * 2 * D + 16 * (h ^ sw3<D>(r)));
+  return static_cast<unsigned>(r * 2 * D + 16 * (h ^ lds_sw<D>(r)));
 }
 // Byte offset of this lane's transposing read for column block 0, row set
 // t (rows 8 t + 4 h + 0..3 of the chunk's first 16); column block db is
@@ -367,7 +243,7 @@ __device__ inline unsigned tr3(int lane, int t) {
   const int G = lane >> 4, i = lane & 15, h = lane >> 5;
   const int row = 8 * t + 4 * h + (i >> 2);
   const int col = 16 * (G & 1) + 4 * (i & 3);
-  return static_cast<unsigned>(row * 2 * D + 16 * ((col >> 3) ^ sw3<D>(row)) + 2 * (col & 7));
+  return static_cast<unsigned>(row * 2 * D + 16 * ((col >> 3) ^ lds_sw<D>(row)) + 2 * (col & 7));
 }
 
 // Every LDS read address a wave needs in its loop, computed once per tile:
@@ -559,7 +435,7 @@ __device__ inline void b4_dkdv(const TileDesc td, const bf16* __restrict__ q_rot
         f32x16& xp = xs[PB];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          tie3(pr[j]);
+          tie_v(pr[j]);
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const float d = pr[j][e] * xp[4 * j + e];
@@ -589,15 +465,15 @@ __device__ inline void b4_dkdv(const TileDesc td, const bf16* __restrict__ q_rot
       constexpr int ahead = (NL - 1 - j) < (PF - 1) ? (NL - 1 - j) : (PF - 1);
       lgkm<RPL * ahead>();
       if constexpr (HA && j < NKK) {
-        tie3(fa[j]);
+        tie_v(fa[j]);
         if constexpr (j == 0)
           mma32_zero(xa, fa[j], kf[j]);
         else
           mma32(xa, fa[j], kf[j]);
       }
       if constexpr (HB && j < NST) {
-        tie3(ta[j][0]);
-        tie3(ta[j][1]);
+        tie_v(ta[j][0]);
+        tie_v(ta[j][1]);
         mma32_acc(acc[j >> 1], join8(ta[j][0], ta[j][1]), opb[PB][j & 1]);
       }
       if constexpr (j + PF < NL) issue_link(std::integral_constant<int, j + PF>{});
@@ -613,7 +489,7 @@ __device__ inline void b4_dkdv(const TileDesc td, const bf16* __restrict__ q_rot
       xdl_to_valu(xa);
       lgkm<0>();
 #pragma unroll
-      for (int j = 0; j < 4; ++j) tie3(st[j]);
+      for (int j = 0; j < 4; ++j) tie_v(st[j]);
       if (role == 0) {
         // P(c), masked, handed over and kept as bf16 for dV at step c + 1
 #pragma unroll
@@ -722,7 +598,7 @@ __device__ inline void b4_dkdv(const TileDesc td, const bf16* __restrict__ q_rot
       const int db = j4 >> 2, qq = j4 & 3;
       f32x4 a = lds4(sbase + static_cast<unsigned>(wr * L::REG + j * 16));
       lgkm<0>();
-      tie3(a);
+      tie_v(a);
       const int key = k0 + 32 * kqr + (sl & 31);
       const int d0 = 32 * db + 8 * qq + 4 * (sl >> 5);
       bf16* dst = rr == 0 ? wv : wk;
@@ -833,8 +709,8 @@ __device__ inline void b4_dq(const TileDesc td, const bf16* __restrict__ q_rot,
       constexpr int ahead = (NL - 1 - j) < (PF - 1) ? (NL - 1 - j) : (PF - 1);
       lgkm<RPL * ahead>();
       if constexpr (HA && j < NKK) {
-        tie3(fk[j]);
-        tie3(fv[j]);
+        tie_v(fk[j]);
+        tie_v(fv[j]);
         if constexpr (j == 0) {
           mma32_zero(s, fk[j], qf[j]);
           mma32_zero(dp, fv[j], of[j]);
@@ -844,8 +720,8 @@ __device__ inline void b4_dq(const TileDesc td, const bf16* __restrict__ q_rot,
         }
       }
       if constexpr (HB && j < NST) {
-        tie3(ta[j][0]);
-        tie3(ta[j][1]);
+        tie_v(ta[j][0]);
+        tie_v(ta[j][1]);
         mma32_acc(acc[j >> 1], join8(ta[j][0], ta[j][1]), dsb[PB][j & 1]);
       }
       if constexpr (j + PF < NL) issue_link(std::integral_constant<int, j + PF>{});
@@ -958,10 +834,10 @@ __device__ inline void b4_dq(const TileDesc td, const bf16* __restrict__ q_rot,
     f32x4 lo1 = lds4(sbase + static_cast<unsigned>((4 + qqr) * L::REG) + off0);
     f32x4 hi1 = lds4(sbase + static_cast<unsigned>((4 + qqr) * L::REG) + off1);
     lgkm<0>();
-    tie3(lo0);
-    tie3(hi0);
-    tie3(lo1);
-    tie3(hi1);
+    tie_v(lo0);
+    tie_v(hi0);
+    tie_v(lo1);
+    tie_v(hi1);
     lo0 += lo1;
     hi0 += hi1;
     const int qi2 = q0t + 32 * qqr + (sl & 31);

@@ -24,6 +24,7 @@
 // ends at the last valid row, so rows past T or past a projection's outputs
 // read as zero.  Fixed reduction order everywhere: bitwise repeatable.
 #include "attn_common.hpp"
+#include "lds_mfma.hpp"
 #include "proj_launch.hpp"
 
 namespace glacier {
@@ -279,6 +280,327 @@ __global__ __launch_bounds__(kGThreads) void proj_gemm_nn_kernel(const NarrowBwd
   store_tile(acc, a.c, a.K, f0, t0, a.K, a.T, wf, wt, lane);
 }
 
+// ---------------------------------------------------------------------------
+// Wide projections (bf16 tensors; q of a Qwen-style block: 3584 x 3584): a
+// workgroup computes a 128-feature x 64-token tile of C^T on
+// v_mfma_f32_32x32x16_bf16, 4 waves of 64 features x 32 tokens each (two
+// 32 x 32 accumulator blocks per wave).  Stages of 64 reduction elements go
+// global -> LDS by DMA (buffer_load ... lds, 16 bytes a lane) into a 4-slot
+// ring, three stages ahead; one workgroup barrier per stage.  Rows are
+// unpadded with their 16-byte pieces XOR-swizzled (lds_sw), so the fragment
+// reads (16 rows x one piece per quarter-wave) and the transposing reads of
+// the backward (4 rows x 4 pieces per half-wave) are free of bank conflicts.
+//   forward  (NT) C^T[f][t] = sum_k W[f][k] X[t][k]: both operands are read
+//            as fragments, A from the [128][64] W tile, B from the [64][64]
+//            X tile;
+//   backward (NN) C^T[c][t] = sum_f W[f][c] dY[t][f]: A from the [64 f][128 c]
+//            W tile by ds_read_b64_tr_b16 (four f of one column per read,
+//            two reads per k-step), B from the [64][64] dY tile.
+// MFMA layout (lane l, c = l % 32, h = l / 32): A[row c][k = 8h .. 8h + 7],
+// B[k = 8h ..][col c]; accumulator element e holds column c, row
+// 8 (e / 4) + 4h + e % 4, so each group of four is four consecutive
+// features of one token: one 16-byte store.
+// ---------------------------------------------------------------------------
+constexpr int kWF = 128;                 // features per tile
+constexpr int kWT = 64;                  // tokens per tile
+constexpr int kWK = 64;                  // reduction elements per stage
+constexpr int kWA = kWF * kWK * 2;       // A tile bytes (16 KB)
+constexpr int kWB = kWT * kWK * 2;       // B tile bytes (8 KB)
+constexpr int kWStage = kWA + kWB;       // one ring slot
+constexpr int kWRing = 4;
+constexpr int kWThreads = 256;
+constexpr int kWDma = (kWA + kWB) / 1024 / 4;  // DMA instructions per wave per stage (6)
+
+static_assert(kWRing * kWStage <= 160 * 1024, "ring exceeds the LDS of a CU");
+static_assert(kWStage + 4096 * 3 < 65536, "read immediates fit their 16-bit field");
+
+#if defined(__HIP_DEVICE_COMPILE__)
+__device__ inline f32x16 mma32(const bf16x8& a, const bf16x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// Per-lane DMA offsets of 128-byte rows (8 pieces): instruction n covers
+// rows 8 n .. 8 n + 7; lane l writes slot l % 8 of row 8 n + l / 8 and
+// fetches the global piece slot ^ lds_sw<64>(row), which repeats every two
+// instructions.  256-byte rows (16 pieces): rows 4 n .. 4 n + 3, slot l % 16,
+// piece slot ^ lds_sw<128>(row), repeating every four instructions.
+__device__ inline int dma_off128(int lane, int n, int rowb) {
+  const int r = 8 * n + (lane >> 3), slot = lane & 7;
+  return (lane >> 3) * rowb + 16 * (slot ^ lds_sw<64>(r));
+}
+__device__ inline int dma_off256(int lane, int n, int rowb) {
+  const int r = 4 * n + (lane >> 4), slot = lane & 15;
+  return (lane >> 4) * rowb + 16 * (slot ^ lds_sw<128>(r));
+}
+
+// Byte offset, inside a tile of 128-byte rows, of this lane's fragment read
+// of k-step 0 for rows row0 + lane % 32 (row0 a multiple of 16); k-step s
+// reads at that offset ^ 32 s.
+__device__ inline unsigned frag_off128(int lane, int row0) {
+  const int r = row0 + (lane & 31), h = lane >> 5;
+  return static_cast<unsigned>(r * 128 + 16 * (h ^ lds_sw<64>(r)));
+}
+// Byte offset, inside a tile of 256-byte rows, of this lane's transposing
+// read j (0, 1) of k-step 0 for columns col0 + 16 (G & 1) + 4 (i & 3)
+// (quarter-wave G, lane i in it): rows 8 h + 4 j + i / 4; k-step s reads
+// 16 s rows further (+4096 s), the 32 columns after col0 at ^ 64.
+__device__ inline unsigned tr_off256(int lane, int col0, int j) {
+  const int G = lane >> 4, i = lane & 15, h = lane >> 5;
+  const int r = 8 * h + 4 * j + (i >> 2);
+  const int col = col0 + 16 * (G & 1) + 4 * (i & 3);
+  return static_cast<unsigned>(r * 256 + 16 * ((col >> 3) ^ lds_sw<128>(r)) + 2 * (col & 7));
+}
+
+// Stores this wave's two 32 x 32 blocks (features fw + 32 fb, tokens tw) of
+// C^T into C [T][ldc] (fp32), rows past T skipped.
+__device__ inline void store_wide(const f32x16 (&acc)[2], float* c, long ldc, int fw, int tw, int T,
+                                  int lane) {
+  const int t = tw + (lane & 31), h = lane >> 5;
+  if (t >= T) return;
+#pragma unroll
+  for (int fb = 0; fb < 2; ++fb)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int f = fw + 32 * fb + 8 * q + 4 * h;
+      *reinterpret_cast<f32x4*>(c + (long)t * ldc + f) =
+          f32x4{acc[fb][4 * q], acc[fb][4 * q + 1], acc[fb][4 * q + 2], acc[fb][4 * q + 3]};
+    }
+}
+#endif
+
+// The stage loop shared by both directions: prologue of three stages, then
+// per stage: wait for this wave's DMA of the stage (the two later stages
+// stay in flight), barrier, DMA of the stage three ahead into the slot just
+// freed (every wave's reads of it completed before the barrier) (unconditional: past the end
+// it reads through an empty resource), then the stage's products.  The ring
+// slot of every read is an immediate offset: slots 0, 1 from the lane's
+// addresses as given, slots 2, 3 from the same + 2 kWStage.
+template <typename Issue, typename Compute>
+__device__ inline void wide_loop(int nst, Issue&& issue, Compute&& compute) {
+  issue(0, 0);
+  issue(1, 1);
+  issue(2, 2);
+  int st = 0;
+  auto one = [&](auto slot) {
+    constexpr int SL = decltype(slot)::value;
+    vmw<2 * kWDma>();
+    wg_barrier();
+    issue(st + 3, (SL + 3) & 3);
+    compute(slot);
+    ++st;
+  };
+#pragma clang loop unroll(disable)
+  while (st + 3 < nst) {
+    one(std::integral_constant<int, 0>{});
+    one(std::integral_constant<int, 1>{});
+    one(std::integral_constant<int, 2>{});
+    one(std::integral_constant<int, 3>{});
+  }
+  if (st < nst) one(std::integral_constant<int, 0>{});
+  if (st < nst) one(std::integral_constant<int, 1>{});
+  if (st < nst) one(std::integral_constant<int, 2>{});
+  vmw<0>();  // the DMA issued past the end lands before the workgroup ends
+}
+
+__global__ __launch_bounds__(kWThreads) void proj_gemm_wide_nt_kernel(const WideFwd a) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __shared__ __align__(1024) unsigned char lds[kWRing * kWStage];
+  const int ttiles = (a.T + kWT - 1) / kWT;
+  const int id = xcd_logical((int)blockIdx.x, (int)gridDim.x);
+  const int t0 = kWT * (id % ttiles), f0 = kWF * (id / ttiles);
+  const int lane = threadIdx.x & 63, w = wave_id();
+  const int wf = w & 1, wt = w >> 1;
+  const int rowb = a.K * 2;
+  // A: W rows f0 .., B: X rows t0 .. (rows past T read as zeros)
+  const __amdgpu_buffer_rsrc_t ra =
+      wave_rsrc(static_cast<const bf16*>(a.w) + (long)f0 * a.K, kWF * rowb);
+  const __amdgpu_buffer_rsrc_t rb = wave_rsrc(static_cast<const bf16*>(a.x) + (long)t0 * a.K,
+                                              max(0, min(kWT, a.T - t0)) * rowb);
+  const __amdgpu_buffer_rsrc_t rz = wave_rsrc(a.x, 0);
+  // this wave's DMA: A rows 32 w .. 32 w + 31 (4 instructions; every row
+  // valid, the row block in the scalar offset), B rows 16 w .. 16 w + 15 (2
+  // instructions; the row in the per-lane offset, which alone is checked
+  // against the resource's range, so rows past T read as zeros)
+  const int oa0 = dma_off128(lane, 0, rowb), oa1 = dma_off128(lane, 1, rowb);
+  const int ob0 = dma_off128(lane, 0, rowb) + 16 * w * rowb, ob1 = dma_off128(lane, 1, rowb) + (16 * w + 8) * rowb;
+  const unsigned sbase = static_cast<unsigned>(reinterpret_cast<uintptr_t>((GLACIER_LDS void*)lds));
+  auto issue = [&](int st, int slot) {
+    const bool live = st < a.K / kWK;
+    const __amdgpu_buffer_rsrc_t sa = live ? ra : rz, sb = live ? rb : rz;
+    unsigned char* base = lds + slot * kWStage;
+    const int k0 = st * kWK * 2;
+#pragma unroll
+    for (int n = 0; n < 4; ++n)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(sa, (GLACIER_LDS void*)(base + (32 * w + 8 * n) * 128), 16,
+                                               (n & 1) ? oa1 : oa0, (32 * w + 8 * n) * rowb + k0, 0, 0);
+#pragma unroll
+    for (int n = 0; n < 2; ++n)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(sb, (GLACIER_LDS void*)(base + kWA + (16 * w + 8 * n) * 128),
+                                               16, n ? ob1 : ob0, k0, 0, 0);
+  };
+  // read addresses: A rows 64 wf + 32 fb (fb at +4096), B rows 32 wt; k-step s
+  unsigned fa[2][4], fbb[2][4];
+  {
+    const unsigned oa = frag_off128(lane, 64 * wf), ob = frag_off128(lane, 32 * wt);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      fa[0][s] = sbase + (oa ^ (32u * s));
+      fbb[0][s] = sbase + kWA + (ob ^ (32u * s));
+      fa[1][s] = fa[0][s] + 2 * kWStage;
+      fbb[1][s] = fbb[0][s] + 2 * kWStage;
+    }
+  }
+  f32x16 acc[2];
+#pragma unroll
+  for (int fb = 0; fb < 2; ++fb)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[fb][e] = 0.0f;
+  auto compute = [&](auto slot) {
+    constexpr int SL = decltype(slot)::value, HS = SL >> 1, OFF = (SL & 1) * kWStage;
+    bf16x8 ra_[4][2], rb_[4];
+    auto rd = [&](auto sc) {
+      constexpr int S = decltype(sc)::value;
+      ra_[S][0] = rd128<OFF>(fa[HS][S]);
+      ra_[S][1] = rd128<OFF + 4096>(fa[HS][S]);
+      rb_[S] = rd128<OFF>(fbb[HS][S]);
+    };
+    rd(std::integral_constant<int, 0>{});
+    rd(std::integral_constant<int, 1>{});
+    static_for<4>([&](auto sc) {
+      constexpr int S = decltype(sc)::value;
+      if constexpr (S + 2 < 4) {
+        lgkm<3>();
+        rd(std::integral_constant<int, S + 2>{});
+        lgkm<6>();
+      } else if constexpr (S == 2) {
+        lgkm<3>();
+      } else {
+        lgkm<0>();
+      }
+      tie_v(ra_[S][0]);
+      tie_v(ra_[S][1]);
+      tie_v(rb_[S]);
+      acc[0] = mma32(ra_[S][0], rb_[S], acc[0]);
+      acc[1] = mma32(ra_[S][1], rb_[S], acc[1]);
+    });
+  };
+  wide_loop(a.K / kWK, issue, compute);
+  store_wide(acc, a.c, a.n, f0 + 64 * wf, t0 + 32 * wt, a.T, lane);
+#endif
+}
+
+__global__ __launch_bounds__(kWThreads) void proj_gemm_wide_nn_kernel(const WideBwd a) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __shared__ __align__(1024) unsigned char lds[kWRing * kWStage];
+  const int ttiles = (a.T + kWT - 1) / kWT;
+  const int id = xcd_logical((int)blockIdx.x, (int)gridDim.x);
+  const int t0 = kWT * (id % ttiles), c0 = kWF * (id / ttiles);
+  const int lane = threadIdx.x & 63, w = wave_id();
+  const int wf = w & 1, wt = w >> 1;
+  const int rowbw = a.K * 2;
+  int nst = 0;
+  for (int z = 0; z < a.n; ++z) nst += a.j[z].n / kWK;
+  const __amdgpu_buffer_rsrc_t rz = wave_rsrc(a.j[0].w, 0);
+  const int ow[4] = {dma_off256(lane, 0, rowbw), dma_off256(lane, 1, rowbw), dma_off256(lane, 2, rowbw),
+                     dma_off256(lane, 3, rowbw)};
+  const unsigned sbase = static_cast<unsigned>(reinterpret_cast<uintptr_t>((GLACIER_LDS void*)lds));
+  // the job of the stages being issued (stages are issued in order): its
+  // resources over W_z (from column c0) and dY_z (from token t0), its first
+  // stage and the first stage of the next job
+  int z = -1, zbase = 0, zend = 0, rowby = 0, oy0 = 0, oy1 = 0;
+  __amdgpu_buffer_rsrc_t ra = rz, rb = rz;
+  auto issue = [&](int st, int slot) {
+    while (st >= zend && z + 1 < a.n) {
+      ++z;
+      zbase = zend;
+      zend += a.j[z].n / kWK;
+      const WideJob& job = a.j[z];
+      rowby = job.n * 2;
+      ra = wave_rsrc(static_cast<const bf16*>(job.w) + c0, (job.n - 1) * rowbw + kWF * 2);
+      rb = wave_rsrc(static_cast<const bf16*>(job.dy) + (long)t0 * job.n,
+                     max(0, min(kWT, a.T - t0)) * rowby);
+      // the row in the per-lane offset (checked against the range: rows
+      // past T read as zeros), the column f0 in the scalar one
+      oy0 = dma_off128(lane, 0, rowby) + 16 * w * rowby;
+      oy1 = dma_off128(lane, 1, rowby) + (16 * w + 8) * rowby;
+    }
+    const bool live = st < nst;
+    const __amdgpu_buffer_rsrc_t sa = live ? ra : rz, sb = live ? rb : rz;
+    const int f0 = (st - zbase) * kWK;  // the job's reduction rows f0 .. f0 + 63
+    unsigned char* base = lds + slot * kWStage;
+    // A: W_z[f0 + r][c0 ..] (256-byte rows); B: dY_z[t0 + r][f0 ..] (128 bytes)
+#pragma unroll
+    for (int n = 0; n < 4; ++n)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(sa, (GLACIER_LDS void*)(base + (16 * w + 4 * n) * 256), 16,
+                                               ow[n], (f0 + 16 * w + 4 * n) * rowbw, 0, 0);
+#pragma unroll
+    for (int n = 0; n < 2; ++n)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(sb, (GLACIER_LDS void*)(base + kWA + (16 * w + 8 * n) * 128),
+                                               16, n ? oy1 : oy0, 2 * f0, 0, 0);
+  };
+  // read addresses: A transposed, columns 64 wf + 32 fb (fb: ^ 64), reads j;
+  // B fragments rows 32 wt, k-step s
+  unsigned ta[2][2][2], fbb[2][4];
+  {
+    const unsigned o0 = tr_off256(lane, 64 * wf, 0), o1 = tr_off256(lane, 64 * wf, 1);
+    const unsigned ob = frag_off128(lane, 32 * wt);
+#pragma unroll
+    for (int hs = 0; hs < 2; ++hs) {
+#pragma unroll
+      for (int fb = 0; fb < 2; ++fb) {
+        ta[hs][fb][0] = sbase + 2u * kWStage * hs + (o0 ^ (64u * fb));
+        ta[hs][fb][1] = sbase + 2u * kWStage * hs + (o1 ^ (64u * fb));
+      }
+#pragma unroll
+      for (int s = 0; s < 4; ++s) fbb[hs][s] = sbase + 2u * kWStage * hs + kWA + (ob ^ (32u * s));
+    }
+  }
+  f32x16 acc[2];
+#pragma unroll
+  for (int fb = 0; fb < 2; ++fb)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[fb][e] = 0.0f;
+  auto compute = [&](auto slot) {
+    constexpr int SL = decltype(slot)::value, HS = SL >> 1, OFF = (SL & 1) * kWStage;
+    bf16x4 rt[4][2][2];
+    bf16x8 rb_[4];
+    auto rd = [&](auto sc) {
+      constexpr int S = decltype(sc)::value;
+#pragma unroll
+      for (int fb = 0; fb < 2; ++fb) {
+        rt[S][fb][0] = rdtr<OFF + 4096 * S>(ta[HS][fb][0]);
+        rt[S][fb][1] = rdtr<OFF + 4096 * S>(ta[HS][fb][1]);
+      }
+      rb_[S] = rd128<OFF>(fbb[HS][S]);
+    };
+    rd(std::integral_constant<int, 0>{});
+    rd(std::integral_constant<int, 1>{});
+    static_for<4>([&](auto sc) {
+      constexpr int S = decltype(sc)::value;
+      if constexpr (S + 2 < 4) {
+        lgkm<5>();
+        rd(std::integral_constant<int, S + 2>{});
+        lgkm<10>();
+      } else if constexpr (S == 2) {
+        lgkm<5>();
+      } else {
+        lgkm<0>();
+      }
+#pragma unroll
+      for (int fb = 0; fb < 2; ++fb) {
+        tie_v(rt[S][fb][0]);
+        tie_v(rt[S][fb][1]);
+      }
+      tie_v(rb_[S]);
+      acc[0] = mma32(join8(rt[S][0][0], rt[S][0][1]), rb_[S], acc[0]);
+      acc[1] = mma32(join8(rt[S][1][0], rt[S][1][1]), rb_[S], acc[1]);
+    });
+  };
+  wide_loop(nst, issue, compute);
+  store_wide(acc, a.c, a.K, c0 + 64 * wf, t0 + 32 * wt, a.T, lane);
+#endif
+}
+
 }  // namespace
 
 bool narrow_gemm_fits(int in_features, int out_features) {
@@ -303,6 +625,28 @@ hipError_t launch_narrow_fwd(NarrowFwd a, hipStream_t st) {
   }
   if (total == 0) return hipSuccess;
   hipLaunchKernelGGL(proj_gemm_nt_kernel, dim3(total), dim3(kGThreads), 0, st, a);
+  return hipGetLastError();
+}
+
+bool wide_gemm_fits(int in_features, int out_features) {
+  return in_features % kWF == 0 && out_features % kWF == 0;
+}
+
+hipError_t launch_wide_fwd(const WideFwd& a, hipStream_t st) {
+  const int ttiles = (a.T + kWT - 1) / kWT, ftiles = a.n / kWF;
+  if (ttiles == 0 || ftiles == 0) return hipSuccess;
+  if (a.K % kWK != 0 || a.n % kWF != 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(proj_gemm_wide_nt_kernel, dim3(ttiles * ftiles), dim3(kWThreads), 0, st, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_wide_bwd(const WideBwd& a, hipStream_t st) {
+  const int ttiles = (a.T + kWT - 1) / kWT, ftiles = a.K / kWF;
+  if (ttiles == 0 || ftiles == 0 || a.n == 0) return hipSuccess;
+  if (a.K % kWF != 0) return hipErrorInvalidValue;
+  for (int z = 0; z < a.n; ++z)
+    if (a.j[z].n % kWK != 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(proj_gemm_wide_nn_kernel, dim3(ttiles * ftiles), dim3(kWThreads), 0, st, a);
   return hipGetLastError();
 }
 

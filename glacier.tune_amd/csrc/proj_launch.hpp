@@ -78,13 +78,43 @@ int narrow_feature_tiles(int out_features);
 hipError_t launch_narrow_fwd(NarrowFwd a, hipStream_t st);
 hipError_t launch_narrow_bwd(const NarrowBwd& a, hipStream_t st);
 
+// ---- the wide base products on the library's own GEMM (proj_gemm.hip) ----
+// bf16 tensors, inputs and outputs multiples of 128 (the q projection).
+struct WideJob {
+  const void* w;   // W_z [n][K] (bf16)
+  const void* dy;  // dY_z [T][n] (bf16)
+  int n;           // outputs of the projection
+};
+// c [T][n] = X W^T (fp32), one projection.
+struct WideFwd {
+  const void* x;  // [T][K] (bf16)
+  const void* w;  // [n][K] (bf16)
+  float* c;
+  int T, K, n;
+};
+// c [T][K] = sum over the jobs of dY_z W_z (fp32).
+struct WideBwd {
+  float* c;
+  int T, K, n;
+  WideJob j[kMaxProj];
+};
+bool wide_gemm_fits(int in_features, int out_features);
+hipError_t launch_wide_fwd(const WideFwd& a, hipStream_t st);
+hipError_t launch_wide_bwd(const WideBwd& a, hipStream_t st);
+
 // Floats of each ProjLaunch scratch buffer for a forward or backward call.
 struct ProjScratchNeed {
   long yf, dxf, lowrank, part;
 };
 ProjScratchNeed proj_scratch_need(const ProjLaunch& a, bool backward);
 
-// Enqueue on st; blas is a handle from create_blas_handle() (blas_lt.hpp).
+// Whether a call has a projection that neither of the library's own GEMMs
+// covers (fp32 tensors, or shapes off their tiles): only then is a
+// hipBLASLt handle needed.
+bool proj_needs_blas(const ProjLaunch& a);
+
+// Enqueue on st; blas is a handle from create_blas_handle() (blas_lt.hpp),
+// or null when proj_needs_blas(a) is false.
 hipError_t launch_proj_forward(const ProjLaunch& a, hipStream_t st, void* blas);
 hipError_t launch_proj_backward(const ProjLaunch& a, hipStream_t st, void* blas);
 

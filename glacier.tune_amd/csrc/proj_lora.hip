@@ -484,9 +484,14 @@ hipError_t run_out(const ProjLaunch& a, OutJobs& jobs, hipStream_t st) {
 
 const float* slot(const ProjLaunch& a, int z) { return a.lowrank + (long)z * a.T * a.rank; }
 
-// Which projections of a call take the library's own narrow GEMM.
+// Which projections of a call take the library's own narrow GEMM, which
+// its own wide GEMM; the rest (fp32 tensors, shapes neither covers) take
+// hipBLASLt.
 bool is_narrow(const ProjLaunch& a, int p) {
   return a.io_bf16 && narrow_gemm_fits(a.in, a.p[p].out);
+}
+bool is_wide(const ProjLaunch& a, int p) {
+  return a.io_bf16 && !is_narrow(a, p) && wide_gemm_fits(a.in, a.p[p].out);
 }
 
 // Input slices of the narrow forward launch (1 when there is none).
@@ -518,6 +523,10 @@ hipError_t forward_impl(const ProjLaunch& a, hipStream_t st, void* h) {
       out.j[p].nbase = nf.nsplit;
       out.j[p].stride = (long)a.T * s.out;
       off += (long)nf.nsplit * a.T * s.out;
+    } else if (is_wide(a, p)) {
+      // Yf_p = X W_p^T on the library's own wide GEMM
+      GL_CHECK(launch_wide_fwd(WideFwd{a.x, s.w, a.yf + off, a.T, a.in, s.out}, st));
+      off += (long)a.T * s.out;
     } else {
       // Yf_p = X W_p^T
       GL_CHECK(blas_gemm(h, BF, false, true, a.T, s.out, a.in, 1.0f, a.x, a.in, s.w, a.in, 0.0f,
@@ -542,19 +551,32 @@ hipError_t forward_impl(const ProjLaunch& a, hipStream_t st, void* h) {
 template <typename IO>
 hipError_t backward_impl(const ProjLaunch& a, hipStream_t st, void* h) {
   constexpr bool BF = sizeof(IO) == 2;
-  // dXf = sum_p dY_p W_p: the library GEMM for the wide projections into
-  // dxf, the narrow ones into the buffer after it; lowrank_out adds the two
+  // dXf = sum_p dY_p W_p: the wide projections (own wide GEMM, one launch
+  // over all of them, then hipBLASLt for any other) into dxf, the narrow
+  // ones into the buffer after it; lowrank_out adds the two
   NarrowBwd nb{};
   nb.T = a.T;
   nb.K = a.in;
   nb.c = a.dxf + (long)a.T * a.in;
-  int wide = 0;
+  WideBwd wb{};
+  wb.c = a.dxf;
+  wb.T = a.T;
+  wb.K = a.in;
   for (int p = 0; p < a.n_proj; ++p) {
     const ProjSpec& s = a.p[p];
-    if (is_narrow(a, p)) {
+    if (is_narrow(a, p))
       nb.j[nb.n++] = NarrowJob{s.w, s.dy, nullptr, s.out, 0};
-      continue;
-    }
+    else if (is_wide(a, p))
+      wb.j[wb.n++] = WideJob{s.w, s.dy, s.out};
+  }
+  int wide = 0;  // products written into dxf so far
+  if (wb.n > 0) {
+    GL_CHECK(launch_wide_bwd(wb, st));
+    wide = wb.n;
+  }
+  for (int p = 0; p < a.n_proj; ++p) {
+    const ProjSpec& s = a.p[p];
+    if (is_narrow(a, p) || is_wide(a, p)) continue;
     GL_CHECK(blas_gemm(h, BF, false, false, a.T, a.in, s.out, 1.0f, s.dy, s.out, s.w, a.in,
                        wide == 0 ? 0.0f : 1.0f, a.dxf, a.in, st));
     ++wide;
@@ -630,6 +652,12 @@ ProjScratchNeed proj_scratch_need(const ProjLaunch& a, bool backward) {
     need.part = (long)plan.n * rows_splits(a, plan) * slabs * 256 * nt;
   }
   return need;
+}
+
+bool proj_needs_blas(const ProjLaunch& a) {
+  for (int p = 0; p < a.n_proj; ++p)
+    if (!is_narrow(a, p) && !is_wide(a, p)) return true;
+  return false;
 }
 
 hipError_t launch_proj_forward(const ProjLaunch& a, hipStream_t st, void* blas) {

@@ -95,6 +95,10 @@ SHAPES = {  # T, in, (q, k, v outs), rank
     "ragged_t37": (37, 96, (64, 32, 32), 4),
     "r40_t70": (70, 192, (128, 64, 64), 40),  # 3 rank tiles, the last one partial
     "r64_t50": (50, 256, (64, 32, 128), 64),  # the largest rank
+    # two projections on the wide GEMM (outputs over 1024, multiples of 128:
+    # one backward launch reduces over both) beside a narrow one; a partial
+    # token tile
+    "wide_t70": (70, 256, (1152, 1280, 64), 8),
 }
 
 
