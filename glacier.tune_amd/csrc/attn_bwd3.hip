@@ -540,7 +540,7 @@ __device__ inline void b4_dkdv(const TileDesc td, const bf16* __restrict__ q_rot
   step(std::integral_constant<int, 0>{}, std::integral_constant<int, 3>{}, B1{}, B0{}, 0);
   dma_end(0);
   GL_STAMP(kKernBwd, 4);
-  __syncthreads();
+  wg_barrier();
   // steps 1 .. nst - 1: chains of chunk c, products of chunk c - 1, in
   // groups of four by slot
   int c = 1;
@@ -550,7 +550,7 @@ __device__ inline void b4_dkdv(const TileDesc td, const bf16* __restrict__ q_rot
     step(sa, std::integral_constant<int, (SA + 3) & 3>{}, B1{}, B1{}, cc);
     dma_end(cc);
     if (cc < 12) GL_STAMP(kKernBwd, 4 + cc);
-    __syncthreads();
+    wg_barrier();
   };
 #pragma clang loop unroll(disable)
   for (; c + 3 < nst; c += 4) {
@@ -768,7 +768,7 @@ __device__ inline void b4_dq(const TileDesc td, const bf16* __restrict__ q_rot,
     dma_end(0);
   }
   GL_STAMP(kKernBwd, 4);
-  __syncthreads();
+  wg_barrier();
   c = 1;
   auto full = [&](auto sa, int cc) {
     constexpr int SA = decltype(sa)::value;
@@ -776,7 +776,7 @@ __device__ inline void b4_dq(const TileDesc td, const bf16* __restrict__ q_rot,
     step(sa, std::integral_constant<int, (SA + 3) & 3>{}, B1{}, B1{}, cc);
     dma_end(cc);
     if (cc < 12) GL_STAMP(kKernBwd, 4 + cc);
-    __syncthreads();
+    wg_barrier();
   };
 #pragma clang loop unroll(disable)
   for (; c + 3 < mych; c += 4) {
@@ -808,7 +808,7 @@ __device__ inline void b4_dq(const TileDesc td, const bf16* __restrict__ q_rot,
   }
   // every wave passes 1 + nch barriers in the loop above (a group with
   // mych chunks passes 1 + max(mych - 1, 0)); make up the difference
-  for (int k = (mych > 0 ? mych : 1); k < nch; ++k) __syncthreads();
+  for (int k = (mych > 0 ? mych : 1); k < nch; ++k) wg_barrier();
   GL_STAMP(kKernBwd, 20);
 
   fence16(acc);

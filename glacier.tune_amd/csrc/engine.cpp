@@ -594,16 +594,14 @@ class GpuAttentionEngine {
   void ProjForward(ProjLaunch& a) {
     if (a.T == 0) return;
     ProjScratch(a, false);
-    check_hip(launch_proj_forward(a, stream(), proj_needs_blas(a) ? blas() : nullptr),
-              "projection forward launch");
+    check_hip(launch_proj_forward(a, stream()), "projection forward launch");
   }
 
   // The block's LoraAdapter.Backward calls (LoraAdapter.cs:190-247).
   void ProjBackward(ProjLaunch& a) {
     if (a.T == 0) return;
     ProjScratch(a, true);
-    check_hip(launch_proj_backward(a, stream(), proj_needs_blas(a) ? blas() : nullptr),
-              "projection backward launch");
+    check_hip(launch_proj_backward(a, stream()), "projection backward launch");
   }
 
   // ---- residual add and RMSNorm (glacier_norm.h) ------------------------

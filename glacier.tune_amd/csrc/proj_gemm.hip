@@ -601,6 +601,168 @@ __global__ __launch_bounds__(kWThreads) void proj_gemm_wide_nn_kernel(const Wide
 #endif
 }
 
+// ---------------------------------------------------------------------------
+// Every other projection (fp32 tensors, the fp32-operand mode, or bf16
+// tensors of a shape neither kernel above takes): both directions on
+// v_mfma_f32_16x16x4f32, any shape, operands converted to fp32 on load.  A workgroup computes a 64-feature x
+// 64-token tile of C^T, 4 waves of 32 x 32 (2 x 2 blocks of 16 x 16).
+// Stages of 32 reduction elements go global -> registers -> LDS (two
+// buffers, one barrier per stage, the next stage's loads in flight during
+// the products); elements past any edge load as zero.
+//   forward  (NT) C^T[f][t] = sum_k W[f][k] X[t][k]   (A tile [f][k])
+//   backward (NN) C^T[c][t] = sum_z sum_f W_z[f][c] dY_z[t][f]   (A tile [f][c])
+// MFMA layout (lane l, c = l % 16, g = l / 16): A[row c][k = g],
+// B[k = g][col c]; accumulator i holds column c, row 4 g + i: four
+// consecutive features of one token.
+// ---------------------------------------------------------------------------
+constexpr int kFT = 64;       // features and tokens per tile
+constexpr int kFK = 32;       // reduction elements per stage
+constexpr int kFS = kFK + 4;  // row stride of [row][k] tiles (floats): conflict-free
+constexpr int kFC = kFT + 16; // row stride of the backward's [k][feature] tile
+constexpr int kFThreads = 256;
+
+// Four elements k .. k + 3 of a row (len elements valid) as fp32, zero past
+// the end; vec: the row allows one aligned vector load.
+template <typename IO>
+__device__ inline f32x4 load4_f32(const IO* row, int k, int len, bool vec) {
+  if (vec && k + 3 < len) {
+    if constexpr (sizeof(IO) == 4) {
+      return *reinterpret_cast<const f32x4*>(row + k);
+    } else {
+      const bf16x4 h = *reinterpret_cast<const bf16x4*>(row + k);
+      return f32x4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
+    }
+  }
+  f32x4 v;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = k + i < len ? (float)row[k + i] : 0.0f;
+  return v;
+}
+
+template <typename IO, bool NN>
+__global__ __launch_bounds__(kFThreads) void proj_gemm_f32_kernel(const WideFwd fa, const WideBwd ba) {
+  __shared__ __align__(16) float la[2][NN ? kFK * kFC : kFT * kFS];
+  __shared__ __align__(16) float lb[2][kFT * kFS];
+  const int T = NN ? ba.T : fa.T;
+  const int nout = NN ? ba.K : fa.n;  // C^T rows: features
+  const int ttiles = (T + kFT - 1) / kFT;
+  const int id = xcd_logical((int)blockIdx.x, (int)gridDim.x);
+  const int t0 = kFT * (id % ttiles), f0 = kFT * (id / ttiles);
+  const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
+  const int wf = w & 1, wt = w >> 1, c = lane & 15, g = lane >> 4;
+  // stages: forward over K; backward over every job's outputs in turn
+  int nst = 0;
+  if constexpr (NN) {
+    for (int z = 0; z < ba.n; ++z) nst += (ba.j[z].n + kFK - 1) / kFK;
+  } else {
+    nst = (fa.K + kFK - 1) / kFK;
+  }
+  f32x4 ra[2], rb[2];
+  auto load = [&](int st) {
+    const IO* wsrc;
+    const IO* bsrc;
+    int k0, klen, bstride;
+    if constexpr (NN) {
+      int z = 0, base = 0;
+      while (z + 1 < ba.n && st >= base + (ba.j[z].n + kFK - 1) / kFK) base += (ba.j[z++].n + kFK - 1) / kFK;
+      k0 = kFK * (st - base);
+      klen = ba.j[z].n;
+      wsrc = static_cast<const IO*>(ba.j[z].w);
+      bsrc = static_cast<const IO*>(ba.j[z].dy);
+      bstride = klen;
+    } else {
+      k0 = kFK * st;
+      klen = fa.K;
+      wsrc = static_cast<const IO*>(fa.w);
+      bsrc = static_cast<const IO*>(fa.x);
+      bstride = fa.K;
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int idx = tid + kFThreads * i;
+      if constexpr (NN) {
+        // A: W_z rows k0 + idx / 16 (of klen), columns f0 + 4 (idx % 16)
+        const int kr = k0 + (idx >> 4), cc = f0 + 4 * (idx & 15);
+        ra[i] = kr < klen ? load4_f32(wsrc + (long)kr * ba.K, cc, nout, (ba.K & 3) == 0) : f32x4{0, 0, 0, 0};
+      } else {
+        // A: W rows f0 + idx / 8, columns k0 + 4 (idx % 8)
+        const int fr = f0 + (idx >> 3), kc = k0 + 4 * (idx & 7);
+        ra[i] = fr < nout ? load4_f32(wsrc + (long)fr * fa.K, kc, klen, (fa.K & 3) == 0) : f32x4{0, 0, 0, 0};
+      }
+      // B: rows t0 + idx / 8 (tokens), columns k0 + 4 (idx % 8)
+      const int tr = t0 + (idx >> 3), kc = k0 + 4 * (idx & 7);
+      rb[i] = tr < T ? load4_f32(bsrc + (long)tr * bstride, kc, klen, (bstride & 3) == 0) : f32x4{0, 0, 0, 0};
+    }
+  };
+  auto store = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int idx = tid + kFThreads * i;
+      if constexpr (NN)
+        *reinterpret_cast<f32x4*>(&la[buf][(idx >> 4) * kFC + 4 * (idx & 15)]) = ra[i];
+      else
+#pragma unroll
+        for (int e = 0; e < 4; ++e) la[buf][(idx >> 3) * kFS + 4 * (idx & 7) + e] = ra[i][e];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) lb[buf][(idx >> 3) * kFS + 4 * (idx & 7) + e] = rb[i][e];
+    }
+  };
+  f32x4 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  if (nst > 0) {
+    load(0);
+    store(0);
+  }
+  __syncthreads();
+  for (int st = 0; st < nst; ++st) {
+    const int buf = st & 1;
+    if (st + 1 < nst) load(st + 1);
+#pragma unroll
+    for (int kk = 0; kk < kFK / 4; ++kk) {
+      float av[2], bv[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int fr = 32 * wf + 16 * i + c, tr = 32 * wt + 16 * i + c, k = 4 * kk + g;
+        av[i] = NN ? la[buf][k * kFC + fr] : la[buf][fr * kFS + k];
+        bv[i] = lb[buf][tr * kFS + k];
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i], bv[j], acc[i][j], 0, 0, 0);
+    }
+    if (st + 1 < nst) store(buf ^ 1);
+    __syncthreads();
+  }
+  // C [T][nout]: token t0 + 32 wt + 16 j + c, features f0 + 32 wf + 16 i + 4 g ..
+  float* cdst = NN ? ba.c : fa.c;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int t = t0 + 32 * wt + 16 * j + c;
+    if (t >= T) continue;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int f = f0 + 32 * wf + 16 * i + 4 * g;
+      float* d = cdst + (long)t * nout + f;
+      // backward after the wide kernel: add to what it wrote
+      const bool add = NN && ba.accumulate;
+      if (f + 3 < nout && (nout & 3) == 0) {
+        f32x4 v = acc[i][j];
+        if (add) v += *reinterpret_cast<const f32x4*>(d);
+        *reinterpret_cast<f32x4*>(d) = v;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (f + e < nout) d[e] = add ? d[e] + acc[i][j][e] : acc[i][j][e];
+      }
+    }
+  }
+}
+
 }  // namespace
 
 bool narrow_gemm_fits(int in_features, int out_features) {
@@ -647,6 +809,22 @@ hipError_t launch_wide_bwd(const WideBwd& a, hipStream_t st) {
   for (int z = 0; z < a.n; ++z)
     if (a.j[z].n % kWK != 0) return hipErrorInvalidValue;
   hipLaunchKernelGGL(proj_gemm_wide_nn_kernel, dim3(ttiles * ftiles), dim3(kWThreads), 0, st, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_generic_fwd(const WideFwd& a, bool io_bf16, hipStream_t st) {
+  const int ttiles = (a.T + kFT - 1) / kFT, ftiles = (a.n + kFT - 1) / kFT;
+  if (ttiles == 0 || ftiles == 0) return hipSuccess;
+  auto fn = io_bf16 ? proj_gemm_f32_kernel<bf16, false> : proj_gemm_f32_kernel<float, false>;
+  hipLaunchKernelGGL(fn, dim3(ttiles * ftiles), dim3(kFThreads), 0, st, a, WideBwd{});
+  return hipGetLastError();
+}
+
+hipError_t launch_generic_bwd(const WideBwd& a, bool io_bf16, hipStream_t st) {
+  const int ttiles = (a.T + kFT - 1) / kFT, ftiles = (a.K + kFT - 1) / kFT;
+  if (ttiles == 0 || ftiles == 0 || a.n == 0) return hipSuccess;
+  auto fn = io_bf16 ? proj_gemm_f32_kernel<bf16, true> : proj_gemm_f32_kernel<float, true>;
+  hipLaunchKernelGGL(fn, dim3(ttiles * ftiles), dim3(kFThreads), 0, st, WideFwd{}, a);
   return hipGetLastError();
 }
 

@@ -92,15 +92,22 @@ struct WideFwd {
   float* c;
   int T, K, n;
 };
-// c [T][K] = sum over the jobs of dY_z W_z (fp32).
+// c [T][K] = sum over the jobs of dY_z W_z (fp32); accumulate (generic
+// kernel only): c += instead.
 struct WideBwd {
   float* c;
   int T, K, n;
   WideJob j[kMaxProj];
+  bool accumulate;
 };
 bool wide_gemm_fits(int in_features, int out_features);
 hipError_t launch_wide_fwd(const WideFwd& a, hipStream_t st);
 hipError_t launch_wide_bwd(const WideBwd& a, hipStream_t st);
+
+// ---- every other projection: the same two products on fp32 MFMAs, any ----
+// shape, fp32 or bf16 operands (io_bf16) converted to fp32 on load
+hipError_t launch_generic_fwd(const WideFwd& a, bool io_bf16, hipStream_t st);
+hipError_t launch_generic_bwd(const WideBwd& a, bool io_bf16, hipStream_t st);
 
 // Floats of each ProjLaunch scratch buffer for a forward or backward call.
 struct ProjScratchNeed {
@@ -108,14 +115,8 @@ struct ProjScratchNeed {
 };
 ProjScratchNeed proj_scratch_need(const ProjLaunch& a, bool backward);
 
-// Whether a call has a projection that neither of the library's own GEMMs
-// covers (fp32 tensors, or shapes off their tiles): only then is a
-// hipBLASLt handle needed.
-bool proj_needs_blas(const ProjLaunch& a);
-
-// Enqueue on st; blas is a handle from create_blas_handle() (blas_lt.hpp),
-// or null when proj_needs_blas(a) is false.
-hipError_t launch_proj_forward(const ProjLaunch& a, hipStream_t st, void* blas);
-hipError_t launch_proj_backward(const ProjLaunch& a, hipStream_t st, void* blas);
+// Enqueue on st.
+hipError_t launch_proj_forward(const ProjLaunch& a, hipStream_t st);
+hipError_t launch_proj_backward(const ProjLaunch& a, hipStream_t st);
 
 }  // namespace glacier

@@ -10,11 +10,12 @@
 //   backward  dX   = sum_p dY_p W_p + s_p (dY_p B_p^T) A_p^T
 //             dA_p += s_p X^T (dY_p B_p^T),  dB_p += s_p (X A_p)^T dY_p
 //
-// The base products X W_p^T and dY_p W_p are GEMMs with fp32 results:
-// hipBLASLt (blas_lt.cpp) for the wide ones, the library's own kernels
-// (proj_gemm.hip) for the narrow ones of bf16 tensors (the k and v
-// projections of a GQA block).  Everything low-rank is here, each kernel taking every
-// projection of the call in one launch:
+// The base products X W_p^T and dY_p W_p are GEMMs with fp32 results, all on
+// the library's own kernels (proj_gemm.hip): for bf16 tensors the narrow
+// GEMM (the k and v projections of a GQA block) and the wide one (q), and
+// for fp32 tensors or shapes neither takes, a generic fp32-MFMA GEMM.
+// Everything low-rank is here, each kernel taking every projection of the
+// call in one launch:
 //   lowrank_rows    L = X A_p and dL = dY_p B_p^T (output r columns wide,
 //                   reduction over in / out): 16-row slabs, the reduction
 //                   split over workgroups and over their 8 waves, fp32 MFMAs
@@ -26,13 +27,10 @@
 //                   product on MFMAs, fused with the dtype conversion
 // The adapters, the low-rank activations and the gradients stay fp32, as in
 // the reference (LoraAdapter.cs:23-24); bf16 tensors round only the base
-// operands and the outputs.  hipBLASLt runs without workspace (no split
-// reductions) and every reduction here has a fixed order, so every result is
-// bitwise repeatable.
+// operands and the outputs.  Every reduction has a fixed order, so every
+// result is bitwise repeatable.
 #include "attn_common.hpp"
 #include "proj_launch.hpp"
-
-#include "blas_lt.hpp"
 
 namespace glacier {
 namespace {
@@ -484,9 +482,8 @@ hipError_t run_out(const ProjLaunch& a, OutJobs& jobs, hipStream_t st) {
 
 const float* slot(const ProjLaunch& a, int z) { return a.lowrank + (long)z * a.T * a.rank; }
 
-// Which projections of a call take the library's own narrow GEMM, which
-// its own wide GEMM; the rest (fp32 tensors, shapes neither covers) take
-// hipBLASLt.
+// Which projections of a call take the narrow GEMM, which the wide one; the
+// rest (fp32 tensors, shapes neither covers) take the generic one.
 bool is_narrow(const ProjLaunch& a, int p) {
   return a.io_bf16 && narrow_gemm_fits(a.in, a.p[p].out);
 }
@@ -503,8 +500,7 @@ int fwd_splits(const ProjLaunch& a) {
 }
 
 template <typename IO>
-hipError_t forward_impl(const ProjLaunch& a, hipStream_t st, void* h) {
-  constexpr bool BF = sizeof(IO) == 2;
+hipError_t forward_impl(const ProjLaunch& a, hipStream_t st) {
   long off = 0;
   OutJobs out{};
   out.n = a.n_proj;
@@ -528,9 +524,8 @@ hipError_t forward_impl(const ProjLaunch& a, hipStream_t st, void* h) {
       GL_CHECK(launch_wide_fwd(WideFwd{a.x, s.w, a.yf + off, a.T, a.in, s.out}, st));
       off += (long)a.T * s.out;
     } else {
-      // Yf_p = X W_p^T
-      GL_CHECK(blas_gemm(h, BF, false, true, a.T, s.out, a.in, 1.0f, a.x, a.in, s.w, a.in, 0.0f,
-                         a.yf + off, s.out, st));
+      // Yf_p = X W_p^T on the generic GEMM
+      GL_CHECK(launch_generic_fwd(WideFwd{a.x, s.w, a.yf + off, a.T, a.in, s.out}, a.io_bf16, st));
       off += (long)a.T * s.out;
     }
   }
@@ -549,38 +544,31 @@ hipError_t forward_impl(const ProjLaunch& a, hipStream_t st, void* h) {
 }
 
 template <typename IO>
-hipError_t backward_impl(const ProjLaunch& a, hipStream_t st, void* h) {
-  constexpr bool BF = sizeof(IO) == 2;
-  // dXf = sum_p dY_p W_p: the wide projections (own wide GEMM, one launch
-  // over all of them, then hipBLASLt for any other) into dxf, the narrow
-  // ones into the buffer after it; lowrank_out adds the two
+hipError_t backward_impl(const ProjLaunch& a, hipStream_t st) {
+  // dXf = sum_p dY_p W_p: the wide projections (one launch over all of
+  // them), then the generic ones (one launch, adding to the wide sum) into
+  // dxf, the narrow ones into the buffer after it; lowrank_out adds the two
   NarrowBwd nb{};
   nb.T = a.T;
   nb.K = a.in;
   nb.c = a.dxf + (long)a.T * a.in;
-  WideBwd wb{};
-  wb.c = a.dxf;
-  wb.T = a.T;
-  wb.K = a.in;
+  WideBwd wb{}, gb{};
+  wb.c = gb.c = a.dxf;
+  wb.T = gb.T = a.T;
+  wb.K = gb.K = a.in;
   for (int p = 0; p < a.n_proj; ++p) {
     const ProjSpec& s = a.p[p];
     if (is_narrow(a, p))
       nb.j[nb.n++] = NarrowJob{s.w, s.dy, nullptr, s.out, 0};
     else if (is_wide(a, p))
       wb.j[wb.n++] = WideJob{s.w, s.dy, s.out};
+    else
+      gb.j[gb.n++] = WideJob{s.w, s.dy, s.out};
   }
-  int wide = 0;  // products written into dxf so far
-  if (wb.n > 0) {
-    GL_CHECK(launch_wide_bwd(wb, st));
-    wide = wb.n;
-  }
-  for (int p = 0; p < a.n_proj; ++p) {
-    const ProjSpec& s = a.p[p];
-    if (is_narrow(a, p) || is_wide(a, p)) continue;
-    GL_CHECK(blas_gemm(h, BF, false, false, a.T, a.in, s.out, 1.0f, s.dy, s.out, s.w, a.in,
-                       wide == 0 ? 0.0f : 1.0f, a.dxf, a.in, st));
-    ++wide;
-  }
+  if (wb.n > 0) GL_CHECK(launch_wide_bwd(wb, st));
+  gb.accumulate = wb.n > 0;
+  if (gb.n > 0) GL_CHECK(launch_generic_bwd(gb, a.io_bf16, st));
+  const int wide = wb.n + gb.n;  // products written into dxf
   if (nb.n > 0) GL_CHECK(launch_narrow_bwd(nb, st));
   // dL_p = dY_p B_p^T, and L_p = X A_p where grad_B_p is wanted
   const RowsPlan plan = rows_plan(a, true);
@@ -654,18 +642,12 @@ ProjScratchNeed proj_scratch_need(const ProjLaunch& a, bool backward) {
   return need;
 }
 
-bool proj_needs_blas(const ProjLaunch& a) {
-  for (int p = 0; p < a.n_proj; ++p)
-    if (!is_narrow(a, p) && !is_wide(a, p)) return true;
-  return false;
+hipError_t launch_proj_forward(const ProjLaunch& a, hipStream_t st) {
+  return a.io_bf16 ? forward_impl<bf16>(a, st) : forward_impl<float>(a, st);
 }
 
-hipError_t launch_proj_forward(const ProjLaunch& a, hipStream_t st, void* blas) {
-  return a.io_bf16 ? forward_impl<bf16>(a, st, blas) : forward_impl<float>(a, st, blas);
-}
-
-hipError_t launch_proj_backward(const ProjLaunch& a, hipStream_t st, void* blas) {
-  return a.io_bf16 ? backward_impl<bf16>(a, st, blas) : backward_impl<float>(a, st, blas);
+hipError_t launch_proj_backward(const ProjLaunch& a, hipStream_t st) {
+  return a.io_bf16 ? backward_impl<bf16>(a, st) : backward_impl<float>(a, st);
 }
 
 }  // namespace glacier
