@@ -589,21 +589,34 @@ __device__ inline void b4_dkdv(const TileDesc td, const bf16* __restrict__ q_rot
   __syncthreads();
   {
     // slot (j4 = 4 db + qq, source lane sl) of region w holds elements
-    // d = 32 db + 8 qq + 4 (sl / 32) .. + 3 of key sl % 32 of key quarter w % 4
+    // d = 32 db + 8 qq + 4 (sl / 32) .. + 3 of key sl % 32 of key quarter w % 4;
+    // a thread's pieces are read in batches of eight, one wait per batch
     constexpr int NSLOT = 4 * NDB * 64;
-    for (int i2 = threadIdx.x; i2 < kW3 * NSLOT; i2 += kNT3) {
-      const int wr = i2 / NSLOT, j = i2 % NSLOT;
-      const int kqr = wr & 3, rr = wr >> 2;
-      const int j4 = j >> 6, sl = j & 63;
-      const int db = j4 >> 2, qq = j4 & 3;
-      f32x4 a = lds4(sbase + static_cast<unsigned>(wr * L::REG + j * 16));
+    constexpr int NIT = kW3 * NSLOT / kNT3, NB = 8;
+    static_assert(NIT % NB == 0, "epilogue batches");
+#pragma unroll
+    for (int b0 = 0; b0 < NIT; b0 += NB) {
+      f32x4 a[NB];
+#pragma unroll
+      for (int t = 0; t < NB; ++t) {
+        const int i2 = threadIdx.x + kNT3 * (b0 + t);
+        a[t] = lds4(sbase + static_cast<unsigned>((i2 / NSLOT) * L::REG + (i2 % NSLOT) * 16));
+      }
       lgkm<0>();
-      tie_v(a);
-      const int key = k0 + 32 * kqr + (sl & 31);
-      const int d0 = 32 * db + 8 * qq + 4 * (sl >> 5);
-      bf16* dst = rr == 0 ? wv : wk;
-      if (key < td.len)
-        store4(dst + ((long)(td.tok0 + key) * n_heads_q + h) * D + d0, rr == 0 ? a : a * scale);
+#pragma unroll
+      for (int t = 0; t < NB; ++t) {
+        tie_v(a[t]);
+        const int i2 = threadIdx.x + kNT3 * (b0 + t);
+        const int wr = i2 / NSLOT, j = i2 % NSLOT;
+        const int kqr = wr & 3, rr = wr >> 2;
+        const int j4 = j >> 6, sl = j & 63;
+        const int db = j4 >> 2, qq = j4 & 3;
+        const int key = k0 + 32 * kqr + (sl & 31);
+        const int d0 = 32 * db + 8 * qq + 4 * (sl >> 5);
+        bf16* dst = rr == 0 ? wv : wk;
+        if (key < td.len)
+          store4(dst + ((long)(td.tok0 + key) * n_heads_q + h) * D + d0, rr == 0 ? a[t] : a[t] * scale);
+      }
     }
   }
   GL_STAMP(kKernBwd, 22);
@@ -811,19 +824,37 @@ __device__ inline void b4_dq(const TileDesc td, const bf16* __restrict__ q_rot,
   for (int k = (mych > 0 ? mych : 1); k < nch; ++k) wg_barrier();
   GL_STAMP(kKernBwd, 20);
 
-  fence16(acc);
-  __syncthreads();
   // Merge: every wave writes its sums into region (key group, query
   // quarter); then all threads add the two key groups of each element in
   // group order, scale, apply the inverse RoPE at the query's position and
   // store rows of dq.  A thread takes elements d0 .. d0 + 3 and d0 + D/2 ..
   // (the rotation pairs: column block db and db + NDB/2 of one slot) of one
-  // query.
+  // query, NIT such pieces; their cos/sin are loaded first, so that those
+  // loads (and the position lookups before them) run beside the merge.
+  constexpr int NHALF = 2 * NDB * 64;  // slots of column blocks 0 .. NDB/2 - 1
+  constexpr int NIT = 4 * NHALF / kNT3;
+  static_assert(NIT * kNT3 == 4 * NHALF, "epilogue pieces");
+  f32x4 pcs[NIT], psn[NIT];
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+    const int i2 = threadIdx.x + kNT3 * it;
+    const int qqr = i2 / NHALF, j = i2 % NHALF;
+    const int j4 = j >> 6, sl = j & 63;
+    const int db = j4 >> 2, qp = j4 & 3;
+    const int qi2 = min(q0t + 32 * qqr + (sl & 31), td.len - 1);
+    const int d0 = 32 * db + 8 * qp + 4 * (sl >> 5);
+    const long pos = pos_of != nullptr ? pos_of[td.tok0 + qi2] : qi2;
+    pcs[it] = *reinterpret_cast<const f32x4*>(cos_t + pos * H + d0);
+    psn[it] = *reinterpret_cast<const f32x4*>(sin_t + pos * H + d0);
+  }
+  fence16(acc);
+  __syncthreads();
   write_accs(sbase + static_cast<unsigned>((kg * 4 + qq) * L::REG + lane * 16), acc);
   lgkm<0>();
   __syncthreads();
-  constexpr int NHALF = 2 * NDB * 64;  // slots of column blocks 0 .. NDB/2 - 1
-  for (int i2 = threadIdx.x; i2 < 4 * NHALF; i2 += kNT3) {
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+    const int i2 = threadIdx.x + kNT3 * it;
     const int qqr = i2 / NHALF, j = i2 % NHALF;
     const int j4 = j >> 6, sl = j & 63;
     const int db = j4 >> 2, qp = j4 & 3;
@@ -843,9 +874,7 @@ __device__ inline void b4_dq(const TileDesc td, const bf16* __restrict__ q_rot,
     const int qi2 = q0t + 32 * qqr + (sl & 31);
     const int d0 = 32 * db + 8 * qp + 4 * (sl >> 5);  // elements d0 .. d0 + 3 and H + d0 ..
     if (qi2 < td.len) {
-      const long pos = pos_of != nullptr ? pos_of[td.tok0 + qi2] : qi2;
-      const f32x4 cs = *reinterpret_cast<const f32x4*>(cos_t + pos * H + d0);
-      const f32x4 sn = *reinterpret_cast<const f32x4*>(sin_t + pos * H + d0);
+      const f32x4 cs = pcs[it], sn = psn[it];
       const f32x4 a = lo0 * scale, b = hi0 * scale;
       f32x4 y0, y1;
 #pragma unroll
