@@ -1084,11 +1084,9 @@ hipError_t backward_impl(const BwdLaunch& a, hipStream_t st, KernelTimer* tm) {
   bool rows32 = false, mfma32 = false;
   if constexpr (std::is_same<IO, bf16>::value && (D == 64 || D == 128)) {
     const long long min_wide = D == 128 ? kBwdMfma32MinPairsD128 : kBwdMfma32MinPairsD64;
-    const long long min_rows32 = D == 128 ? kBwdRows32MinPairsD128 : kBwdRows32MinPairsD64;
-    const bool wide = a.tiles_wide != nullptr;
-    mfma32 = wide && (a.variant == kBwdMfma32 || (a.variant == kBwdAuto && a.pairs >= min_wide));
-    rows32 = !mfma32 && (a.variant == kBwdRows32 ||
-                         (a.variant != kBwdRows16 && !wide && a.pairs >= min_rows32));
+    mfma32 = a.tiles_wide != nullptr &&
+             (a.variant == kBwdMfma32 || (a.variant == kBwdAuto && a.pairs >= min_wide));
+    rows32 = !mfma32 && a.variant == kBwdRows32;
   }
   if (mfma32) {
     // bf16 tensors: the 32x32x16-MFMA kernel (attn_bwd3.hip)

@@ -156,14 +156,11 @@ struct FwdLaunch {
 // kernel (attn_bwd3.hip) once a head's causal pair count reaches the measured
 // break-even below, the 16-row-wave kernel (attn_kernels.hip) under it: the
 // wide kernel's extra row-stats launch and larger per-workgroup fixed costs
-// only pay off on long sequences.  Where the 128-row tile table is absent
-// (the allocation-free entry point) the 32-row-wave kernel (attn_bwd.hip)
-// takes the long sequences instead, from its own break-even.
+// only pay off on long sequences.  The 32-row-wave kernel (attn_bwd.hip),
+// slower than the wide one at every length measured, runs only when pinned.
 enum BwdVariant : int { kBwdAuto = 0, kBwdRows16 = 1, kBwdRows32 = 2, kBwdMfma32 = 3 };
 constexpr long long kBwdMfma32MinPairsD128 = 1024LL * 1025 / 2;  // one S=1024 sequence
 constexpr long long kBwdMfma32MinPairsD64 = 2048LL * 2049 / 2;   // one S=2048 sequence
-constexpr long long kBwdRows32MinPairsD128 = 1664LL * 1665 / 2;  // one S=1664 sequence
-constexpr long long kBwdRows32MinPairsD64 = 2048LL * 2049 / 2;   // one S=2048 sequence
 
 struct BwdLaunch {
   int precision;

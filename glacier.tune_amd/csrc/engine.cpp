@@ -165,6 +165,9 @@ constexpr int kNoAllocMaxTokens = GLACIER_ATTN_MAX_SEQ_LEN;
 constexpr int kNoAllocMaxTiles = kNoAllocMaxTokens / kTile + kNoAllocMaxSeqs;
 constexpr int kNoAllocMaxCost = 63 + 16 * (kNoAllocMaxTokens / kTile);
 constexpr int kNoAllocMaxSplitEntries = 4096;  // a split table fits the CUs: far fewer
+// the 128-row table of the wide backward: two entries per 128-row tile
+constexpr int kNoAllocMaxWideEntries = 2 * (kNoAllocMaxTokens / kWideTile + kNoAllocMaxSeqs);
+constexpr int kNoAllocMaxWideCost = 50 + 12 * ((kNoAllocMaxTokens + 31) / 32 + 1);
 constexpr int kNoAllocRopeChunk = 16384;  // floats staged per table upload
 
 // What one device's scratch holds across calls: the RoPE tables and the tile
@@ -173,15 +176,15 @@ struct NoAllocResident {
   int rope_cap = 0, rope_dim = 0;
   float rope_base = 0.0f;
   size_t tiles_off = 0;  // 0: no tile table resident
-  int n_seqs = 0, total_tokens = 0, split = 0;
+  int n_seqs = 0, total_tokens = 0, split = 0, n_wide = 0;
   int32_t cu[kNoAllocMaxSeqs + 1] = {};
 };
 
 std::mutex g_noalloc_mutex;  // guards the records and host staging below
 NoAllocResident g_noalloc[kNoAllocMaxDevices];
-TileDesc g_noalloc_tiles[2 * kNoAllocMaxTiles + kNoAllocMaxSplitEntries];
+TileDesc g_noalloc_tiles[2 * kNoAllocMaxTiles + kNoAllocMaxSplitEntries + kNoAllocMaxWideEntries];
 int32_t g_noalloc_pos[kNoAllocMaxTokens];
-int32_t g_noalloc_count[kNoAllocMaxCost + 2];
+int32_t g_noalloc_count[(kNoAllocMaxCost > kNoAllocMaxWideCost ? kNoAllocMaxCost : kNoAllocMaxWideCost) + 2];
 float g_noalloc_freq[512];  // head_dim / 2 (head_dim <= 1024, make_shape_args)
 float g_noalloc_stage[kNoAllocRopeChunk];
 
@@ -193,6 +196,8 @@ struct NoAllocBwd {
   int split, n_split_entries;  // split dK/dV tiles (split > 0): their table and partials
   const TileDesc* tiles_split;
   void *wk2, *wv2;
+  const TileDesc* tiles_wide;  // the wide backward's table (null: not built)
+  int n_wide_entries;
   const int32_t* pos_of;
   const float *cos_t, *sin_t;
   int n_tiles;
@@ -200,7 +205,8 @@ struct NoAllocBwd {
 };
 
 // Lays out one backward call inside the scratch at `base` on `device`:
-//   [cos table][sin table][dK/dV + dQ tile table, then the split table][positions][row stats]
+//   [cos table][sin table][dK/dV + dQ tile table, the split table, the wide table][positions]
+//   [row stats]
 //   [dK partials][dV partials][second-half dK partials][second-half dV partials]
 // (each region 256-byte aligned; the split regions only when the call splits
 // dK/dV tiles, by the rule of the allocating backward: bwd_split_of with the
@@ -241,7 +247,12 @@ NoAllocBwd noalloc_bwd_workspace(int device, void* base, const ShapeArgs& s, int
   const int rope_cap = rope_ok ? r.rope_cap : (std::max(s.max_len, 1) + 255) / 256 * 256;
   const size_t rope_bytes = align256(static_cast<size_t>(rope_cap) * half * sizeof(float));
   const size_t off_tiles = 2 * rope_bytes;
-  const size_t n_entries = 2 * static_cast<size_t>(n_tiles) + n_split_entries;
+  // the wide backward's table, for the tensors and head sizes it takes
+  int n_wide = 0;
+  if (s.io_bf16 && (s.head_dim == 64 || s.head_dim == 128))
+    for (int b = 0; b < s.n_seqs; ++b)
+      n_wide += 2 * ((s.seq_start(b + 1) - s.seq_start(b) + kWideTile - 1) / kWideTile);
+  const size_t n_entries = 2 * static_cast<size_t>(n_tiles) + n_split_entries + n_wide;
   const size_t off_pos = off_tiles + align256(n_entries * sizeof(TileDesc));
   const size_t off_stats = off_pos + align256(T * sizeof(int32_t));
   const size_t stats_bytes = s.io_bf16 ? align256((T * Hq + 64) * 2 * sizeof(float)) : 0;
@@ -255,7 +266,7 @@ NoAllocBwd noalloc_bwd_workspace(int device, void* base, const ShapeArgs& s, int
              " bytes of scratch for this call; its fixed scratch holds " +
              std::to_string(kNoAllocScratchBytes) + " (GLACIER_ATTN_NOALLOC_SCRATCH_BYTES)");
   bool tiles_ok = r.tiles_off == off_tiles && r.n_seqs == s.n_seqs &&
-                  r.total_tokens == s.total_tokens && r.split == split;
+                  r.total_tokens == s.total_tokens && r.split == split && r.n_wide == n_wide;
   for (int b = 0; tiles_ok && b <= s.n_seqs; ++b) tiles_ok = r.cu[b] == s.seq_start(b);
   char* const sb = static_cast<char*>(base);
   if (!rope_ok || !tiles_ok) {
@@ -330,6 +341,28 @@ NoAllocBwd noalloc_bwd_workspace(int device, void* base, const ShapeArgs& s, int
           });
         }
       }
+      if (n_wide > 0) {
+        // the wide table: the same stable counting sort by bwd_wide_cost
+        TileDesc* const out = g_noalloc_tiles + 2 * n_tiles + n_split_entries;
+        std::fill(g_noalloc_count, g_noalloc_count + kNoAllocMaxWideCost + 2, 0);
+        for (int b = 0; b < s.n_seqs; ++b) {
+          const int len = s.seq_start(b + 1) - s.seq_start(b);
+          for (int t = 0; t < (len + kWideTile - 1) / kWideTile; ++t)
+            for (int kind = 0; kind < 2; ++kind) ++g_noalloc_count[bwd_wide_cost(len, t, kind)];
+        }
+        int at = 0;
+        for (int c = kNoAllocMaxWideCost; c >= 0; --c) {
+          const int n = g_noalloc_count[c];
+          g_noalloc_count[c] = at;
+          at += n;
+        }
+        for (int b = 0; b < s.n_seqs; ++b) {
+          const int tok0 = s.seq_start(b), len = s.seq_start(b + 1) - tok0;
+          for (int t = 0; t < (len + kWideTile - 1) / kWideTile; ++t)
+            for (int kind = 0; kind < 2; ++kind)
+              out[g_noalloc_count[bwd_wide_cost(len, t, kind)]++] = TileDesc{tok0, len, t, kind};
+        }
+      }
       check_hip(hipMemcpy(sb + off_tiles, g_noalloc_tiles, n_entries * sizeof(TileDesc),
                           hipMemcpyHostToDevice),
                 "allocation-free backward: tile table upload");
@@ -338,6 +371,7 @@ NoAllocBwd noalloc_bwd_workspace(int device, void* base, const ShapeArgs& s, int
       r.n_seqs = s.n_seqs;
       r.total_tokens = s.total_tokens;
       r.split = split;
+      r.n_wide = n_wide;
       for (int b = 0; b <= s.n_seqs; ++b) r.cu[b] = s.seq_start(b);
       r.tiles_off = off_tiles;
     }
@@ -355,6 +389,8 @@ NoAllocBwd noalloc_bwd_workspace(int device, void* base, const ShapeArgs& s, int
   w.tiles_split = split > 0 ? w.tiles_bwd + 2 * n_tiles : nullptr;
   w.wk2 = split > 0 ? sb + off_wk2 : nullptr;
   w.wv2 = split > 0 ? sb + off_wv2 : nullptr;
+  w.tiles_wide = n_wide > 0 ? w.tiles_bwd + 2 * n_tiles + n_split_entries : nullptr;
+  w.n_wide_entries = n_wide;
   w.n_tiles = n_tiles;
   w.pairs = pairs;
   return w;
@@ -582,6 +618,8 @@ class GpuAttentionEngine {
     a.tiles_split = w.tiles_split;
     a.wk2 = w.wk2;
     a.wv2 = w.wv2;
+    a.tiles_wide = w.tiles_wide;
+    a.n_wide_entries = w.n_wide_entries;
     a.pos_of = w.pos_of;
     a.cos_t = w.cos_t;
     a.sin_t = w.sin_t;

@@ -173,7 +173,10 @@ int glacier_attn_backward(glacier_attn_ctx *ctx, const glacier_attn_desc *desc,
  * fixed device array of GLACIER_ATTN_NOALLOC_SCRATCH_BYTES per GPU, laid
  * out per call as (each part rounded up to 256 bytes)
  *   RoPE cos and sin tables    2 x 4 * ceil_256(L) * D/2   (L: longest sequence)
- *   tile and position tables   32 * tiles + 4 * T          (tiles: sum of ceil(len/64))
+ *   tile and position tables   32 * tiles + 32 * wtiles + 4 * T
+ *                              (tiles: sum of ceil(len/64); wtiles: sum of
+ *                              ceil(len/128) for bf16 tensors at head_dim 64
+ *                              or 128, else 0)
  *   row stats (bf16 tensors)   8 * (T * Hq + 64)
  *   dK and dV partials         2 x esz * T * Hq * D        (esz 2 bf16, 4 fp32 tensors)
  * A call that needs more, or has more than 1024 sequences or 65536 tokens,

@@ -93,6 +93,33 @@ def test_noalloc_backward_matches_backward_bitwise(kernel, precision, dtype):
         eng.close()
 
 
+# long sequences of bf16 tensors: both entry points take the wide backward
+# (128-row tiles from the scratch's own table); two calls, the second smaller
+CALLS_LONG = [
+    ([1100, 7], 14, 2, 128, 1.0e6),
+    ([2050], 4, 1, 64, 1.0e4),
+]
+
+
+@pytest.mark.parametrize("kernel", ["auto", "mfma32"])
+def test_noalloc_backward_long_sequences_match_backward_bitwise(kernel):
+    eng = _engine(kernel, ga.PREC_BF16)
+    try:
+        for i, (lens, hq, hkv, d, base) in enumerate(CALLS_LONG):
+            _say(f"[noalloc long] {kernel} call {i}: lens={lens} Hq={hq} Hkv={hkv} D={d}")
+            q, k, v, dO, cu = _inputs(lens, hq, hkv, d, torch.bfloat16, 60 + i)
+            out, lse, q_rot, k_rot = eng.forward(q, k, v, base, cu_seqlens=cu)
+            ref = eng.backward(dO, q_rot, k_rot, v, out, lse, base, cu_seqlens=cu)
+            got = [torch.full_like(t, float("nan")) for t in ref]
+            rc = backward_noalloc(eng, dO, q_rot, k_rot, v, out, lse, base, ga.PREC_BF16, cu, *got)
+            assert rc == ga.OK, ga.load().glacier_attn_last_error()
+            torch.cuda.synchronize()
+            for name, a, b in zip(("dq", "dk", "dv"), ref, got):
+                assert torch.equal(a, b), name
+    finally:
+        eng.close()
+
+
 def test_noalloc_backward_allocates_no_device_memory():
     """A fresh context: the allocation-free call leaves the device's free
     memory where it was (the same call through glacier_attn_backward would
