@@ -69,11 +69,11 @@ __device__ inline void wait_kfrags(bf16x8 (&t)[2][2]) {
 // accumulators (24 >= the 18 a 16-pass MFMA result needs); every
 // accumulator is tied through a volatile asm after the wait, so no access
 // moves above it.
-template <int NDB>
-__device__ inline void fence_acc(f32x4 (&o)[NDB][4], f32x4 (&l)[4]) {
+template <int NDB, int QB>
+__device__ inline void fence_acc(f32x4 (&o)[NDB][QB], f32x4 (&l)[QB]) {
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
 #pragma unroll
-  for (int qb = 0; qb < 4; ++qb) {
+  for (int qb = 0; qb < QB; ++qb) {
     asm volatile("" : "+a"(l[qb]));
 #pragma unroll
     for (int db = 0; db < NDB; ++db) asm volatile("" : "+a"(o[db][qb]));
@@ -81,18 +81,22 @@ __device__ inline void fence_acc(f32x4 (&o)[NDB][4], f32x4 (&l)[4]) {
 }
 
 // the NDB 16-byte pieces of block qb of the accumulators at addr + 64 db
-template <int NDB, int... DB>
-__device__ inline void write_acc_block(unsigned addr, const f32x4 (&o)[NDB][4], int qb,
+template <int NDB, int QB, int... DB>
+__device__ inline void write_acc_block(unsigned addr, const f32x4 (&o)[NDB][QB], int qb,
                                        std::integer_sequence<int, DB...>) {
   (write_acc<64 * DB>(addr, o[DB][qb]), ...);
 }
 
-template <typename IO, int D, bool VARLEN>
+// The arguments the first loads need come first: the 14 dwords up to cos_t
+// arrive preloaded in SGPRs (-amdgpu-kernarg-preload-count, build.py), so the
+// K/V and Q loads issue without waiting for the kernarg segment.  The sine
+// table starts sin_off floats after the cosine table.
+template <typename IO, int D, bool VARLEN, int QB>
 __global__ __launch_bounds__(kFwdWaves * 64) void attn_fwd_kernel_ks(
-    const IO* __restrict__ q, const bf16* __restrict__ kc, const bf16* __restrict__ v,
-    IO* __restrict__ out, float* __restrict__ lse, IO* __restrict__ q_rot,
-    const TileDesc* __restrict__ tiles, int n_tiles, int total_tokens,
-    float scale_log2, const float* __restrict__ cos_t, const float* __restrict__ sin_t) {
+    int total_tokens, int n_heads_kv, int group, int sin_off, const bf16* __restrict__ kc,
+    const bf16* __restrict__ v, const TileDesc* __restrict__ tiles, const IO* __restrict__ q,
+    const float* __restrict__ cos_t, IO* __restrict__ out, float* __restrict__ lse,
+    IO* __restrict__ q_rot, float scale_log2) {
   using M = Mfma<bf16>;
   using F = FwdLayout<D>;
   using Frag = M::Frag;
@@ -100,23 +104,30 @@ __global__ __launch_bounds__(kFwdWaves * 64) void attn_fwd_kernel_ks(
   constexpr int NDB = D / 16;
   constexpr int H = D / 2;
   constexpr int NT = kFwdWaves * 64;
+  static_assert(QB == 4 || QB == 2, "16-query blocks per workgroup");
+  constexpr int TR = 16 * QB;       // query rows of the workgroup
+  constexpr int NSUB = kTile / TR;  // workgroups per 64-row table entry
   constexpr int NDMA = 2 * (kChunk * D / 512);  // DMA instructions per chunk (K and V)
   static_assert(NDMA < 64, "vmcnt range");
   constexpr unsigned SLOT = F::CHUNK * sizeof(bf16);  // bytes of one ring slot
   extern __shared__ __align__(16) unsigned char smem_raw[];
   bf16* const lds = reinterpret_cast<bf16*>(smem_raw);  // [wave][K ring, V ring], Q
 
-  // grid (query heads per KV head, KV heads, tiles): no integer division
-  const int n_heads_kv = gridDim.y, n_heads_q = gridDim.x * gridDim.y;
-  const int kvh = blockIdx.y, h = kvh * gridDim.x + blockIdx.x;
-  const TileDesc td = VARLEN ? tiles[blockIdx.z]
-                             : TileDesc{0, total_tokens, n_tiles - 1 - (int)blockIdx.z, 0};
+  // grid (group = query heads per KV head, KV heads, tiles): no integer division
+  const int n_heads_q = group * n_heads_kv;
+  const int kvh = blockIdx.y, h = kvh * group + blockIdx.x;
+  const float* const sin_t = cos_t + sin_off;
+  // the rows of an entry's later part see more keys and start first
+  const int entry = (int)blockIdx.z / NSUB, sub = NSUB - 1 - (int)blockIdx.z % NSUB;
+  const TileDesc td =
+      VARLEN ? tiles[entry] : TileDesc{0, total_tokens, (total_tokens + kTile - 1) / kTile - 1 - entry, 0};
   const int tid = threadIdx.x, w = wave_id(), lane = tid & 63;
   GL_STAMP(kKernFwd, 0);
-  GL_STAMP_VALUE(kKernFwd, 31, td.tile);
   const int g = lane >> 4, c = lane & 15;
-  const int q0 = kTile * td.tile;          // the tile's first query position
-  const int nq = min(kTile, td.len - q0);  // its valid queries
+  const int q0 = kTile * td.tile + TR * sub;  // the workgroup's first query position
+  const int nq = min(TR, td.len - q0);        // its valid queries
+  if (nq <= 0) return;  // the part of a short last tile past the sequence's end
+  GL_STAMP_VALUE(kKernFwd, 31, q0 / TR);
   const int nch = (q0 + nq + kChunk - 1) / kChunk;  // key chunks of the causal range
   const int nit = __builtin_amdgcn_readfirstlane(nch > w ? (nch - w + kFwdWaves - 1) / kFwdWaves : 0);
   // This wave's LDS: a two-slot ring of K chunks, then one of V chunks
@@ -124,6 +135,42 @@ __global__ __launch_bounds__(kFwdWaves * 64) void attn_fwd_kernel_ks(
   // V of chunk i, so the rings refill at different points of an iteration.
   bf16* const kring = lds + w * F::WAVE;
   bf16* const vring = kring + 2 * F::CHUNK;
+
+  // Q: the workgroup's rows are loaded by all threads (coalesced, 8 rotation
+  // pairs per thread), rotated in fp32 (rope_fwd) and rounded to bf16,
+  // written to LDS (swizzled), from where every wave reads the operand
+  // fragments of all TR queries, and later to q_rot as whole rows.  Their
+  // loads issue ahead of the K/V DMA: loads return in order, and Q is
+  // needed first.
+  bf16* const qst = lds + kFwdWaves * F::WAVE;
+  constexpr int PPR = H / 8;                // 8-pair pieces per row
+  constexpr int QP = TR * PPR;              // pieces of the rows
+  constexpr int QI = (QP + NT - 1) / NT;    // pieces per thread
+  // Q pieces as loaded (bf16 rows stay packed until the rotation, so that
+  // no conversion waits for them before the DMA has issued)
+  using QRaw = std::conditional_t<std::is_same_v<IO, bf16>, bf16x8, float[8]>;
+  QRaw qx[QI][2];
+  float qc[QI][8], qs[QI][8];
+  auto load_raw = [](const IO* p, QRaw& x) {
+    if constexpr (std::is_same_v<IO, bf16>)
+      x = *reinterpret_cast<const bf16x8*>(p);
+    else
+      load8(p, x);
+  };
+  const long qrow0 = (long)td.tok0 + q0;
+#pragma unroll
+  for (int n = 0; n < QI; ++n) {
+    const int idx = tid + n * NT;
+    if (QP % NT != 0 && idx >= QP) break;
+    const int r = idx / PPR, j = idx % PPR;
+    const int rr = r < nq ? r : 0;  // rows past the sequence load row 0, rotate zeros
+    const long gq = ((qrow0 + rr) * n_heads_q + h) * D + 8 * j;
+    load_raw(q + gq, qx[n][0]);
+    load_raw(q + gq + H, qx[n][1]);
+    const long ti = (long)(q0 + rr) * H + 8 * j;
+    load8(cos_t + ti, qc[n]);
+    load8(sin_t + ti, qs[n]);
+  }
 
   const long kvstride = (long)n_heads_kv * D;
   const bf16* kbase = kc + ((long)td.tok0 * n_heads_kv + kvh) * D;
@@ -146,43 +193,30 @@ __global__ __launch_bounds__(kFwdWaves * 64) void attn_fwd_kernel_ks(
     dma_k(1);
     dma_v(1);
   }
+  GL_STAMP(kKernFwd, 23);
 
-  // Q: the tile's rows are loaded by all threads (coalesced, 8 rotation pairs
-  // per thread), rotated in fp32 (rope_fwd) and rounded to bf16, written to
-  // LDS (swizzled), from where every wave reads the operand fragments of all
-  // 64 queries, and later to q_rot as whole rows.
-  bf16* const qst = lds + kFwdWaves * F::WAVE;
-  constexpr int PPR = H / 8;            // 8-pair pieces per row
-  constexpr int QI = kTile * PPR / NT;  // pieces per thread
-  static_assert(QI * NT == kTile * PPR, "Q tile must split evenly");
   float qy[QI][2][8];
-  const long qrow0 = (long)td.tok0 + q0;
 #pragma unroll
   for (int n = 0; n < QI; ++n) {
     const int idx = tid + n * NT;
+    if (QP % NT != 0 && idx >= QP) break;
     const int r = idx / PPR, j = idx % PPR;
     const bool valid = r < nq;
-    const long gq = ((qrow0 + (valid ? r : 0)) * n_heads_q + h) * D + 8 * j;
-    float x0[8], x1[8], cs[8], sn[8];
-    load8(q + gq, x0);
-    load8(q + gq + H, x1);
-    const long ti = (long)(q0 + (valid ? r : 0)) * H + 8 * j;
-    load8(cos_t + ti, cs);
-    load8(sin_t + ti, sn);
 #pragma unroll
     for (int e = 0; e < 8; ++e)
-      rope_fwd(valid ? x0[e] : 0.0f, valid ? x1[e] : 0.0f, cs[e], sn[e], qy[n][0][e], qy[n][1][e]);
+      rope_fwd(valid ? (float)qx[n][0][e] : 0.0f, valid ? (float)qx[n][1][e] : 0.0f, qc[n][e], qs[n][e],
+               qy[n][0][e], qy[n][1][e]);
     const int sw = swz<D>(r);
     store8(qst + r * D + 8 * (j ^ sw), qy[n][0]);
     store8(qst + r * D + 8 * ((PPR + j) ^ sw), qy[n][1]);
   }
   GL_STAMP(kKernFwd, 1);
   __syncthreads();
-  Frag qf[4][NKD];
+  Frag qf[QB][NKD];
   {
     const int sq = swz<D>(c);  // rows 16 qb + c
 #pragma unroll
-    for (int qb = 0; qb < 4; ++qb)
+    for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
       for (int kk = 0; kk < NKD; ++kk)
         qf[qb][kk] = *reinterpret_cast<const bf16x8*>(qst + (16 * qb + c) * D + 8 * ((4 * kk + g) ^ sq));
@@ -210,10 +244,10 @@ __global__ __launch_bounds__(kFwdWaves * 64) void attn_fwd_kernel_ks(
 
   // O^T accumulators and per-query row sums (MFMA accumulators pinned in
   // AGPRs), the reference maxima the probabilities are taken against.
-  f32x4 o[NDB][4], lsum[4];
-  float m_ref[4], m_seen[4];
+  f32x4 o[NDB][QB], lsum[QB];
+  float m_ref[QB], m_seen[QB];
 #pragma unroll
-  for (int qb = 0; qb < 4; ++qb) {
+  for (int qb = 0; qb < QB; ++qb) {
     // a wave without chunks merges as (kNegBig, 0, 0)
     m_ref[qb] = kNegBig;
     m_seen[qb] = kNegBig;
@@ -229,7 +263,7 @@ __global__ __launch_bounds__(kFwdWaves * 64) void attn_fwd_kernel_ks(
   // i + 1 may reach the diagonal (only a wave's last chunk can).  FETCH:
   // chunk i + 2 exists; its K goes into K(i)'s slot at the start, its V into
   // V(i)'s at the end.  On entry K(i + 1) and V(i) are in LDS or in flight.
-  f32x4 sc[2][4];
+  f32x4 sc[2][QB];
   auto iteration = [&](int i, auto more, auto mask, auto fetch) {
     constexpr bool MORE = decltype(more)::value;
     constexpr bool MASK = decltype(mask)::value;
@@ -257,23 +291,23 @@ __global__ __launch_bounds__(kFwdWaves * 64) void attn_fwd_kernel_ks(
       vt[2 * db] = read_tr_async<0>(vaddr[db] + vslot);
       vt[2 * db + 1] = read_tr_async<32 * D>(vaddr[db] + vslot);
     }
-    f32x4 sn[2][4];
+    f32x4 sn[2][QB];
     if constexpr (MORE) {
       wait_kfrags<(2 * NDB < 15 ? 2 * NDB : 15)>(kf);
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int qb = 0; qb < 4; ++qb) sn[kb][qb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int qb = 0; qb < QB; ++qb) sn[kb][qb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int kk = 0; kk < NKD; ++kk)
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-          for (int qb = 0; qb < 4; ++qb) sn[kb][qb] = M::mma(kf[kk][kb], qf[qb][kk], sn[kb][qb]);
+          for (int qb = 0; qb < QB; ++qb) sn[kb][qb] = M::mma(kf[kk][kb], qf[qb][kk], sn[kb][qb]);
     }
-    bf16x8 pb[4];
+    bf16x8 pb[QB];
 #pragma unroll
-    for (int qb = 0; qb < 4; ++qb)
+    for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -282,7 +316,7 @@ __global__ __launch_bounds__(kFwdWaves * 64) void attn_fwd_kernel_ks(
               (bf16)__builtin_amdgcn_exp2f(__builtin_fmaf(sc[kb][qb][r], scale_log2, -m_ref[qb]));
     wait_tr(vt);
 #pragma unroll
-    for (int qb = 0; qb < 4; ++qb) mma_acc(lsum[qb], ones, pb[qb]);
+    for (int qb = 0; qb < QB; ++qb) mma_acc(lsum[qb], ones, pb[qb]);
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {
       bf16x8 a;
@@ -292,14 +326,14 @@ __global__ __launch_bounds__(kFwdWaves * 64) void attn_fwd_kernel_ks(
         a[4 + r] = vt[2 * db + 1][r];
       }
 #pragma unroll
-      for (int qb = 0; qb < 4; ++qb) mma_acc(o[db][qb], a, pb[qb]);
+      for (int qb = 0; qb < QB; ++qb) mma_acc(o[db][qb], a, pb[qb]);
     }
     if constexpr (MORE) {
       // maxima of chunk i + 1 in log2 units, keys after a query set to -inf
       // first when the chunk may reach the diagonal
       const int koff = kChunk * (w + kFwdWaves * (i + 1)) - q0;  // its key 0, from query 0
 #pragma unroll
-      for (int qb = 0; qb < 4; ++qb) {
+      for (int qb = 0; qb < QB; ++qb) {
         float mloc = -INFINITY;
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
@@ -319,7 +353,7 @@ __global__ __launch_bounds__(kFwdWaves * 64) void attn_fwd_kernel_ks(
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int qb = 0; qb < 4; ++qb) sc[kb][qb] = sn[kb][qb];
+        for (int qb = 0; qb < QB; ++qb) sc[kb][qb] = sn[kb][qb];
     }
     if constexpr (FETCH) {
       __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): every read of V(i) is complete
@@ -348,7 +382,7 @@ __global__ __launch_bounds__(kFwdWaves * 64) void attn_fwd_kernel_ks(
       }
     }
 #pragma unroll
-    for (int qb = 0; qb < 4; ++qb) {
+    for (int qb = 0; qb < QB; ++qb) {
       lsum[qb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int db = 0; db < NDB; ++db) o[db][qb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -360,6 +394,7 @@ __global__ __launch_bounds__(kFwdWaves * 64) void attn_fwd_kernel_ks(
         wait_vmcnt<NDMA / 2 * 3>();
       else
         wait_vmcnt<NDMA / 2>();
+      GL_STAMP(kKernFwd, 18);
       bf16x8 kf[NKD][2];
 #pragma unroll
       for (int kk = 0; kk < NKD; ++kk) {
@@ -367,19 +402,20 @@ __global__ __launch_bounds__(kFwdWaves * 64) void attn_fwd_kernel_ks(
         kf[kk][1] = read_b128_async<32 * D>(kaddr[kk]);
       }
       wait_kfrags<0>(kf);
+      GL_STAMP(kKernFwd, 19);
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int qb = 0; qb < 4; ++qb) sc[kb][qb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int qb = 0; qb < QB; ++qb) sc[kb][qb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int kk = 0; kk < NKD; ++kk)
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-          for (int qb = 0; qb < 4; ++qb) sc[kb][qb] = M::mma(kf[kk][kb], qf[qb][kk], sc[kb][qb]);
+          for (int qb = 0; qb < QB; ++qb) sc[kb][qb] = M::mma(kf[kk][kb], qf[qb][kk], sc[kb][qb]);
       const int koff = kChunk * w - q0;
 #pragma unroll
-      for (int qb = 0; qb < 4; ++qb) {
+      for (int qb = 0; qb < QB; ++qb) {
         float mloc = -INFINITY;
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
@@ -395,6 +431,7 @@ __global__ __launch_bounds__(kFwdWaves * 64) void attn_fwd_kernel_ks(
         m_seen[qb] = m0;
       }
     }
+    GL_STAMP(kKernFwd, 22);
     if (pass == 0 && q_rot != nullptr) {
       // q_rot as whole rows, issued after chunk 0's wait so that it does not
       // wait for these stores
@@ -425,33 +462,36 @@ __global__ __launch_bounds__(kFwdWaves * 64) void attn_fwd_kernel_ks(
     GL_STAMP(kKernFwd, 17);
     if (__builtin_amdgcn_ballot_w64(grew) == 0) break;
 #pragma unroll
-    for (int qb = 0; qb < 4; ++qb) m_seen[qb] = col_max_swap(m_seen[qb]);
+    for (int qb = 0; qb < QB; ++qb) m_seen[qb] = col_max_swap(m_seen[qb]);
 #pragma unroll
-    for (int qb = 0; qb < 4; ++qb) m_ref[qb] = m_seen[qb];
+    for (int qb = 0; qb < QB; ++qb) m_ref[qb] = m_seen[qb];
   }
   GL_STAMP(kKernFwd, 20);
 
-  // Merge.  Wave w owns query block w.  Each wave writes its raw partial
-  // O^T of the three other blocks and its (maximum, sum) per query into its
-  // own ring region (free once its loop is done, so no wave waits for the
-  // others first), straight from the AGPRs.  After one barrier the owner
+  // Merge.  Wave w < QB owns query block w.  Each wave writes its raw partial
+  // O^T of the blocks it does not own and its (maximum, sum) per query into
+  // its own ring region (free once its loop is done, so no wave waits for the
+  // others first), straight from the AGPRs.  After one barrier each owner
   // weighs the four partials by exp2(m_u - M) / L (M = max of the maxima,
   // L = sum of exp2(m_u - M) l_u, both in wave order), adds them in wave
   // order (its own from registers) and stores its 16 rows.
-  static_assert(3 * 16 * F::OS + 2 * kTile <= F::WAVE / 2, "merge data exceeds a wave's region");
-  float* const mine = reinterpret_cast<float*>(kring);  // [3 blocks][16][OS], maxima, sums
-  constexpr int MOFF = 3 * 16 * F::OS;                   // maxima, then sums (floats)
+  constexpr int MBLK = kFwdWaves > QB ? QB : QB - 1;  // blocks one wave writes, at most
+  static_assert(MBLK * 16 * F::OS + 2 * TR <= F::WAVE / 2, "merge data exceeds a wave's region");
+  float* const mine = reinterpret_cast<float*>(kring);  // [MBLK blocks][16][OS], maxima, sums
+  constexpr int MOFF = MBLK * 16 * F::OS;                // maxima, then sums (floats)
+  // the block slot of query block qb in the region of wave u (u does not own qb)
+  auto slot_of = [](int u, int qb) { return u < QB ? qb - (qb > u) : qb; };
   if (g == 0) {
 #pragma unroll
-    for (int qb = 0; qb < 4; ++qb) {
+    for (int qb = 0; qb < QB; ++qb) {
       mine[MOFF + 16 * qb + c] = m_ref[qb];
-      mine[MOFF + kTile + 16 * qb + c] = lsum[qb][0];
+      mine[MOFF + TR + 16 * qb + c] = lsum[qb][0];
     }
   }
 #pragma unroll
-  for (int qb = 0; qb < 4; ++qb) {
+  for (int qb = 0; qb < QB; ++qb) {
     if (qb == w) continue;
-    const unsigned a = lds_addr(reinterpret_cast<const bf16*>(mine + ((qb - (qb > w)) * 16 + c) * F::OS + 4 * g));
+    const unsigned a = lds_addr(reinterpret_cast<const bf16*>(mine + (slot_of(w, qb) * 16 + c) * F::OS + 4 * g));
     write_acc_block(a, o, qb, std::make_integer_sequence<int, NDB>{});
   }
   __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the merge writes are complete
@@ -459,7 +499,7 @@ __global__ __launch_bounds__(kFwdWaves * 64) void attn_fwd_kernel_ks(
   GL_STAMP(kKernFwd, 24);
   __syncthreads();
   GL_STAMP(kKernFwd, 25);
-  {
+  if (w < QB) {
     const int qi = 16 * w + c;
     const float* region[kFwdWaves];
 #pragma unroll
@@ -469,7 +509,7 @@ __global__ __launch_bounds__(kFwdWaves * 64) void attn_fwd_kernel_ks(
 #pragma unroll
     for (int u = 0; u < kFwdWaves; ++u) {
       mw[u] = region[u][MOFF + qi];
-      lw[u] = region[u][MOFF + kTile + qi];
+      lw[u] = region[u][MOFF + TR + qi];
       m_all = fmaxf(m_all, mw[u]);
     }
     float l_all = 0.0f;
@@ -482,9 +522,9 @@ __global__ __launch_bounds__(kFwdWaves * 64) void attn_fwd_kernel_ks(
     if (g == 0 && lse != nullptr && qi < nq)
       lse[(long)h * total_tokens + td.tok0 + q0 + qi] = (m_all + log2f(l_all)) * kLn2;
     f32x4 acc[NDB];
-    // QB: the owner's block as a constant (one branch on the wave index)
-    auto sum_block = [&](auto qbc) {
-      constexpr int QB = decltype(qbc)::value;
+    // OWN: the owner's block as a constant (one branch on the wave index)
+    auto sum_block = [&](auto own) {
+      constexpr int OWN = decltype(own)::value;
 #pragma unroll
       for (int db = 0; db < NDB; ++db) acc[db] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -493,21 +533,23 @@ __global__ __launch_bounds__(kFwdWaves * 64) void attn_fwd_kernel_ks(
 #pragma unroll
         for (int db = 0; db < NDB; ++db) {
           const f32x4 x =
-              u == QB ? o[db][QB]
-                      : *reinterpret_cast<const f32x4*>(region[u] + ((QB - (QB > u)) * 16 + c) * F::OS +
-                                                        16 * db + 4 * g);
+              u == OWN ? o[db][OWN]
+                       : *reinterpret_cast<const f32x4*>(region[u] + (slot_of(u, OWN) * 16 + c) * F::OS +
+                                                         16 * db + 4 * g);
           acc[db] += x * f;
         }
       }
     };
-    if (w == 0)
+    if (w == 0) {
       sum_block(std::integral_constant<int, 0>{});
-    else if (w == 1)
+    } else if (w == 1) {
       sum_block(std::integral_constant<int, 1>{});
-    else if (w == 2)
-      sum_block(std::integral_constant<int, 2>{});
-    else
-      sum_block(std::integral_constant<int, 3>{});
+    } else if constexpr (QB == 4) {
+      if (w == 2)
+        sum_block(std::integral_constant<int, 2>{});
+      else
+        sum_block(std::integral_constant<int, 3>{});
+    }
     GL_STAMP(kKernFwd, 28);
     // rows of the block: lane (g, c) holds d = 16 db + 4 g .. + 3 of query qi
     if (qi < nq) {
@@ -523,16 +565,23 @@ __global__ __launch_bounds__(kFwdWaves * 64) void attn_fwd_kernel_ks(
 
 template <typename IO, int D>
 hipError_t launch_fwd_bf16(const FwdLaunch& a, hipStream_t st, KernelTimer* tm) {
-  auto fn = a.single_seq ? attn_fwd_kernel_ks<IO, D, false> : attn_fwd_kernel_ks<IO, D, true>;
+  // 32-query workgroups (two per table entry) when the launch is short of CUs
+  const bool rows32 = a.tile_rows == 32;
+  auto fn = a.single_seq ? (rows32 ? attn_fwd_kernel_ks<IO, D, false, 2> : attn_fwd_kernel_ks<IO, D, false, 4>)
+                         : (rows32 ? attn_fwd_kernel_ks<IO, D, true, 2> : attn_fwd_kernel_ks<IO, D, true, 4>);
   constexpr size_t lds = FwdLayout<D>::BYTES;
   GL_CHECK(allow_lds(fn, lds));
+  // the tables are one allocation: the sine table's offset in floats
+  const ptrdiff_t sin_off = a.sin_t - a.cos_t;
+  if (sin_off <= 0 || sin_off > INT32_MAX) return hipErrorInvalidValue;
+  const int group = a.n_heads_q / a.n_heads_kv;
   LaunchTiming t(tm, kKernFwd);
-  GL_LAUNCH(t, fn, dim3(a.n_heads_q / a.n_heads_kv, a.n_heads_kv, a.n_tiles),
-                        dim3(kFwdWaves * 64), lds, st,
-                        static_cast<const IO*>(a.q), static_cast<const bf16*>(a.kc),
-                        static_cast<const bf16*>(a.vc != nullptr ? a.vc : a.v),
-                        static_cast<IO*>(a.out), a.lse, static_cast<IO*>(a.q_rot), a.tiles_fwd,
-                        a.n_tiles, a.total_tokens, a.scale_log2, a.cos_t, a.sin_t);
+  GL_LAUNCH(t, fn, dim3(group, a.n_heads_kv, a.n_tiles * (rows32 ? 2 : 1)), dim3(kFwdWaves * 64), lds,
+                        st, a.total_tokens, a.n_heads_kv, group, static_cast<int>(sin_off),
+                        static_cast<const bf16*>(a.kc),
+                        static_cast<const bf16*>(a.vc != nullptr ? a.vc : a.v), a.tiles_fwd,
+                        static_cast<const IO*>(a.q), a.cos_t, static_cast<IO*>(a.out), a.lse,
+                        static_cast<IO*>(a.q_rot), a.scale_log2);
   GL_CHECK(hipGetLastError());
   t.launched();
   return hipSuccess;

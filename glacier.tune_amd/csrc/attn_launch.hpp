@@ -141,6 +141,9 @@ struct FwdLaunch {
   bool single_seq;               // one sequence: tile order is computed in-kernel
   int head_dim, n_heads_q, n_heads_kv, total_tokens;
   int n_tiles;
+  // query rows per workgroup of the bf16 forward: 64, or 32 (two workgroups
+  // per tile) for launches that would otherwise leave most CUs idle
+  int tile_rows;
   float scale_log2;
   const void *q, *k, *v;
   void *out, *q_rot, *k_rot;

@@ -450,6 +450,17 @@ class GpuAttentionEngine {
         fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT,
              "GLACIER_ATTN_BWD_SPLIT must be auto or 0, not " + m);
     }
+    // GLACIER_ATTN_FWD_ROWS=32|64 pins the bf16 forward's query rows per
+    // workgroup; unset or "auto" takes 32 when 64-row workgroups would
+    // leave at least half of the CUs idle.
+    if (const char* v = std::getenv("GLACIER_ATTN_FWD_ROWS")) {
+      const std::string m(v);
+      if (m == "32") fwd_rows_ = 32;
+      else if (m == "64") fwd_rows_ = 64;
+      else if (m != "auto" && !m.empty())
+        fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT,
+             "GLACIER_ATTN_FWD_ROWS must be auto, 32 or 64, not " + m);
+    }
   }
 
   ~GpuAttentionEngine() {
@@ -501,6 +512,8 @@ class GpuAttentionEngine {
     a.n_heads_kv = s.n_heads_kv;
     a.total_tokens = s.total_tokens;
     a.n_tiles = ts.n_tiles;
+    a.tile_rows = fwd_rows_ != 0 ? fwd_rows_
+                  : 2LL * s.n_heads_q * ts.n_tiles <= n_cu_ ? 32 : 64;
     a.scale_log2 = kLog2e / std::sqrt(static_cast<float>(s.head_dim));
     a.q = q; a.k = k; a.v = v;
     a.out = out; a.lse = lse; a.q_rot = q_rot; a.k_rot = k_rot;
@@ -516,8 +529,8 @@ class GpuAttentionEngine {
     const TileDesc* t = static_cast<const TileDesc*>(ts.tiles.ptr);
     a.tiles_fwd = t;
     a.pos_of = static_cast<const int32_t*>(ts.pos.ptr);
-    a.cos_t = static_cast<const float*>(rope_cos_.ptr);
-    a.sin_t = static_cast<const float*>(rope_sin_.ptr);
+    a.cos_t = rope_cos();
+    a.sin_t = rope_sin();
     check_hip(launch_forward(a, stream(), &timer_), "attention forward launch");
   }
 
@@ -579,8 +592,8 @@ class GpuAttentionEngine {
       a.wv2 = wv2_.ensure(T * Hq * D * wsz, "second-half dV partials");
     }
     a.pos_of = static_cast<const int32_t*>(ts.pos.ptr);
-    a.cos_t = static_cast<const float*>(rope_cos_.ptr);
-    a.sin_t = static_cast<const float*>(rope_sin_.ptr);
+    a.cos_t = rope_cos();
+    a.sin_t = rope_sin();
     check_hip(launch_backward(a, stream(), &timer_), "attention backward launch");
   }
 
@@ -781,7 +794,9 @@ class GpuAttentionEngine {
 
   // cos/sin per (position, pair) computed on the host with exactly the fp32
   // operations of RoPEKernel.cs:64-68 (glibc powf/cosf/sinf), uploaded once
-  // per (length capacity, head_dim, theta).
+  // per (length capacity, head_dim, theta).  One allocation holds the cosine
+  // table and then the sine table (the bf16 forward takes the second as an
+  // offset from the first).
   void EnsureRopeTable(int max_len, int head_dim, float base) {
     if (max_len <= rope_len_ && head_dim == rope_dim_ && base == rope_base_) return;
     const int len = std::max(max_len, std::min(2 * rope_len_, GLACIER_ATTN_MAX_SEQ_LEN));
@@ -796,11 +811,11 @@ class GpuAttentionEngine {
         sn[(size_t)pos * half + i] = sinf(theta);
       }
     const size_t bytes = cs.size() * sizeof(float);
-    rope_cos_.ensure(bytes, "rope cos");
-    rope_sin_.ensure(bytes, "rope sin");
+    rope_.ensure(2 * bytes, "rope tables");
     check_hip(hipStreamSynchronize(stream()), "rope table");
-    check_hip(hipMemcpy(rope_cos_.ptr, cs.data(), bytes, hipMemcpyHostToDevice), "rope cos upload");
-    check_hip(hipMemcpy(rope_sin_.ptr, sn.data(), bytes, hipMemcpyHostToDevice), "rope sin upload");
+    check_hip(hipMemcpy(rope_.ptr, cs.data(), bytes, hipMemcpyHostToDevice), "rope cos upload");
+    check_hip(hipMemcpy(static_cast<char*>(rope_.ptr) + bytes, sn.data(), bytes, hipMemcpyHostToDevice),
+              "rope sin upload");
     rope_len_ = len;
     rope_dim_ = head_dim;
     rope_base_ = base;
@@ -926,7 +941,9 @@ class GpuAttentionEngine {
   std::mutex mutex_;
   KernelTimer timer_;
   std::map<std::vector<int32_t>, std::unique_ptr<TileSet>> tile_cache_;
-  DeviceBuffer rope_cos_, rope_sin_;
+  DeviceBuffer rope_;  // [rope_len_][rope_dim_ / 2] cosines, then as many sines
+  const float* rope_cos() const { return static_cast<const float*>(rope_.ptr); }
+  const float* rope_sin() const { return rope_cos() + (size_t)rope_len_ * (rope_dim_ / 2); }
   int rope_len_ = 0, rope_dim_ = 0;
   float rope_base_ = 0.0f;
   // device-path scratch
@@ -934,6 +951,7 @@ class GpuAttentionEngine {
   int bwd_variant_ = kBwdAuto;
   int n_cu_ = 0;          // compute units of the device
   bool split_ok_ = true;  // dK/dV tiles may be split (GLACIER_ATTN_BWD_SPLIT)
+  int fwd_rows_ = 0;      // bf16 forward rows per workgroup (GLACIER_ATTN_FWD_ROWS; 0: auto)
   // projection scratch and the hipBLASLt handle (created on first use)
   DeviceBuffer yf_, dxf_, lowrank_, part_;
   DeviceBuffer rstd_, dyw_;  // RMSNorm backward row scales, dy copy (weight gradient)

@@ -231,6 +231,59 @@ def test_split_dkdv_tiles_match_whole_tiles(engines, case):
         assert oracle.max_rel_err(got_s[key], got_w[key]) <= BF16_GATE, key
 
 
+@pytest.fixture(scope="module")
+def fwd_rows():
+    """bf16-mode engines pinned to 32- and 64-query forward workgroups
+    (GLACIER_ATTN_FWD_ROWS is read when an engine is created)."""
+    assert torch.cuda.is_available(), "GPU tests need a ROCm GPU"
+    made = {}
+    old = os.environ.get("GLACIER_ATTN_FWD_ROWS")
+    try:
+        for rows in ("32", "64"):
+            os.environ["GLACIER_ATTN_FWD_ROWS"] = rows
+            made[rows] = ga.GpuAttentionEngine(0, ga.PREC_BF16)
+    finally:
+        if old is None:
+            os.environ.pop("GLACIER_ATTN_FWD_ROWS", None)
+        else:
+            os.environ["GLACIER_ATTN_FWD_ROWS"] = old
+    yield made
+    for e in made.values():
+        e.close()
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp32"])
+@pytest.mark.parametrize("case", ["qwen05b_s512", "qwen7b_s512", "packed"])
+def test_forward_32_row_workgroups_match_64_row_workgroups(fwd_rows, case, dtype):
+    """The bf16 forward with two 32-query workgroups per 64-query tile (taken
+    when 64-row workgroups would leave half of the CUs idle) against 64-row
+    workgroups.  A query's scores, probabilities and partial sums come from
+    the same wave over the same key chunks in both, and the one extra chunk a
+    64-row workgroup walks for its first 32 queries is masked to exact zeros,
+    so out, lse and q_rot are bit-identical (no rescue pass: N(0, 1) inputs).
+    Both match the oracle.  The packed batch has a sequence of 70 tokens
+    (its second tile's later 32-query workgroup has no queries and returns)
+    and one of a single token."""
+    if case == "packed":
+        Hq, Hkv, D, base = 14, 2, 128, 1.0e4
+        cu = np.array([0, 70, 103, 233, 234], np.int32)
+        q, k, v, dO = make_inputs(int(cu[-1]), Hq, Hkv, D, 8, True)
+        ref = oracle.layer_fwd_bwd_varlen(q, k, v, dO, cu, base)
+    else:
+        S, Hq, Hkv, D, base = CONFIGS[case]
+        (q, k, v, dO), ref = oracle_case(S, Hq, Hkv, D, base, 1, True)
+        cu = None
+    _say(f"[forward rows 32 vs 64] {case} {dtype} tensors")
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    got = {rows: run_device(fwd_rows[rows], q, k, v, dO, base, tdt, cu=cu) for rows in ("32", "64")}
+    for rows, g in got.items():
+        err = errors(g, ref)
+        _say(f"  rows {rows}: {err}")
+        assert all(e <= BF16_GATE for e in err.values()), (rows, err)
+    for key in ("out", "lse", "q_rot"):
+        assert np.array_equal(got["32"][key], got["64"][key]), key
+
+
 @pytest.mark.parametrize("kernel", BWD_KERNELS)
 def test_bf16_device_backward_is_bitwise_repeatable(bf16_kernels, kernel):
     S, Hq, Hkv, D, base = 300, 14, 2, 128, 1.0e6

@@ -12,7 +12,8 @@ one mode:
                for the oracle too): gate 2e-2
   bf16_f32io   fp32 device tensors of bf16-rounded values, bf16 math: 2e-2
   rows16/32,   bf16 device tensors with each bf16 backward kernel pinned
-  mfma32       (head sizes 64 and 128 only): 2e-2
+  mfma32       (head sizes 64 and 128 only) and 64-query forward
+               workgroups: 2e-2
 The same seed always gives the same cases; each prints its draw first.
 """
 import os
@@ -70,16 +71,20 @@ def engines():
     assert torch.cuda.is_available(), "GPU tests need a ROCm GPU"
     made = {"fp32": ga.GpuAttentionEngine(0, ga.PREC_FP32),
             "bf16": ga.GpuAttentionEngine(0, ga.PREC_BF16)}
-    old = os.environ.get("GLACIER_ATTN_BWD")
+    # the pinned-backward engines also pin 64-query forward workgroups, which
+    # "auto" replaces by 32-query ones on most of these small launches
+    old = {key: os.environ.get(key) for key in ("GLACIER_ATTN_BWD", "GLACIER_ATTN_FWD_ROWS")}
     try:
+        os.environ["GLACIER_ATTN_FWD_ROWS"] = "64"
         for name in ("rows16", "rows32", "mfma32"):
             os.environ["GLACIER_ATTN_BWD"] = name
             made[name] = ga.GpuAttentionEngine(0, ga.PREC_BF16)
     finally:
-        if old is None:
-            os.environ.pop("GLACIER_ATTN_BWD", None)
-        else:
-            os.environ["GLACIER_ATTN_BWD"] = old
+        for key, val in old.items():
+            if val is None:
+                os.environ.pop(key, None)
+            else:
+                os.environ[key] = val
     yield made
     for e in made.values():
         e.close()
