@@ -27,10 +27,11 @@ __device__ inline int swz(int r) {
 // bytes per lane): instruction n fills 1 KB of dst, lane l the 16 bytes at
 // l * 16, i.e. slot l % (D/8) of row n * (512/D) + l / (D/8).  The per-lane
 // offsets repeat every P instructions (the swizzle period) and are computed
-// once; the row offset of instruction n goes into the scalar offset.  A
-// chunk with fewer than 32 rows left in its sequence repeats row nvalid - 1
-// for the rest: those keys lie past every query of the sequence, so their
-// probabilities are exactly 0 and any finite contents give the same sums.
+// once; instruction n adds its row offset (one VALU add, the buffer's range
+// check covers the vector offset only).  A chunk with fewer than 32 rows
+// left in its sequence repeats row nvalid - 1 for the rest: those keys lie
+// past every query of the sequence, so their probabilities are exactly 0
+// and any finite contents give the same sums.
 // Completion is tracked by vmcnt only (the compiler does not track these
 // writes): see wait_vmcnt.
 // The per-lane part of the offsets, by instruction index modulo P.
@@ -74,19 +75,15 @@ __device__ inline void dma_chunk(const DmaLanes& dl, const bf16* src, int nvalid
   const int nv = __builtin_amdgcn_readfirstlane(nvalid < kChunk ? nvalid : kChunk);
   const __amdgpu_buffer_rsrc_t rs =
       __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(au), (short)0, nv * dl.rowb, kBufferWord3);
-  if (nv == kChunk) {
+  // One straight-line path for whole and partial chunks (a short prologue:
+  // every workgroup fetches this code cold): lane row n RPI + rl loads row
+  // min(n RPI + rl, nv - 1), i.e. steps min(n RPI, nv - 1 - rl) rows.
+  const int limb = (nv - 1 - dl.rl) * dl.rowb;
 #pragma unroll
-    for (int n = 0; n < L::NI; ++n)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (GLACIER_LDS void*)(dst + 512 * n), 16, dl.loff[n % L::P],
-                                               n * L::RPI * dl.rowb, 0, 0);
-  } else {
-#pragma unroll
-    for (int n = 0; n < L::NI; ++n) {
-      const int r = n * L::RPI + dl.rl;
-      const int rr = r < nv ? r : nv - 1;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (GLACIER_LDS void*)(dst + 512 * n), 16,
-                                               rr * dl.rowb + 16 * (dl.slot ^ swz<D>(r)), 0, 0, 0);
-    }
+  for (int n = 0; n < L::NI; ++n) {
+    const int step = n * L::RPI * dl.rowb;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (GLACIER_LDS void*)(dst + 512 * n), 16,
+                                             dl.loff[n % L::P] + (step < limb ? step : limb), 0, 0, 0);
   }
 #endif
 }
