@@ -291,6 +291,10 @@ __global__ __launch_bounds__(kFwdWaves * 64) void attn_fwd_kernel_ks(
       vt[2 * db] = read_tr_async<0>(vaddr[db] + vslot);
       vt[2 * db + 1] = read_tr_async<32 * D>(vaddr[db] + vslot);
     }
+    // Part 1: chunk i + 1's score MFMAs with chunk i's probabilities
+    // (independent work) interleaved, so that the VALU takes the
+    // exponentials while the matrix core runs: one wave per SIMD issues in
+    // order, and a run of MFMAs would stall the VALU work behind it.
     f32x4 sn[2][QB];
     if constexpr (MORE) {
       wait_kfrags<(2 * NDB < 15 ? 2 * NDB : 15)>(kf);
@@ -298,51 +302,63 @@ __global__ __launch_bounds__(kFwdWaves * 64) void attn_fwd_kernel_ks(
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) sn[kb][qb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-      for (int kk = 0; kk < NKD; ++kk)
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int qb = 0; qb < QB; ++qb) sn[kb][qb] = M::mma(kf[kk][kb], qf[qb][kk], sn[kb][qb]);
     }
+    // G groups, each of MPG score MFMAs (m -> kk, kb, qb) and one pair of
+    // probabilities (p -> qb, kb, r pair), fenced so the order holds.
     bf16x8 pb[QB];
+    constexpr int G = 4 * QB;
+    constexpr int MPG = 2 * QB * NKD / G;
+    static_assert(MPG * G == 2 * QB * NKD, "score MFMAs per group");
 #pragma unroll
-    for (int qb = 0; qb < QB; ++qb)
+    for (int grp = 0; grp < G; ++grp) {
+      if constexpr (MORE) {
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+        for (int mm = 0; mm < MPG; ++mm) {
+          const int m = grp * MPG + mm;
+          const int kk = m / (2 * QB), kb = (m / QB) % 2, qb = m % QB;
+          sn[kb][qb] = M::mma(kf[kk][kb], qf[qb][kk], sn[kb][qb]);
+        }
+      }
+      const int qb = grp / 4, kb = (grp / 2) % 2, r0 = 2 * (grp % 2);
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          pb[qb][4 * kb + r] =
-              (bf16)__builtin_amdgcn_exp2f(__builtin_fmaf(sc[kb][qb][r], scale_log2, -m_ref[qb]));
+      for (int r = r0; r < r0 + 2; ++r)
+        pb[qb][4 * kb + r] = (bf16)__builtin_amdgcn_exp2f(__builtin_fmaf(sc[kb][qb][r], scale_log2, -m_ref[qb]));
+      __builtin_amdgcn_sched_barrier(0);
+    }
     wait_tr(vt);
+    bf16x8 va[NDB];
 #pragma unroll
-    for (int qb = 0; qb < QB; ++qb) mma_acc(lsum[qb], ones, pb[qb]);
-#pragma unroll
-    for (int db = 0; db < NDB; ++db) {
-      bf16x8 a;
+    for (int db = 0; db < NDB; ++db)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        a[r] = vt[2 * db][r];
-        a[4 + r] = vt[2 * db + 1][r];
+        va[db][r] = vt[2 * db][r];
+        va[db][4 + r] = vt[2 * db + 1][r];
       }
+    // Part 2: chunk i's row sums and PV products (query block by query
+    // block), with chunk i + 1's maxima in log2 units interleaved, EPS score
+    // elements after each product (keys after a query set to -inf first when
+    // the chunk may reach the diagonal).
+    constexpr int EPS = 8 / NDB;
+    const int koff = kChunk * (w + kFwdWaves * (i + 1)) - q0;  // chunk i + 1's key 0, from query 0
 #pragma unroll
-      for (int qb = 0; qb < QB; ++qb) mma_acc(o[db][qb], a, pb[qb]);
-    }
-    if constexpr (MORE) {
-      // maxima of chunk i + 1 in log2 units, keys after a query set to -inf
-      // first when the chunk may reach the diagonal
-      const int koff = kChunk * (w + kFwdWaves * (i + 1)) - q0;  // its key 0, from query 0
+    for (int qb = 0; qb < QB; ++qb) {
+      mma_acc(lsum[qb], ones, pb[qb]);
+      float mloc = -INFINITY;
 #pragma unroll
-      for (int qb = 0; qb < QB; ++qb) {
-        float mloc = -INFINITY;
+      for (int db = 0; db < NDB; ++db) {
+        mma_acc(o[db][qb], va[db], pb[qb]);
+        if constexpr (MORE) {
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
+          for (int e = EPS * db; e < EPS * db + EPS; ++e) {
+            const int kb = e >> 2, r = e & 3;
             if (MASK)
               sn[kb][qb][r] = (koff + 16 * kb + 4 * g + r <= 16 * qb + c) ? sn[kb][qb][r] : -INFINITY;
             mloc = fmaxf(mloc, sn[kb][qb][r]);
           }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if constexpr (MORE) {
         // lane-local: a chunk exceeds a column's reference iff one of the
         // column's four lanes does, and the maxima seen become the rescue
         // pass's references only after one cross-lane reduction at the end
@@ -350,6 +366,8 @@ __global__ __launch_bounds__(kFwdWaves * 64) void attn_fwd_kernel_ks(
         grew = grew || (ml > m_ref[qb] + kRescale);
         m_seen[qb] = fmaxf(m_seen[qb], ml);
       }
+    }
+    if constexpr (MORE) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
