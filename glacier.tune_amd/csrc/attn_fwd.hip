@@ -335,29 +335,48 @@ __global__ __launch_bounds__(kFwdWaves * 64) void attn_fwd_kernel_ks(
         va[db][4 + r] = vt[2 * db + 1][r];
       }
     // Part 2: chunk i's row sums and PV products (query block by query
-    // block), with chunk i + 1's maxima in log2 units interleaved, EPS score
-    // elements after each product (keys after a query set to -inf first when
-    // the chunk may reach the diagonal).
-    constexpr int EPS = 8 / NDB;
+    // block, in pairs behind one wait), with chunk i + 1's maxima in log2
+    // units interleaved, EPP score elements after each pair (keys after a
+    // query set to -inf first when the chunk may reach the diagonal).
+    constexpr int NPAIR = (NDB + 2) / 2;             // pairs of the NDB + 1 products
+    constexpr int EPP = (8 + NPAIR - 1) / NPAIR;     // maxima elements per pair
     const int koff = kChunk * (w + kFwdWaves * (i + 1)) - q0;  // chunk i + 1's key 0, from query 0
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
-      mma_acc(lsum[qb], ones, pb[qb]);
       float mloc = -INFINITY;
-#pragma unroll
-      for (int db = 0; db < NDB; ++db) {
-        mma_acc(o[db][qb], va[db], pb[qb]);
+      // product j: the row sums (j = 0) or O^T block j - 1
+      auto acc_of = [&](auto jc) -> f32x4& {
+        if constexpr (decltype(jc)::value == 0)
+          return lsum[qb];
+        else
+          return o[decltype(jc)::value - 1][qb];
+      };
+      auto opa_of = [&](auto jc) -> const bf16x8& {
+        if constexpr (decltype(jc)::value == 0)
+          return ones;
+        else
+          return va[decltype(jc)::value - 1];
+      };
+      static_for<NPAIR>([&](auto pc) {
+        constexpr int j0 = 2 * decltype(pc)::value, j1 = j0 + 1;
+        using J0 = std::integral_constant<int, j0>;
+        using J1 = std::integral_constant<int, (j1 <= NDB ? j1 : j0)>;
+        if constexpr (j1 <= NDB)
+          mma_acc2(acc_of(J0{}), opa_of(J0{}), pb[qb], acc_of(J1{}), opa_of(J1{}), pb[qb]);
+        else
+          mma_acc(acc_of(J0{}), opa_of(J0{}), pb[qb]);
         if constexpr (MORE) {
 #pragma unroll
-          for (int e = EPS * db; e < EPS * db + EPS; ++e) {
+          for (int e = EPP * decltype(pc)::value; e < EPP * decltype(pc)::value + EPP && e < 8; ++e) {
             const int kb = e >> 2, r = e & 3;
             if (MASK)
               sn[kb][qb][r] = (koff + 16 * kb + 4 * g + r <= 16 * qb + c) ? sn[kb][qb][r] : -INFINITY;
             mloc = fmaxf(mloc, sn[kb][qb][r]);
           }
+          asm volatile("" ::"v"(mloc));  // computed here, not sunk past the products
         }
         __builtin_amdgcn_sched_barrier(0);
-      }
+      });
       if constexpr (MORE) {
         // lane-local: a chunk exceeds a column's reference iff one of the
         // column's four lanes does, and the maxima seen become the rescue

@@ -27,11 +27,10 @@ __device__ inline int swz(int r) {
 // bytes per lane): instruction n fills 1 KB of dst, lane l the 16 bytes at
 // l * 16, i.e. slot l % (D/8) of row n * (512/D) + l / (D/8).  The per-lane
 // offsets repeat every P instructions (the swizzle period) and are computed
-// once; instruction n adds its row offset (one VALU add, the buffer's range
-// check covers the vector offset only).  A chunk with fewer than 32 rows
-// left in its sequence repeats row nvalid - 1 for the rest: those keys lie
-// past every query of the sequence, so their probabilities are exactly 0
-// and any finite contents give the same sums.
+// once.  A chunk with fewer than 32 rows left in its sequence repeats row
+// nvalid - 1 for the rest: those keys lie past every query of the sequence,
+// so their probabilities are exactly 0 and any finite contents give the
+// same sums.
 // Completion is tracked by vmcnt only (the compiler does not track these
 // writes): see wait_vmcnt.
 // The per-lane part of the offsets, by instruction index modulo P.
@@ -75,15 +74,24 @@ __device__ inline void dma_chunk(const DmaLanes& dl, const bf16* src, int nvalid
   const int nv = __builtin_amdgcn_readfirstlane(nvalid < kChunk ? nvalid : kChunk);
   const __amdgpu_buffer_rsrc_t rs =
       __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(au), (short)0, nv * dl.rowb, kBufferWord3);
-  // One straight-line path for whole and partial chunks (a short prologue:
-  // every workgroup fetches this code cold): lane row n RPI + rl loads row
-  // min(n RPI + rl, nv - 1), i.e. steps min(n RPI, nv - 1 - rl) rows.
-  const int limb = (nv - 1 - dl.rl) * dl.rowb;
+  if (nv == kChunk) {
+    // whole chunk: the row offset of instruction n goes into the scalar
+    // offset (no per-lane arithmetic inside the loop)
 #pragma unroll
-  for (int n = 0; n < L::NI; ++n) {
-    const int step = n * L::RPI * dl.rowb;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (GLACIER_LDS void*)(dst + 512 * n), 16,
-                                             dl.loff[n % L::P] + (step < limb ? step : limb), 0, 0, 0);
+    for (int n = 0; n < L::NI; ++n)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (GLACIER_LDS void*)(dst + 512 * n), 16, dl.loff[n % L::P],
+                                               n * L::RPI * dl.rowb, 0, 0);
+  } else {
+    // lane row n RPI + rl loads row min(n RPI + rl, nv - 1), i.e. steps
+    // min(n RPI, nv - 1 - rl) rows (the range check covers the vector
+    // offset only, so the rows go there)
+    const int limb = (nv - 1 - dl.rl) * dl.rowb;
+#pragma unroll
+    for (int n = 0; n < L::NI; ++n) {
+      const int step = n * L::RPI * dl.rowb;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (GLACIER_LDS void*)(dst + 512 * n), 16,
+                                               dl.loff[n % L::P] + (step < limb ? step : limb), 0, 0, 0);
+    }
   }
 #endif
 }
@@ -145,6 +153,14 @@ __device__ inline void wait_tr(bf16x4 (&t)[16]) {
 // needs (s_nop 1), and fence_acc below the MFMA-to-reader wait states.
 __device__ inline void mma_acc(f32x4& acc, const bf16x8& a, const bf16x8& b) {
   asm("s_nop 1\n\tv_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+// Two independent accumulations behind one pair of wait states (one issue
+// slot fewer than two mma_acc calls).
+__device__ inline void mma_acc2(f32x4& acc0, const bf16x8& a0, const bf16x8& b0, f32x4& acc1,
+                                const bf16x8& a1, const bf16x8& b1) {
+  asm("s_nop 1\n\tv_mfma_f32_16x16x32_bf16 %0, %2, %3, %0\n\tv_mfma_f32_16x16x32_bf16 %1, %4, %5, %1"
+      : "+a"(acc0), "+a"(acc1)
+      : "v"(a0), "v"(b0), "v"(a1), "v"(b1));
 }
 
 // ds_write_b128 of an accumulator straight from its AGPRs (OFF: the offset

@@ -121,16 +121,6 @@ __device__ inline bf16x8 join8(bf16x4 lo, bf16x4 hi) {
   return r;
 }
 
-// f(integral_constant<int, i>) for i = 0 .. N - 1, in order
-template <int N, typename F, int... I>
-__device__ inline void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
-  (f(std::integral_constant<int, I>{}), ...);
-}
-template <int N, typename F>
-__device__ inline void static_for(F&& f) {
-  static_for_impl<N>(f, std::make_integer_sequence<int, N>{});
-}
-
 // A buffer resource over [base, base + bytes) with base made wave-uniform.
 #if defined(__HIP_DEVICE_COMPILE__)
 __device__ inline __amdgpu_buffer_rsrc_t wave_rsrc(const void* base, int bytes) {
