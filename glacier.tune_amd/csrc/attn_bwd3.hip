@@ -9,7 +9,9 @@
 //               D_i = dO_i . O_i (the softmax-gradient row term), [Hq][T].
 //   attn_bwd3   one workgroup of 8 waves per entry of the 128-row tile table
 //               (both kinds, longest expected first):
-//     dK/dV tile  128 keys of one query head.  Waves = 4 key quarters x 2
+//     dK/dV tile  128 keys of one query head, or of two (heads 2p, 2p + 1
+//                 walked in sequence into the same accumulators, one
+//                 partial per pair).  Waves = 4 key quarters x 2
 //                 roles, the two waves of a quarter on one SIMD.  The P wave
 //                 keeps its 32 keys' K fragments and dV^T in AGPRs and forms
 //                 S = Q K^T, P (masked) and dV^T += dO^T P; the dS wave keeps
@@ -346,7 +348,7 @@ __device__ inline void b4_dkdv(const TileDesc td, const bf16* __restrict__ q_rot
                                const bf16* __restrict__ d_out, const bf16* __restrict__ k_rot,
                                const bf16* __restrict__ v, const float2* __restrict__ stats,
                                bf16* __restrict__ wk, bf16* __restrict__ wv, int total_tokens,
-                               int n_heads_q, int n_heads_kv, int h, int kvh, float c2,
+                               int n_heads_q, int n_heads_kv, int h, int hp, int kvh, float c2,
                                float scale, unsigned char* smem) {
   using L = L3<D>;
   constexpr int NKK = L::NKK, NDB = L::NDB, NST = 2 * NDB;
@@ -357,7 +359,11 @@ __device__ inline void b4_dkdv(const TileDesc td, const bf16* __restrict__ q_rot
   const int kq = w & 3, role = w >> 2;
   const int k0 = kWideTile * td.tile;
   const int kw = k0 + 32 * kq;                          // this wave's first key
-  const int nst = (td.len - k0 + kC3 - 1) / kC3;        // 32-query chunks from k0 on
+  const int nst = (td.len - k0 + kC3 - 1) / kC3;        // 32-query chunks from k0 on, per head
+  // hp query heads (h, h + 1) in sequence: chunk n is chunk n % nst of head
+  // h + n / nst; the accumulators run on across the heads
+  const int ntot = hp * nst;
+  auto local = [&](int n) { return n >= nst ? n - nst : n; };
   const long qstride = (long)n_heads_q * D, kvstride = (long)n_heads_kv * D;
   const int qrowb = static_cast<int>(qstride * 2), kvrowb = static_cast<int>(kvstride * 2);
   const bf16* qb0 = q_rot + ((long)td.tok0 * n_heads_q + h) * D;
@@ -377,21 +383,23 @@ __device__ inline void b4_dkdv(const TileDesc td, const bf16* __restrict__ q_rot
   // the stats (2)
   auto issue = [&](int n) {
     if (role != 1 || kq == 3) return;
-    const int q0 = k0 + kC3 * n, sl = n & 3;
+    const int hh = n >= nst ? 1 : 0;
+    const int q0 = k0 + kC3 * (n - hh * nst), sl = n & 3;
     if (kq == 0)
-      dma3<D>(dq3, qb0 + (long)q0 * qstride, td.len - q0, smem + L::KV_STATS + sl * SL, lane);
+      dma3<D>(dq3, qb0 + hh * D + (long)q0 * qstride, td.len - q0, smem + L::KV_STATS + sl * SL, lane);
     else if (kq == 1)
-      dma3<D>(dq3, ob0 + (long)q0 * qstride, td.len - q0, smem + L::KV_STATS + sl * SL + L::CB,
-              lane);
+      dma3<D>(dq3, ob0 + hh * D + (long)q0 * qstride, td.len - q0,
+              smem + L::KV_STATS + sl * SL + L::CB, lane);
     else
-      dma_stats3<D>(dq3, sb0 + q0, td.len - q0, smem + sl * L::ST);
+      dma_stats3<D>(dq3, sb0 + (long)hh * total_tokens + q0, td.len - q0, smem + sl * L::ST);
   };
   // DMA instructions per chunk of this wave (for its waits)
   const int per = role == 1 ? (kq < 2 ? D / 16 : kq == 2 ? 1 : 0) : 0;
-  auto mask_of = [&](int n) {
-    // the chunk's first query precedes the wave's last key, or the chunk or
-    // the wave's keys run past the sequence end
-    return k0 + kC3 * n < kw + 31 || k0 + kC3 * (n + 1) > td.len || kw + 32 > td.len;
+  auto mask_of = [&](int m) {
+    // (m: the chunk's index within its head) the chunk's first query
+    // precedes the wave's last key, or the chunk or the wave's keys run past
+    // the sequence end
+    return k0 + kC3 * m < kw + 31 || k0 + kC3 * (m + 1) > td.len || kw + 32 > td.len;
   };
 
   // Prologue: the wave's 32 K rows (P waves) or V rows (dS waves) into
@@ -400,7 +408,7 @@ __device__ inline void b4_dkdv(const TileDesc td, const bf16* __restrict__ q_rot
   load_rows3<D>((role == 0 ? k_rot : v) + ((long)(td.tok0 + kw) * n_heads_kv + kvh) * D, kvrowb,
                 td.len - kw, kf, lane);
   issue(0);
-  if (nst > 1) issue(1);
+  if (ntot > 1) issue(1);
   f32x16 acc[NDB];
   zero16(acc);
   vmw<0>();
@@ -495,8 +503,9 @@ __device__ inline void b4_dkdv(const TileDesc td, const bf16* __restrict__ q_rot
 #pragma unroll
         for (int e = 0; e < 16; ++e)
           xa[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(xa[e], c2, st[e >> 2][e & 3]));
-        if (mask_of(c)) {
-          const int key = kw + (lane & 31), hh = lane >> 5, q0 = k0 + kC3 * c;
+        const int cl = local(c);
+        if (mask_of(cl)) {
+          const int key = kw + (lane & 31), hh = lane >> 5, q0 = k0 + kC3 * cl;
 #pragma unroll
           for (int e = 0; e < 16; ++e) {
             const int q = q0 + 8 * (e >> 2) + 4 * hh + (e & 3);
@@ -526,11 +535,11 @@ __device__ inline void b4_dkdv(const TileDesc td, const bf16* __restrict__ q_rot
   // DMA bookkeeping of step c: chunk c + 2 goes out at the start; chunk
   // c + 1 must have landed by the end (chunk c + 2's copy may stay in flight)
   auto dma_begin = [&](int c) {
-    if (c + 2 < nst) issue(c + 2);
+    if (c + 2 < ntot) issue(c + 2);
   };
   auto dma_end = [&](int c) {
     if (per == 0) return;
-    if (c + 2 < nst)
+    if (c + 2 < ntot)
       vm_wait_v(per);
     else
       vmw<0>();
@@ -541,7 +550,7 @@ __device__ inline void b4_dkdv(const TileDesc td, const bf16* __restrict__ q_rot
   dma_end(0);
   GL_STAMP(kKernBwd, 4);
   wg_barrier();
-  // steps 1 .. nst - 1: chains of chunk c, products of chunk c - 1, in
+  // steps 1 .. ntot - 1: chains of chunk c, products of chunk c - 1, in
   // groups of four by slot
   int c = 1;
   auto full = [&](auto sa, int cc) {
@@ -553,30 +562,30 @@ __device__ inline void b4_dkdv(const TileDesc td, const bf16* __restrict__ q_rot
     wg_barrier();
   };
 #pragma clang loop unroll(disable)
-  for (; c + 3 < nst; c += 4) {
+  for (; c + 3 < ntot; c += 4) {
     full(std::integral_constant<int, 1>{}, c);
     full(std::integral_constant<int, 2>{}, c + 1);
     full(std::integral_constant<int, 3>{}, c + 2);
     full(std::integral_constant<int, 0>{}, c + 3);
   }
-  if (c < nst) {
+  if (c < ntot) {
     full(std::integral_constant<int, 1>{}, c);
     ++c;
   }
-  if (c < nst) {
+  if (c < ntot) {
     full(std::integral_constant<int, 2>{}, c);
     ++c;
   }
-  if (c < nst) {
+  if (c < ntot) {
     full(std::integral_constant<int, 3>{}, c);
     ++c;
   }
-  // step nst: products of the last chunk only
-  switch ((nst - 1) & 3) {
-    case 0: step(std::integral_constant<int, 1>{}, std::integral_constant<int, 0>{}, B0{}, B1{}, nst); break;
-    case 1: step(std::integral_constant<int, 2>{}, std::integral_constant<int, 1>{}, B0{}, B1{}, nst); break;
-    case 2: step(std::integral_constant<int, 3>{}, std::integral_constant<int, 2>{}, B0{}, B1{}, nst); break;
-    default: step(std::integral_constant<int, 0>{}, std::integral_constant<int, 3>{}, B0{}, B1{}, nst); break;
+  // step ntot: products of the last chunk only
+  switch ((ntot - 1) & 3) {
+    case 0: step(std::integral_constant<int, 1>{}, std::integral_constant<int, 0>{}, B0{}, B1{}, ntot); break;
+    case 1: step(std::integral_constant<int, 2>{}, std::integral_constant<int, 1>{}, B0{}, B1{}, ntot); break;
+    case 2: step(std::integral_constant<int, 3>{}, std::integral_constant<int, 2>{}, B0{}, B1{}, ntot); break;
+    default: step(std::integral_constant<int, 0>{}, std::integral_constant<int, 3>{}, B0{}, B1{}, ntot); break;
   }
   GL_STAMP(kKernBwd, 20);
 
@@ -892,25 +901,39 @@ __device__ inline void b4_dq(const TileDesc td, const bf16* __restrict__ q_rot,
   GL_STAMP(kKernBwd, 22);
 }
 
-// grid (Hq/Hkv, Hkv, 2 n_tiles); z indexes the tile table (both kinds,
-// longest expected first).
+// grid (ratio, Hkv, entries) or, with head_pairs, (ceil(ratio / 2), Hkv,
+// entries) (ratio = Hq / Hkv); z indexes the tile table (both kinds,
+// longest expected first).  head_pairs: x stands for query heads 2x and
+// 2x + 1 of the group (the last one alone when ratio is odd): a dK/dV tile
+// walks both heads' queries into the same accumulators (one partial per
+// pair); the table then holds each dQ tile twice, kTileDq for head 2x and
+// kTileDqSecond for head 2x + 1.
 template <int D>
 __global__ __launch_bounds__(kNT3) void attn_bwd3_kernel(
     const bf16* __restrict__ q_rot, const bf16* __restrict__ d_out, const bf16* __restrict__ k_rot,
     const bf16* __restrict__ v, const float2* __restrict__ stats, bf16* __restrict__ dq,
     bf16* __restrict__ wk, bf16* __restrict__ wv, const TileDesc* __restrict__ tiles_bwd,
     const int32_t* __restrict__ pos_of, int total_tokens, float c2, float scale,
-    const float* __restrict__ cos_t, const float* __restrict__ sin_t) {
+    const float* __restrict__ cos_t, const float* __restrict__ sin_t, int ratio, int head_pairs) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  const int ratio = gridDim.x, n_heads_kv = gridDim.y, n_heads_q = ratio * n_heads_kv;
-  const int kvh = blockIdx.y, h = kvh * ratio + blockIdx.x;
+  const int n_heads_kv = gridDim.y, n_heads_q = ratio * n_heads_kv;
+  // Head pairs: the x index is rotated by the entry index, so that with an
+  // odd group the pair holding one head (half a dK/dV tile's work, no second
+  // dQ tile) does not always land on the same XCDs (workgroup ids are dealt
+  // to the XCDs in turn).
+  const int x = head_pairs ? 2 * (((int)blockIdx.x + (int)blockIdx.z) % (int)gridDim.x) : (int)blockIdx.x;
+  const int kvh = blockIdx.y;
   const TileDesc td = tiles_bwd[blockIdx.z];
-  if (td.kind == kTileDkDv)
-    b4_dkdv<D>(td, q_rot, d_out, k_rot, v, stats, wk, wv, total_tokens, n_heads_q, n_heads_kv, h,
-               kvh, c2, scale, smem_raw);
-  else
-    b4_dq<D>(td, q_rot, d_out, k_rot, v, stats, dq, pos_of, total_tokens, n_heads_q, n_heads_kv, h,
-             kvh, c2, scale, cos_t, sin_t, smem_raw);
+  if (td.kind == kTileDkDv) {
+    const int hp = head_pairs && ratio - x >= 2 ? 2 : 1;
+    b4_dkdv<D>(td, q_rot, d_out, k_rot, v, stats, wk, wv, total_tokens, n_heads_q, n_heads_kv,
+               kvh * ratio + x, hp, kvh, c2, scale, smem_raw);
+  } else {
+    const int hq = x + (td.kind == kTileDqSecond ? 1 : 0);
+    if (hq >= ratio) return;  // an odd group's last pair has no second head
+    b4_dq<D>(td, q_rot, d_out, k_rot, v, stats, dq, pos_of, total_tokens, n_heads_q, n_heads_kv,
+             kvh * ratio + hq, kvh, c2, scale, cos_t, sin_t, smem_raw);
+  }
 }
 
 }  // namespace
@@ -935,13 +958,15 @@ hipError_t launch_bwd3(const BwdLaunch& a, hipStream_t st, KernelTimer* tm) {
     constexpr size_t lds = L3<D>::BYTES;
     GL_CHECK(allow_lds(fn, lds));
     LaunchTiming t(tm, kKernBwd);
-    GL_LAUNCH(t, fn, dim3(ratio, a.n_heads_kv, a.n_wide_entries), dim3(kNT3), lds, st,
+    const bool pairs = a.dkdv_head_pairs && ratio > 1;
+    GL_LAUNCH(t, fn, dim3(pairs ? (ratio + 1) / 2 : ratio, a.n_heads_kv, a.n_wide_entries), dim3(kNT3),
+              lds, st,
               static_cast<const bf16*>(a.q_rot), static_cast<const bf16*>(a.d_out),
               static_cast<const bf16*>(a.k_rot), static_cast<const bf16*>(a.v),
               static_cast<const float2*>(stats), static_cast<bf16*>(a.dq),
               static_cast<bf16*>(a.wk), static_cast<bf16*>(a.wv), a.tiles_wide,
               a.single_seq ? nullptr : a.pos_of, a.total_tokens, a.scale * kLog2e, a.scale,
-              a.cos_t, a.sin_t);
+              a.cos_t, a.sin_t, ratio, pairs ? 1 : 0);
     GL_CHECK(hipGetLastError());
     t.launched();
   }

@@ -915,13 +915,14 @@ __device__ inline f32x4 load_partial4(const bf16* p) {
 }
 
 // SPLIT: the call split dK/dV tiles (bf16 partials), so rows below
-// split_rows have second partials.
+// split_rows have second partials.  hstep: the partials sit at every
+// hstep-th head of the group (2 after the wide backward's head pairs).
 template <typename IO, typename T, int D, bool SPLIT>
 __global__ __launch_bounds__(kRedThreads) void attn_bwd_reduce_kernel(
     const IO* __restrict__ wk, const IO* __restrict__ wv, IO* __restrict__ dk,
     IO* __restrict__ dv, const IO* __restrict__ wk2, const IO* __restrict__ wv2,
     int split_rows, const int32_t* __restrict__ pos_of, int total_tokens, int ratio,
-    int n_heads_kv, const float* __restrict__ cos_t, const float* __restrict__ sin_t) {
+    int n_heads_kv, const float* __restrict__ cos_t, const float* __restrict__ sin_t, int hstep) {
   constexpr int H = D / 2;
   constexpr int CH = H / 4;  // 4-pair chunks per row
   constexpr int ROWS = kRedThreads / CH;
@@ -947,7 +948,8 @@ __global__ __launch_bounds__(kRedThreads) void attn_bwd_reduce_kernel(
   f32x4 k0 = {0.0f, 0.0f, 0.0f, 0.0f}, k1 = k0, v0 = k0, v1 = k0;
   constexpr int RMAX = 8;
   constexpr int RMAX2 = SPLIT ? RMAX : 1;
-  if (ratio <= RMAX) {
+  const int nparts = (ratio + hstep - 1) / hstep;  // partials per row, at heads 0, hstep, ..
+  if (nparts <= RMAX) {
     // Every head's partial in flight at once (a load per head that the sum
     // waits on would cost one memory round trip per head), then the sum in
     // ascending head order; heads past the group add nothing.
@@ -955,7 +957,7 @@ __global__ __launch_bounds__(kRedThreads) void attn_bwd_reduce_kernel(
     f32x4 qk0[RMAX2], qk1[RMAX2], qv0[RMAX2], qv1[RMAX2];
 #pragma unroll
     for (int hh = 0; hh < RMAX; ++hh) {
-      const long o = (long)(hh < ratio ? hh : 0) * D;
+      const long o = (long)(hh < nparts ? hh * hstep : 0) * D;
       pk0[hh] = load_partial4(wkr + o);
       pk1[hh] = load_partial4(wkr + o + H);
       pv0[hh] = load_partial4(wvr + o);
@@ -975,7 +977,7 @@ __global__ __launch_bounds__(kRedThreads) void attn_bwd_reduce_kernel(
     }
 #pragma unroll
     for (int hh = 0; hh < RMAX; ++hh) {
-      if (hh < ratio) {
+      if (hh < nparts) {
         k0 += pk0[hh];
         k1 += pk1[hh];
         v0 += pv0[hh];
@@ -991,7 +993,7 @@ __global__ __launch_bounds__(kRedThreads) void attn_bwd_reduce_kernel(
       }
     }
   } else {
-    for (int hh = 0; hh < ratio; ++hh) {
+    for (int hh = 0; hh < ratio; hh += hstep) {
       k0 += load_partial4(wkr + (long)hh * D);
       k1 += load_partial4(wkr + (long)hh * D + H);
       v0 += load_partial4(wvr + (long)hh * D);
@@ -1132,7 +1134,8 @@ hipError_t backward_impl(const BwdLaunch& a, hipStream_t st, KernelTimer* tm) {
                           static_cast<IO*>(a.dv), static_cast<const IO*>(split ? a.wk2 : nullptr),
                           static_cast<const IO*>(split ? a.wv2 : nullptr),
                           split ? kTile * a.split : 0, a.single_seq ? nullptr : a.pos_of,
-                          a.total_tokens, ratio, a.n_heads_kv, a.cos_t, a.sin_t);
+                          a.total_tokens, ratio, a.n_heads_kv, a.cos_t, a.sin_t,
+                          mfma32 && a.dkdv_head_pairs && ratio > 1 ? 2 : 1);
     GL_CHECK(hipGetLastError());
     t.launched();
   }

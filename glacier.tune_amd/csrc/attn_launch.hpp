@@ -36,6 +36,7 @@ enum TileKind : int {
   kTileDq = 1,
   kTileDkDvFirstHalf = 2,
   kTileDkDvSecondHalf = 3,
+  kTileDqSecond = 4,  // wide backward over head pairs: the dQ tile of the pair's second head
 };
 // dK/dV tiles 0 .. split - 1 of each sequence may be split (16-row backward,
 // bf16 tensors, only while the launch about fits one workgroup per CU).
@@ -191,6 +192,10 @@ struct BwdLaunch {
   // that kernel is then not used) and its length.
   const TileDesc* tiles_wide;
   int n_wide_entries;
+  // That kernel's workgroups take two query heads of a group each: a dK/dV
+  // tile walks both into one partial (the head reduction then sums every
+  // second head), a dQ tile runs both heads' tiles in turn.
+  bool dkdv_head_pairs;
   const int32_t* pos_of;
   const float *cos_t, *sin_t;
 };

@@ -136,12 +136,20 @@ inline int bwd_tile_cost(int n_tiles_in_seq, int tile, int kind) {
 // len tokens: its step count (one per 32-row chunk it visits, plus one),
 // weighted by the step time of its kind, plus a fixed part; it only orders
 // the launch.
-inline int bwd_wide_cost(int len, int tile, int kind) {
-  if (kind == kTileDq) {
+inline int bwd_wide_cost(int len, int tile, int kind, bool head_pairs) {
+  if (kind == kTileDq || kind == kTileDqSecond) {
     const int keys = std::min(len, kWideTile * (tile + 1));
     return 50 + 18 * (((keys + 31) / 32 + 1) / 2 + 1);
   }
-  return 50 + 12 * ((len - kWideTile * tile + 31) / 32 + 1);
+  // a dK/dV tile over a head pair walks twice the query chunks
+  return 50 + (head_pairs ? 24 : 12) * ((len - kWideTile * tile + 31) / 32 + 1);
+}
+
+// The wide backward's entries per 128-row tile: dK/dV and dQ, plus the dQ
+// tile of a head pair's second head when its workgroups take head pairs.
+inline std::vector<int> wide_kinds(bool head_pairs) {
+  if (head_pairs) return {kTileDkDv, kTileDq, kTileDqSecond};
+  return {kTileDkDv, kTileDq};
 }
 
 // The backward entries of one sequence of nt tiles in natural order (tile by
@@ -167,7 +175,7 @@ constexpr int kNoAllocMaxCost = 63 + 16 * (kNoAllocMaxTokens / kTile);
 constexpr int kNoAllocMaxSplitEntries = 4096;  // a split table fits the CUs: far fewer
 // the 128-row table of the wide backward: two entries per 128-row tile
 constexpr int kNoAllocMaxWideEntries = 2 * (kNoAllocMaxTokens / kWideTile + kNoAllocMaxSeqs);
-constexpr int kNoAllocMaxWideCost = 50 + 12 * ((kNoAllocMaxTokens + 31) / 32 + 1);
+constexpr int kNoAllocMaxWideCost = 50 + 24 * ((kNoAllocMaxTokens + 31) / 32 + 1);
 constexpr int kNoAllocRopeChunk = 16384;  // floats staged per table upload
 
 // What one device's scratch holds across calls: the RoPE tables and the tile
@@ -216,7 +224,7 @@ struct NoAllocBwd {
 // waits for the whole device, since any earlier call may still read them.
 // Every other region is written by the call's own kernels before it is read.
 NoAllocBwd noalloc_bwd_workspace(int device, void* base, const ShapeArgs& s, int n_cu,
-                                 bool split_ok) {
+                                 bool split_ok, bool head_pairs) {
   if (s.n_seqs > kNoAllocMaxSeqs)
     fail(GLACIER_ATTN_ERR_UNSUPPORTED, "the allocation-free backward takes at most " +
                                            std::to_string(kNoAllocMaxSeqs) + " sequences per call");
@@ -249,9 +257,11 @@ NoAllocBwd noalloc_bwd_workspace(int device, void* base, const ShapeArgs& s, int
   const size_t off_tiles = 2 * rope_bytes;
   // the wide backward's table, for the tensors and head sizes it takes
   int n_wide = 0;
+  const std::vector<int> wkinds = wide_kinds(head_pairs);
+  const int per_wide = static_cast<int>(wkinds.size());  // entries per 128-row tile
   if (s.io_bf16 && (s.head_dim == 64 || s.head_dim == 128))
     for (int b = 0; b < s.n_seqs; ++b)
-      n_wide += 2 * ((s.seq_start(b + 1) - s.seq_start(b) + kWideTile - 1) / kWideTile);
+      n_wide += per_wide * ((s.seq_start(b + 1) - s.seq_start(b) + kWideTile - 1) / kWideTile);
   const size_t n_entries = 2 * static_cast<size_t>(n_tiles) + n_split_entries + n_wide;
   const size_t off_pos = off_tiles + align256(n_entries * sizeof(TileDesc));
   const size_t off_stats = off_pos + align256(T * sizeof(int32_t));
@@ -348,7 +358,7 @@ NoAllocBwd noalloc_bwd_workspace(int device, void* base, const ShapeArgs& s, int
         for (int b = 0; b < s.n_seqs; ++b) {
           const int len = s.seq_start(b + 1) - s.seq_start(b);
           for (int t = 0; t < (len + kWideTile - 1) / kWideTile; ++t)
-            for (int kind = 0; kind < 2; ++kind) ++g_noalloc_count[bwd_wide_cost(len, t, kind)];
+            for (int kind : wkinds) ++g_noalloc_count[bwd_wide_cost(len, t, kind, head_pairs)];
         }
         int at = 0;
         for (int c = kNoAllocMaxWideCost; c >= 0; --c) {
@@ -359,8 +369,8 @@ NoAllocBwd noalloc_bwd_workspace(int device, void* base, const ShapeArgs& s, int
         for (int b = 0; b < s.n_seqs; ++b) {
           const int tok0 = s.seq_start(b), len = s.seq_start(b + 1) - tok0;
           for (int t = 0; t < (len + kWideTile - 1) / kWideTile; ++t)
-            for (int kind = 0; kind < 2; ++kind)
-              out[g_noalloc_count[bwd_wide_cost(len, t, kind)]++] = TileDesc{tok0, len, t, kind};
+            for (int kind : wkinds)
+              out[g_noalloc_count[bwd_wide_cost(len, t, kind, head_pairs)]++] = TileDesc{tok0, len, t, kind};
         }
       }
       check_hip(hipMemcpy(sb + off_tiles, g_noalloc_tiles, n_entries * sizeof(TileDesc),
@@ -406,6 +416,8 @@ struct TileSet {
   int split_at[kBwdMaxSplit + 1] = {};       // entry offset of each split table (0: none)
   int split_entries[kBwdMaxSplit + 1] = {};  // and its length
   int wide_at = 0, wide_entries = 0;         // the 128-row backward table (attn_bwd3.hip)
+  int wide2_at = 0, wide2_entries = 0;       // the same over query-head pairs
+  int wide_tiles = 0;                        // 128-row tiles: sum of ceil(len / 128)
   std::vector<int> seq_tiles;                // tiles of each sequence
   DeviceBuffer pos;    // [T] int32
 };
@@ -449,6 +461,17 @@ class GpuAttentionEngine {
       else if (m != "auto" && !m.empty())
         fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT,
              "GLACIER_ATTN_BWD_SPLIT must be auto or 0, not " + m);
+    }
+    // GLACIER_ATTN_BWD_PAIRS=1 makes the wide backward's workgroups take two
+    // query heads of a group each (one dK/dV partial per head pair), 0 one;
+    // unset or "auto" decides per call (head_pairs_for).
+    if (const char* v = std::getenv("GLACIER_ATTN_BWD_PAIRS")) {
+      const std::string m(v);
+      if (m == "1") bwd_pairs_mode_ = 1;
+      else if (m == "0") bwd_pairs_mode_ = 0;
+      else if (m != "auto" && !m.empty())
+        fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT,
+             "GLACIER_ATTN_BWD_PAIRS must be auto, 0 or 1, not " + m);
     }
     // GLACIER_ATTN_FWD_ROWS=32|64 pins the bf16 forward's query rows per
     // workgroup; unset or "auto" takes 32 when 64-row workgroups would
@@ -534,6 +557,20 @@ class GpuAttentionEngine {
     check_hip(launch_forward(a, stream(), &timer_), "attention forward launch");
   }
 
+  // Whether the wide backward takes query heads in pairs.  Measured (one box,
+  // backward calls): 32/8 heads, B=2 x S=1024 132 -> 120 us, B=2 x S=2048
+  // 370 -> 337 us, S=4096 580 -> 551 us; slower where halving the dK/dV
+  // workgroups leaves the chip short of them (16/2 heads at S=2048: 72 ->
+  // 118 us) and no gain with an odd group (28/4 heads: one head of every
+  // group alone, S=1024 60 -> 75 us, S=4096 511 -> 514 us).  So: an even
+  // group and at least one pair workgroup per CU.
+  bool head_pairs_for(int n_heads_q, int n_heads_kv, int wide_tiles) const {
+    if (bwd_pairs_mode_ >= 0) return bwd_pairs_mode_ == 1;
+    const int ratio = n_heads_q / n_heads_kv;
+    return ratio >= 2 && ratio % 2 == 0 &&
+           static_cast<long long>(ratio / 2) * n_heads_kv * wide_tiles >= n_cu_;
+  }
+
   // Shape part of a backward launch (pointers are filled by the caller).
   BwdLaunch bwd_launch_of(const BwdCall& c) const {
     BwdLaunch a{};
@@ -577,8 +614,9 @@ class GpuAttentionEngine {
     if (s.io_bf16) a.stats = stats_.ensure((T * Hq + 64) * 2 * sizeof(float), "row stats");
     const TileDesc* t = static_cast<const TileDesc*>(ts.tiles.ptr);
     a.tiles_bwd = t + ts.n_tiles;
-    a.tiles_wide = t + ts.wide_at;
-    a.n_wide_entries = ts.wide_entries;
+    a.dkdv_head_pairs = head_pairs_for(s.n_heads_q, s.n_heads_kv, ts.wide_tiles);
+    a.tiles_wide = t + (a.dkdv_head_pairs ? ts.wide2_at : ts.wide_at);
+    a.n_wide_entries = a.dkdv_head_pairs ? ts.wide2_entries : ts.wide_entries;
     // the longest dK/dV tiles in query halves while the launch fits the CUs
     const int split =
         split_ok_ ? bwd_split_of(s.io_bf16, s.n_heads_q, static_cast<int>(ts.seq_tiles.size()),
@@ -616,10 +654,15 @@ class GpuAttentionEngine {
       }
       base = noalloc_scratch(device_);
     }
-    NoAllocBwd w = noalloc_bwd_workspace(device_, base, s, n_cu_, split_ok_);
+    int wide_tiles = 0;
+    for (int b = 0; b < s.n_seqs; ++b)
+      wide_tiles += (s.seq_start(b + 1) - s.seq_start(b) + kWideTile - 1) / kWideTile;
+    const bool head_pairs = head_pairs_for(s.n_heads_q, s.n_heads_kv, wide_tiles);
+    NoAllocBwd w = noalloc_bwd_workspace(device_, base, s, n_cu_, split_ok_, head_pairs);
     BwdLaunch a = bwd_launch_of(BwdCall{s.total_tokens, s.n_heads_q, s.n_heads_kv, s.head_dim,
                                         s.precision, s.io_bf16, s.n_seqs == 1, w.n_tiles,
                                         w.pairs});
+    a.dkdv_head_pairs = head_pairs;
     a.d_out = d_out; a.q_rot = q_rot; a.k_rot = k_rot; a.v = v; a.out = out;
     a.lse = lse; a.dq = dq; a.dk = dk; a.dv = dv;
     a.wk = w.wk;
@@ -883,22 +926,26 @@ class GpuAttentionEngine {
     }
     // the 128-row backward table: dK/dV tiles of 128 keys and dQ tiles of 128
     // queries, longest expected first (bwd_wide_cost)
-    {
+    // (and the same over query-head pairs: each dQ tile twice)
+    for (const bool head_pairs : {false, true}) {
       std::vector<std::pair<int, TileDesc>> bw;
+      int wide_tiles = 0;
       for (int b = 0; b < n; ++b) {
         const int tok0 = s.cu[b], len = s.cu[b + 1] - s.cu[b];
         if (len <= 0) continue;
         const int nt = (len + kWideTile - 1) / kWideTile;
+        wide_tiles += nt;
         for (int t = 0; t < nt; ++t)
-          for (int kind = 0; kind < 2; ++kind)
-            bw.push_back({bwd_wide_cost(len, t, kind), TileDesc{tok0, len, t, kind}});
+          for (int kind : wide_kinds(head_pairs))
+            bw.push_back({bwd_wide_cost(len, t, kind, head_pairs), TileDesc{tok0, len, t, kind}});
       }
       std::stable_sort(bw.begin(), bw.end(),
                        [](const std::pair<int, TileDesc>& x, const std::pair<int, TileDesc>& y) {
                          return x.first > y.first;
                        });
-      ts->wide_at = static_cast<int>(all.size());
-      ts->wide_entries = static_cast<int>(bw.size());
+      (head_pairs ? ts->wide2_at : ts->wide_at) = static_cast<int>(all.size());
+      (head_pairs ? ts->wide2_entries : ts->wide_entries) = static_cast<int>(bw.size());
+      ts->wide_tiles = wide_tiles;
       for (const auto& e : bw) all.push_back(e.second);
     }
     ts->tiles.ensure(all.size() * sizeof(TileDesc), "tile table");
@@ -952,6 +999,7 @@ class GpuAttentionEngine {
   int n_cu_ = 0;          // compute units of the device
   bool split_ok_ = true;  // dK/dV tiles may be split (GLACIER_ATTN_BWD_SPLIT)
   int fwd_rows_ = 0;      // bf16 forward rows per workgroup (GLACIER_ATTN_FWD_ROWS; 0: auto)
+  int bwd_pairs_mode_ = -1;  // wide backward over head pairs: 1 on, 0 off, -1 auto (GLACIER_ATTN_BWD_PAIRS)
   // projection scratch and the hipBLASLt handle (created on first use)
   DeviceBuffer yf_, dxf_, lowrank_, part_;
   DeviceBuffer rstd_, dyw_;  // RMSNorm backward row scales, dy copy (weight gradient)

@@ -176,7 +176,8 @@ int glacier_attn_backward(glacier_attn_ctx *ctx, const glacier_attn_desc *desc,
  *   tile and position tables   32 * tiles + 32 * wtiles + 4 * T
  *                              (tiles: sum of ceil(len/64); wtiles: sum of
  *                              ceil(len/128) for bf16 tensors at head_dim 64
- *                              or 128, else 0)
+ *                              or 128, else 0; 48 * wtiles when the wide
+ *                              backward takes query heads in pairs)
  *   row stats (bf16 tensors)   8 * (T * Hq + 64)
  *   dK and dV partials         2 x esz * T * Hq * D        (esz 2 bf16, 4 fp32 tensors)
  * A call that needs more, or has more than 1024 sequences or 65536 tokens,

@@ -45,25 +45,37 @@ def engines():
     e16.close()
 
 
-BWD_KERNELS = ("rows16", "rows32", "mfma32")
+BWD_KERNELS = ("rows16", "rows32", "mfma32", "mfma32_pairs")
+# the environment that pins each (read when an engine is created);
+# mfma32_pairs: the wide kernel with dK/dV tiles over head pairs
+BWD_ENV = {
+    "rows16": {"GLACIER_ATTN_BWD": "rows16", "GLACIER_ATTN_BWD_PAIRS": "0"},
+    "rows32": {"GLACIER_ATTN_BWD": "rows32", "GLACIER_ATTN_BWD_PAIRS": "0"},
+    "mfma32": {"GLACIER_ATTN_BWD": "mfma32", "GLACIER_ATTN_BWD_PAIRS": "0"},
+    "mfma32_pairs": {"GLACIER_ATTN_BWD": "mfma32", "GLACIER_ATTN_BWD_PAIRS": "1"},
+}
+
+
+def pinned_engine(name, precision=None):
+    """An engine created under BWD_ENV[name]."""
+    env = BWD_ENV[name]
+    old = {key: os.environ.get(key) for key in env}
+    try:
+        os.environ.update(env)
+        return ga.GpuAttentionEngine(0, ga.PREC_BF16 if precision is None else precision)
+    finally:
+        for key, val in old.items():
+            if val is None:
+                os.environ.pop(key, None)
+            else:
+                os.environ[key] = val
 
 
 @pytest.fixture(scope="module")
 def bf16_kernels():
-    """bf16-mode engines pinned to each backward kernel for bf16 tensors
-    (GLACIER_ATTN_BWD is read when an engine is created)."""
+    """bf16-mode engines pinned to each backward kernel for bf16 tensors."""
     assert torch.cuda.is_available(), "GPU tests need a ROCm GPU"
-    made = {}
-    old = os.environ.get("GLACIER_ATTN_BWD")
-    try:
-        for name in BWD_KERNELS:
-            os.environ["GLACIER_ATTN_BWD"] = name
-            made[name] = ga.GpuAttentionEngine(0, ga.PREC_BF16)
-    finally:
-        if old is None:
-            os.environ.pop("GLACIER_ATTN_BWD", None)
-        else:
-            os.environ["GLACIER_ATTN_BWD"] = old
+    made = {name: pinned_engine(name) for name in BWD_KERNELS}
     yield made
     for e in made.values():
         e.close()
@@ -229,6 +241,36 @@ def test_split_dkdv_tiles_match_whole_tiles(engines, case):
     assert np.array_equal(got_s["dq"], got_w["dq"])
     for key in ("dk", "dv"):
         assert oracle.max_rel_err(got_s[key], got_w[key]) <= BF16_GATE, key
+
+
+@pytest.mark.parametrize("case", ["s1100_g7", "packed_g4", "g1", "g3"])
+def test_wide_backward_head_pairs_match_single_heads(bf16_kernels, case):
+    """The wide backward with each dK/dV tile walking two query heads of its
+    group (one partial per pair; the head reduction sums every second head)
+    against one head per tile: dq bit-identical (the dQ tiles do not change),
+    dk and dv within the bf16 gate of each other, both within the gate of the
+    oracle.  Groups of 7 (a last head alone), 4, 1 (no pair) and 3; a packed
+    batch with sequences shorter than one 128-row tile."""
+    lens, Hq, Hkv, D, base = {
+        "s1100_g7": ([1100], 14, 2, 128, 1.0e6),
+        "packed_g4": ([300, 1, 77, 530], 8, 2, 64, 5.0e5),
+        "g1": ([700], 2, 2, 128, 1.0e4),
+        "g3": ([129, 385], 6, 2, 64, 1.0e4),
+    }[case]
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    q, k, v, dO = make_inputs(int(cu[-1]), Hq, Hkv, D, 11, True)
+    ref = oracle.layer_fwd_bwd_varlen(q, k, v, dO, cu, base)
+    _say(f"[wide backward head pairs] {case}")
+    cuv = None if len(lens) == 1 else cu
+    got_p = run_device(bf16_kernels["mfma32_pairs"], q, k, v, dO, base, torch.bfloat16, cu=cuv)
+    got_1 = run_device(bf16_kernels["mfma32"], q, k, v, dO, base, torch.bfloat16, cu=cuv)
+    err_p, err_1 = errors(got_p, ref), errors(got_1, ref)
+    _say(f"  pairs {err_p}\n  single {err_1}")
+    assert all(e <= BF16_GATE for e in err_p.values()), err_p
+    assert all(e <= BF16_GATE for e in err_1.values()), err_1
+    assert np.array_equal(got_p["dq"], got_1["dq"])
+    for key in ("dk", "dv"):
+        assert oracle.max_rel_err(got_p[key], got_1[key]) <= BF16_GATE, key
 
 
 @pytest.fixture(scope="module")

@@ -12,7 +12,8 @@ one mode:
                for the oracle too): gate 2e-2
   bf16_f32io   fp32 device tensors of bf16-rounded values, bf16 math: 2e-2
   rows16/32,   bf16 device tensors with each bf16 backward kernel pinned
-  mfma32       (head sizes 64 and 128 only) and 64-query forward
+  mfma32,      (head sizes 64 and 128 only; mfma32_pairs: the wide kernel
+  mfma32_pairs with dK/dV tiles over head pairs) and 64-query forward
                workgroups: 2e-2
 The same seed always gives the same cases; each prints its draw first.
 """
@@ -35,7 +36,7 @@ EDGE_LENS = [1, 15, 16, 17, 31, 32, 33, 63, 64, 65, 127, 128, 129, 191, 255, 256
              384, 385, 511, 512, 513]
 HEADS = [(1, 1), (2, 1), (3, 3), (4, 2), (6, 3), (7, 1), (8, 2), (12, 3), (14, 2), (28, 4)]
 DIMS = [32, 64, 96, 128, 256]
-MODES = ["fp32", "bf16", "bf16_f32io", "rows16", "rows32", "mfma32"]
+MODES = ["fp32", "bf16", "bf16_f32io", "rows16", "rows32", "mfma32", "mfma32_pairs"]
 
 
 def _draw_cases(n=60, seed=20261202):
@@ -49,7 +50,7 @@ def _draw_cases(n=60, seed=20261202):
         mode = MODES[i % len(MODES)]
         if mode == "fp32" and d > 128:
             d = 128  # fp32 operands stop at 128
-        if mode in ("rows16", "rows32", "mfma32") and d not in (64, 128):
+        if mode in ("rows16", "rows32", "mfma32", "mfma32_pairs") and d not in (64, 128):
             d = 64 if d < 128 else 128  # the pinned kernels' head sizes
         if d == 256 and hq > 8:
             hq, hkv = 8, 2  # keeps the oracle's share of the run short
@@ -73,11 +74,13 @@ def engines():
             "bf16": ga.GpuAttentionEngine(0, ga.PREC_BF16)}
     # the pinned-backward engines also pin 64-query forward workgroups, which
     # "auto" replaces by 32-query ones on most of these small launches
-    old = {key: os.environ.get(key) for key in ("GLACIER_ATTN_BWD", "GLACIER_ATTN_FWD_ROWS")}
+    keys = ("GLACIER_ATTN_BWD", "GLACIER_ATTN_FWD_ROWS", "GLACIER_ATTN_BWD_PAIRS")
+    old = {key: os.environ.get(key) for key in keys}
     try:
         os.environ["GLACIER_ATTN_FWD_ROWS"] = "64"
-        for name in ("rows16", "rows32", "mfma32"):
-            os.environ["GLACIER_ATTN_BWD"] = name
+        for name in ("rows16", "rows32", "mfma32", "mfma32_pairs"):
+            os.environ["GLACIER_ATTN_BWD"] = "mfma32" if name == "mfma32_pairs" else name
+            os.environ["GLACIER_ATTN_BWD_PAIRS"] = "1" if name == "mfma32_pairs" else "0"
             made[name] = ga.GpuAttentionEngine(0, ga.PREC_BF16)
     finally:
         for key, val in old.items():

@@ -26,15 +26,20 @@ def _say(msg):
 
 
 def _engine(kernel, precision):
-    old = os.environ.get("GLACIER_ATTN_BWD")
+    """kernel: a GLACIER_ATTN_BWD value, or mfma32_pairs (the wide kernel with
+    dK/dV tiles over head pairs)."""
+    env = {"GLACIER_ATTN_BWD": "mfma32" if kernel == "mfma32_pairs" else kernel,
+           "GLACIER_ATTN_BWD_PAIRS": "1" if kernel == "mfma32_pairs" else "0"}
+    old = {key: os.environ.get(key) for key in env}
     try:
-        os.environ["GLACIER_ATTN_BWD"] = kernel
+        os.environ.update(env)
         return ga.GpuAttentionEngine(0, precision)
     finally:
-        if old is None:
-            os.environ.pop("GLACIER_ATTN_BWD", None)
-        else:
-            os.environ["GLACIER_ATTN_BWD"] = old
+        for key, val in old.items():
+            if val is None:
+                os.environ.pop(key, None)
+            else:
+                os.environ[key] = val
 
 
 def _inputs(lens, hq, hkv, d, dtype, seed):
@@ -101,7 +106,7 @@ CALLS_LONG = [
 ]
 
 
-@pytest.mark.parametrize("kernel", ["auto", "mfma32"])
+@pytest.mark.parametrize("kernel", ["auto", "mfma32", "mfma32_pairs"])
 def test_noalloc_backward_long_sequences_match_backward_bitwise(kernel):
     eng = _engine(kernel, ga.PREC_BF16)
     try:
