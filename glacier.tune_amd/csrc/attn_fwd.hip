@@ -104,7 +104,7 @@ __global__ __launch_bounds__(kFwdWaves * 64) void attn_fwd_kernel_ks(
   constexpr int NDB = D / 16;
   constexpr int H = D / 2;
   constexpr int NT = kFwdWaves * 64;
-  static_assert(QB == 4 || QB == 2, "16-query blocks per workgroup");
+  static_assert(QB == 4 || QB == 2 || QB == 1, "16-query blocks per workgroup");
   constexpr int TR = 16 * QB;       // query rows of the workgroup
   constexpr int NSUB = kTile / TR;  // workgroups per 64-row table entry
   constexpr int NDMA = 2 * (kChunk * D / 512);  // DMA instructions per chunk (K and V)
@@ -579,6 +579,7 @@ __global__ __launch_bounds__(kFwdWaves * 64) void attn_fwd_kernel_ks(
     };
     if (w == 0) {
       sum_block(std::integral_constant<int, 0>{});
+    } else if constexpr (QB == 1) {
     } else if (w == 1) {
       sum_block(std::integral_constant<int, 1>{});
     } else if constexpr (QB == 4) {
@@ -603,9 +604,10 @@ __global__ __launch_bounds__(kFwdWaves * 64) void attn_fwd_kernel_ks(
 template <typename IO, int D>
 hipError_t launch_fwd_bf16(const FwdLaunch& a, hipStream_t st, KernelTimer* tm) {
   // 32-query workgroups (two per table entry) when the launch is short of CUs
-  const bool rows32 = a.tile_rows == 32;
-  auto fn = a.single_seq ? (rows32 ? attn_fwd_kernel_ks<IO, D, false, 2> : attn_fwd_kernel_ks<IO, D, false, 4>)
-                         : (rows32 ? attn_fwd_kernel_ks<IO, D, true, 2> : attn_fwd_kernel_ks<IO, D, true, 4>);
+  const int nsub = a.tile_rows == 16 ? 4 : a.tile_rows == 32 ? 2 : 1;  // workgroups per 64-row tile
+  auto fn = a.single_seq ? attn_fwd_kernel_ks<IO, D, false, 4> : attn_fwd_kernel_ks<IO, D, true, 4>;
+  if (nsub == 2) fn = a.single_seq ? attn_fwd_kernel_ks<IO, D, false, 2> : attn_fwd_kernel_ks<IO, D, true, 2>;
+  if (nsub == 4) fn = a.single_seq ? attn_fwd_kernel_ks<IO, D, false, 1> : attn_fwd_kernel_ks<IO, D, true, 1>;
   constexpr size_t lds = FwdLayout<D>::BYTES;
   GL_CHECK(allow_lds(fn, lds));
   // the tables are one allocation: the sine table's offset in floats
@@ -613,7 +615,7 @@ hipError_t launch_fwd_bf16(const FwdLaunch& a, hipStream_t st, KernelTimer* tm) 
   if (sin_off <= 0 || sin_off > INT32_MAX) return hipErrorInvalidValue;
   const int group = a.n_heads_q / a.n_heads_kv;
   LaunchTiming t(tm, kKernFwd);
-  GL_LAUNCH(t, fn, dim3(group, a.n_heads_kv, a.n_tiles * (rows32 ? 2 : 1)), dim3(kFwdWaves * 64), lds,
+  GL_LAUNCH(t, fn, dim3(group, a.n_heads_kv, a.n_tiles * nsub), dim3(kFwdWaves * 64), lds,
                         st, a.total_tokens, a.n_heads_kv, group, static_cast<int>(sin_off),
                         static_cast<const bf16*>(a.kc),
                         static_cast<const bf16*>(a.vc != nullptr ? a.vc : a.v), a.tiles_fwd,

@@ -142,8 +142,8 @@ struct FwdLaunch {
   bool single_seq;               // one sequence: tile order is computed in-kernel
   int head_dim, n_heads_q, n_heads_kv, total_tokens;
   int n_tiles;
-  // query rows per workgroup of the bf16 forward: 64, or 32 (two workgroups
-  // per tile) for launches that would otherwise leave most CUs idle
+  // query rows per workgroup of the bf16 forward: 64, or 32 or 16 (two or
+  // four workgroups per tile) for launches that would otherwise leave CUs idle
   int tile_rows;
   float scale_log2;
   const void *q, *k, *v;

@@ -473,16 +473,16 @@ class GpuAttentionEngine {
         fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT,
              "GLACIER_ATTN_BWD_PAIRS must be auto, 0 or 1, not " + m);
     }
-    // GLACIER_ATTN_FWD_ROWS=32|64 pins the bf16 forward's query rows per
-    // workgroup; unset or "auto" takes 32 when 64-row workgroups would
-    // leave at least half of the CUs idle.
+    // GLACIER_ATTN_FWD_ROWS=16|32|64 pins the bf16 forward's query rows per
+    // workgroup; unset or "auto" decides per call (fwd_rows_for).
     if (const char* v = std::getenv("GLACIER_ATTN_FWD_ROWS")) {
       const std::string m(v);
       if (m == "32") fwd_rows_ = 32;
+      else if (m == "16") fwd_rows_ = 16;
       else if (m == "64") fwd_rows_ = 64;
       else if (m != "auto" && !m.empty())
         fail(GLACIER_ATTN_ERR_INVALID_ARGUMENT,
-             "GLACIER_ATTN_FWD_ROWS must be auto, 32 or 64, not " + m);
+             "GLACIER_ATTN_FWD_ROWS must be auto, 16, 32 or 64, not " + m);
     }
   }
 
@@ -535,8 +535,7 @@ class GpuAttentionEngine {
     a.n_heads_kv = s.n_heads_kv;
     a.total_tokens = s.total_tokens;
     a.n_tiles = ts.n_tiles;
-    a.tile_rows = fwd_rows_ != 0 ? fwd_rows_
-                  : 2LL * s.n_heads_q * ts.n_tiles <= n_cu_ ? 32 : 64;
+    a.tile_rows = fwd_rows_ != 0 ? fwd_rows_ : fwd_rows_for(s.n_heads_q, ts.n_tiles, s.head_dim);
     a.scale_log2 = kLog2e / std::sqrt(static_cast<float>(s.head_dim));
     a.q = q; a.k = k; a.v = v;
     a.out = out; a.lse = lse; a.q_rot = q_rot; a.k_rot = k_rot;
@@ -555,6 +554,21 @@ class GpuAttentionEngine {
     a.cos_t = rope_cos();
     a.sin_t = rope_sin();
     check_hip(launch_forward(a, stream(), &timer_), "attention forward launch");
+  }
+
+  // Query rows per workgroup of the bf16 forward: the fewest of 16 and 32
+  // whose workgroups still fit the chip at once (two per CU where head_dim
+  // 64 leaves room in the LDS, one at 128; 32 rows only one per CU), else
+  // 64.  Measured (bench.py, one box): qwen05b S=512 forward 9.5 -> 7.2 us at
+  // 32 rows -> 6.6-6.9 us at 16; where the 64-row grid already fills the chip
+  // fewer rows are slower (qwen7b S=512: 13.3, 14.2 and 19.8 us at 64, 32
+  // and 16 rows).
+  int fwd_rows_for(int n_heads_q, int n_tiles, int head_dim) const {
+    const long long units = static_cast<long long>(n_heads_q) * n_tiles;  // 64-row tiles
+    const int per_cu = head_dim <= 64 ? 2 : 1;
+    if (4 * units <= static_cast<long long>(per_cu) * n_cu_) return 16;
+    if (2 * units <= n_cu_) return 32;
+    return 64;
   }
 
   // Whether the wide backward takes query heads in pairs.  Measured (one box,

@@ -275,13 +275,13 @@ def test_wide_backward_head_pairs_match_single_heads(bf16_kernels, case):
 
 @pytest.fixture(scope="module")
 def fwd_rows():
-    """bf16-mode engines pinned to 32- and 64-query forward workgroups
+    """bf16-mode engines pinned to 16-, 32- and 64-query forward workgroups
     (GLACIER_ATTN_FWD_ROWS is read when an engine is created)."""
     assert torch.cuda.is_available(), "GPU tests need a ROCm GPU"
     made = {}
     old = os.environ.get("GLACIER_ATTN_FWD_ROWS")
     try:
-        for rows in ("32", "64"):
+        for rows in ("16", "32", "64"):
             os.environ["GLACIER_ATTN_FWD_ROWS"] = rows
             made[rows] = ga.GpuAttentionEngine(0, ga.PREC_BF16)
     finally:
@@ -296,16 +296,16 @@ def fwd_rows():
 
 @pytest.mark.parametrize("dtype", ["bf16", "fp32"])
 @pytest.mark.parametrize("case", ["qwen05b_s512", "qwen7b_s512", "packed"])
-def test_forward_32_row_workgroups_match_64_row_workgroups(fwd_rows, case, dtype):
-    """The bf16 forward with two 32-query workgroups per 64-query tile (taken
-    when 64-row workgroups would leave half of the CUs idle) against 64-row
-    workgroups.  A query's scores, probabilities and partial sums come from
-    the same wave over the same key chunks in both, and the one extra chunk a
-    64-row workgroup walks for its first 32 queries is masked to exact zeros,
-    so out, lse and q_rot are bit-identical (no rescue pass: N(0, 1) inputs).
-    Both match the oracle.  The packed batch has a sequence of 70 tokens
-    (its second tile's later 32-query workgroup has no queries and returns)
-    and one of a single token."""
+def test_forward_narrow_workgroups_match_64_row_workgroups(fwd_rows, case, dtype):
+    """The bf16 forward with two 32-query or four 16-query workgroups per
+    64-query tile (taken when 64-row workgroups would leave CUs idle) against
+    64-row workgroups.  A query's scores, probabilities and partial sums come
+    from the same wave over the same key chunks in all three, and the chunks
+    a larger workgroup walks past its first queries' diagonal are masked to
+    exact zeros, so out, lse and q_rot are bit-identical (no rescue pass:
+    N(0, 1) inputs).  All match the oracle.  The packed batch has a sequence
+    of 70 tokens (its second tile's later workgroups have no queries and
+    return) and one of a single token."""
     if case == "packed":
         Hq, Hkv, D, base = 14, 2, 128, 1.0e4
         cu = np.array([0, 70, 103, 233, 234], np.int32)
@@ -317,13 +317,14 @@ def test_forward_32_row_workgroups_match_64_row_workgroups(fwd_rows, case, dtype
         cu = None
     _say(f"[forward rows 32 vs 64] {case} {dtype} tensors")
     tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
-    got = {rows: run_device(fwd_rows[rows], q, k, v, dO, base, tdt, cu=cu) for rows in ("32", "64")}
+    got = {rows: run_device(fwd_rows[rows], q, k, v, dO, base, tdt, cu=cu) for rows in ("16", "32", "64")}
     for rows, g in got.items():
         err = errors(g, ref)
         _say(f"  rows {rows}: {err}")
         assert all(e <= BF16_GATE for e in err.values()), (rows, err)
-    for key in ("out", "lse", "q_rot"):
-        assert np.array_equal(got["32"][key], got["64"][key]), key
+    for rows in ("16", "32"):
+        for key in ("out", "lse", "q_rot"):
+            assert np.array_equal(got[rows][key], got["64"][key]), (rows, key)
 
 
 @pytest.mark.parametrize("kernel", BWD_KERNELS)
