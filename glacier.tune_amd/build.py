@@ -38,6 +38,7 @@ SOURCES = {
     "attn_bwd.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form"),
     "attn_bwd3.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form"),
     "attn_noalloc.hip": (),
+    "attn_pad.hip": (),
     "blas_lt.cpp": (),
     "proj_lora.hip": (),
     "proj_gemm.hip": (),

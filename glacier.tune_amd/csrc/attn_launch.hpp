@@ -253,6 +253,15 @@ hipError_t launch_bwd2(const BwdLaunch& a, hipStream_t st, KernelTimer* tm);
 template <int D>
 hipError_t launch_bwd3(const BwdLaunch& a, hipStream_t st, KernelTimer* tm);
 
+// Head sizes the kernels are not built for (attn_pad.hip): rows of d
+// elements padded to dp (a built size) with the rotation halves kept apart
+// (columns 0 .. d/2 - 1 and dp/2 .. dp/2 + d/2 - 1, an odd d's last element
+// at d/2, zeros elsewhere), and back; rows: tokens x heads; bf16 or float.
+hipError_t launch_pad_rows(bool io_bf16, const void* src, void* dst, long rows, int d, int dp,
+                           hipStream_t st);
+hipError_t launch_unpad_rows(bool io_bf16, const void* src, void* dst, long rows, int d, int dp,
+                             hipStream_t st);
+
 // Kernels whose dynamic LDS exceeds 64 KB must say so before their launch.
 template <typename F>
 hipError_t allow_lds(F* fn, size_t bytes) {

@@ -88,6 +88,7 @@ struct DeviceBuffer {
 struct Shape {
   int total_tokens = 0;
   int n_heads_q = 0, n_heads_kv = 0, head_dim = 0;
+  int real_dim = 0;  // the call's head size when head_dim is its padded one (0: head_dim)
   float rope_freq_base = 0.0f;
   int precision = 0;
   bool io_bf16 = false;
@@ -502,8 +503,13 @@ class GpuAttentionEngine {
   static bool SupportsAttention(int seq_len, int head_dim) {
     return SupportedHeadDim(head_dim) && seq_len >= 1 && seq_len <= GLACIER_ATTN_MAX_SEQ_LEN;
   }
-  static bool SupportedHeadDim(int d) {
-    return d == 32 || d == 64 || d == 96 || d == 128 || d == 256;
+  // The kernels are built for head sizes 32, 64, 96, 128 and 256; any other
+  // size from 1 to 256 runs them on rows padded to the next of those.
+  static bool SupportedHeadDim(int d) { return d >= 1 && d <= 256; }
+  static int PaddedHeadDim(int d) {
+    for (int n : {32, 64, 96, 128, 256})
+      if (d <= n) return n;
+    return 0;
   }
 
   std::mutex& lock() { return mutex_; }
@@ -522,8 +528,34 @@ class GpuAttentionEngine {
   void LaunchAttnTrainFwd(const Shape& s, const void* q, const void* k, const void* v,
                           void* out, float* lse, void* q_rot, void* k_rot) {
     if (s.total_tokens == 0) return;
+    const int dp = PaddedHeadDim(s.head_dim);
+    if (dp != s.head_dim) {
+      // a head size the kernels are not built for: padded rows (attn_pad.hip)
+      const bool bf = s.io_bf16;
+      const long rq = (long)s.total_tokens * s.n_heads_q, rk = (long)s.total_tokens * s.n_heads_kv;
+      const int d = s.head_dim;
+      const size_t esz = bf ? 2 : 4;
+      void* qp = pad_q_.ensure(rq * dp * esz, "padded q");
+      void* kp = pad_k_.ensure(rk * dp * esz, "padded k");
+      void* vp = pad_v_.ensure(rk * dp * esz, "padded v");
+      void* op = pad_o_.ensure(rq * dp * esz, "padded out");
+      void* qrp = q_rot != nullptr ? pad_qr_.ensure(rq * dp * esz, "padded q_rot") : nullptr;
+      void* krp = k_rot != nullptr ? pad_kr_.ensure(rk * dp * esz, "padded k_rot") : nullptr;
+      check_hip(launch_pad_rows(bf, q, qp, rq, d, dp, stream()), "pad q");
+      check_hip(launch_pad_rows(bf, k, kp, rk, d, dp, stream()), "pad k");
+      check_hip(launch_pad_rows(bf, v, vp, rk, d, dp, stream()), "pad v");
+      Shape sp = s;
+      sp.head_dim = dp;
+      sp.real_dim = d;
+      LaunchAttnTrainFwd(sp, qp, kp, vp, op, lse, qrp, krp);
+      check_hip(launch_unpad_rows(bf, op, out, rq, d, dp, stream()), "unpad out");
+      if (q_rot != nullptr) check_hip(launch_unpad_rows(bf, qrp, q_rot, rq, d, dp, stream()), "unpad q_rot");
+      if (k_rot != nullptr) check_hip(launch_unpad_rows(bf, krp, k_rot, rk, d, dp, stream()), "unpad k_rot");
+      return;
+    }
+    const int dreal = s.real_dim > 0 ? s.real_dim : s.head_dim;
     const TileSet& ts = tiles_for(s);
-    EnsureRopeTable(ts.max_len, s.head_dim, s.rope_freq_base);
+    EnsureRopeTable(ts.max_len, s.head_dim, s.rope_freq_base, dreal);
     const size_t esz = compute_elem_size(s.precision, s.io_bf16);
     const size_t io_esz = s.io_bf16 ? 2 : 4;
     FwdLaunch a{};
@@ -536,7 +568,7 @@ class GpuAttentionEngine {
     a.total_tokens = s.total_tokens;
     a.n_tiles = ts.n_tiles;
     a.tile_rows = fwd_rows_ != 0 ? fwd_rows_ : fwd_rows_for(s.n_heads_q, ts.n_tiles, s.head_dim);
-    a.scale_log2 = kLog2e / std::sqrt(static_cast<float>(s.head_dim));
+    a.scale_log2 = kLog2e / std::sqrt(static_cast<float>(dreal));
     a.q = q; a.k = k; a.v = v;
     a.out = out; a.lse = lse; a.q_rot = q_rot; a.k_rot = k_rot;
     // The attention kernel reads rotated K in the compute dtype: the caller's
@@ -608,12 +640,44 @@ class GpuAttentionEngine {
                           const void* k_rot, const void* v, const void* out,
                           const float* lse, void* dq, void* dk, void* dv) {
     if (s.total_tokens == 0) return;
+    const int dp = PaddedHeadDim(s.head_dim);
+    if (dp != s.head_dim) {
+      // a head size the kernels are not built for: padded rows (attn_pad.hip)
+      const bool bf = s.io_bf16;
+      const long rq = (long)s.total_tokens * s.n_heads_q, rk = (long)s.total_tokens * s.n_heads_kv;
+      const int d = s.head_dim;
+      const size_t esz = bf ? 2 : 4;
+      void* dop = pad_do_.ensure(rq * dp * esz, "padded d_out");
+      void* qrp = pad_qr_.ensure(rq * dp * esz, "padded q_rot");
+      void* krp = pad_kr_.ensure(rk * dp * esz, "padded k_rot");
+      void* vp = pad_v_.ensure(rk * dp * esz, "padded v");
+      void* op = pad_o_.ensure(rq * dp * esz, "padded out");
+      void* dqp = pad_dq_.ensure(rq * dp * esz, "padded dq");
+      void* dkp = pad_dk_.ensure(rk * dp * esz, "padded dk");
+      void* dvp = pad_dv_.ensure(rk * dp * esz, "padded dv");
+      check_hip(launch_pad_rows(bf, d_out, dop, rq, d, dp, stream()), "pad d_out");
+      check_hip(launch_pad_rows(bf, q_rot, qrp, rq, d, dp, stream()), "pad q_rot");
+      check_hip(launch_pad_rows(bf, k_rot, krp, rk, d, dp, stream()), "pad k_rot");
+      check_hip(launch_pad_rows(bf, v, vp, rk, d, dp, stream()), "pad v");
+      check_hip(launch_pad_rows(bf, out, op, rq, d, dp, stream()), "pad out");
+      Shape sp = s;
+      sp.head_dim = dp;
+      sp.real_dim = d;
+      LaunchAttnTrainBwd(sp, dop, qrp, krp, vp, op, lse, dqp, dkp, dvp);
+      check_hip(launch_unpad_rows(bf, dqp, dq, rq, d, dp, stream()), "unpad dq");
+      check_hip(launch_unpad_rows(bf, dkp, dk, rk, d, dp, stream()), "unpad dk");
+      check_hip(launch_unpad_rows(bf, dvp, dv, rk, d, dp, stream()), "unpad dv");
+      return;
+    }
+    const int dreal = s.real_dim > 0 ? s.real_dim : s.head_dim;
     const TileSet& ts = tiles_for(s);
-    EnsureRopeTable(ts.max_len, s.head_dim, s.rope_freq_base);
+    EnsureRopeTable(ts.max_len, s.head_dim, s.rope_freq_base, dreal);
     const size_t T = s.total_tokens, Hq = s.n_heads_q, D = s.head_dim;
     BwdLaunch a = bwd_launch_of(BwdCall{s.total_tokens, s.n_heads_q, s.n_heads_kv, s.head_dim,
                                         s.precision, s.io_bf16, s.cu.size() == 2, ts.n_tiles,
                                         ts.pairs});
+    a.scale = 1.0f / std::sqrt(static_cast<float>(dreal));
+    a.scale_log2 = kLog2e * a.scale;
     a.d_out = d_out; a.q_rot = q_rot; a.k_rot = k_rot; a.v = v; a.out = out;
     a.lse = lse; a.dq = dq; a.dk = dk; a.dv = dv;
     // the per-head partials are kept in the tensors' dtype: bf16 tensors get
@@ -854,15 +918,19 @@ class GpuAttentionEngine {
   // per (length capacity, head_dim, theta).  One allocation holds the cosine
   // table and then the sine table (the bf16 forward takes the second as an
   // offset from the first).
-  void EnsureRopeTable(int max_len, int head_dim, float base) {
-    if (max_len <= rope_len_ && head_dim == rope_dim_ && base == rope_base_) return;
+  // real_dim: the call's own head size when head_dim is its padded one (the
+  // angles are those of real_dim, in its first real_dim / 2 columns; the
+  // padded columns rotate by the identity).
+  void EnsureRopeTable(int max_len, int head_dim, float base, int real_dim) {
+    if (max_len <= rope_len_ && head_dim == rope_dim_ && real_dim == rope_real_ && base == rope_base_)
+      return;
     const int len = std::max(max_len, std::min(2 * rope_len_, GLACIER_ATTN_MAX_SEQ_LEN));
-    const int half = head_dim / 2;
-    std::vector<float> cs((size_t)len * half), sn((size_t)len * half);
-    std::vector<float> freq(half);
-    for (int i = 0; i < half; i++) freq[i] = rope_freq(i, head_dim, base);
+    const int half = head_dim / 2, rhalf = real_dim / 2;
+    std::vector<float> cs((size_t)len * half, 1.0f), sn((size_t)len * half, 0.0f);
+    std::vector<float> freq(rhalf);
+    for (int i = 0; i < rhalf; i++) freq[i] = rope_freq(i, real_dim, base);
     for (int pos = 0; pos < len; pos++)
-      for (int i = 0; i < half; i++) {
+      for (int i = 0; i < rhalf; i++) {
         const float theta = static_cast<float>(pos) * freq[i];
         cs[(size_t)pos * half + i] = cosf(theta);
         sn[(size_t)pos * half + i] = sinf(theta);
@@ -875,6 +943,7 @@ class GpuAttentionEngine {
               "rope sin upload");
     rope_len_ = len;
     rope_dim_ = head_dim;
+    rope_real_ = real_dim;
     rope_base_ = base;
   }
 
@@ -1005,10 +1074,12 @@ class GpuAttentionEngine {
   DeviceBuffer rope_;  // [rope_len_][rope_dim_ / 2] cosines, then as many sines
   const float* rope_cos() const { return static_cast<const float*>(rope_.ptr); }
   const float* rope_sin() const { return rope_cos() + (size_t)rope_len_ * (rope_dim_ / 2); }
-  int rope_len_ = 0, rope_dim_ = 0;
+  int rope_len_ = 0, rope_dim_ = 0, rope_real_ = 0;
   float rope_base_ = 0.0f;
   // device-path scratch
   DeviceBuffer kc_, vc_, wk_, wv_, wk2_, wv2_, stats_;
+  // padded copies for head sizes the kernels are not built for
+  DeviceBuffer pad_q_, pad_k_, pad_v_, pad_o_, pad_qr_, pad_kr_, pad_do_, pad_dq_, pad_dk_, pad_dv_;
   int bwd_variant_ = kBwdAuto;
   int n_cu_ = 0;          // compute units of the device
   bool split_ok_ = true;  // dK/dV tiles may be split (GLACIER_ATTN_BWD_SPLIT)
@@ -1067,9 +1138,8 @@ ShapeArgs make_shape_args(int total_tokens, int n_seqs, const int32_t* cu, int h
   for (int b = 0; b < n_seqs; ++b) s.max_len = std::max(s.max_len, s.seq_start(b + 1) - s.seq_start(b));
   if (!GpuAttentionEngine::SupportedHeadDim(d))
     fail(GLACIER_ATTN_ERR_UNSUPPORTED, "head_dim " + std::to_string(d) +
-                                           " is not supported by the GPU kernels (32, 64, 96, "
-                                           "128 or 256)");
-  if (d > 128 && precision == GLACIER_ATTN_PREC_FP32)
+                                           " is not supported by the GPU kernels (1 to 256)");
+  if (GpuAttentionEngine::PaddedHeadDim(d) > 128 && precision == GLACIER_ATTN_PREC_FP32)
     fail(GLACIER_ATTN_ERR_UNSUPPORTED,
          "head_dim " + std::to_string(d) + " runs in GLACIER_ATTN_PREC_BF16 only (its fp32 "
          "key/value tiles do not fit the LDS)");
@@ -1338,6 +1408,10 @@ int glacier_attn_backward_noalloc(glacier_attn_ctx* ctx, const glacier_attn_desc
     const glacier::ShapeArgs s = glacier::make_shape_args(
         desc->total_tokens, desc->n_seqs, desc->cu_seqlens, desc->n_heads_q, desc->n_heads_kv,
         desc->head_dim, desc->rope_freq_base, desc->precision, desc->io_dtype);
+    if (glacier::GpuAttentionEngine::PaddedHeadDim(s.head_dim) != s.head_dim)
+      glacier::fail(GLACIER_ATTN_ERR_UNSUPPORTED,
+                    "the allocation-free backward takes head sizes 32, 64, 96, 128 and 256, not " +
+                        std::to_string(s.head_dim) + " (other sizes need padded copies)");
     need(ctx, "ctx");
     if (s.total_tokens > 0) {
       need(d_out, "d_out"); need(q_rot, "q_rot"); need(k_rot, "k_rot"); need(v, "v");

@@ -98,11 +98,15 @@ void glacier_attn_destroy(glacier_attn_ctx *ctx);
 /* Text of the last failure on the calling thread ("" if none). */
 const char *glacier_attn_last_error(void);
 
-/* 1 if the GPU kernels take this shape, else 0: head_dim 32, 64, 96, 128 or
- * 256 (256 in GLACIER_ATTN_PREC_BF16 only, whose bf16 key/value tiles fit the
- * LDS) and 1 <= seq_len <= GLACIER_ATTN_MAX_SEQ_LEN.  Replaces
+/* 1 if the GPU kernels take this shape, else 0: 1 <= head_dim <= 256 and
+ * 1 <= seq_len <= GLACIER_ATTN_MAX_SEQ_LEN.  The kernels are built for head
+ * sizes 32, 64, 96, 128 and 256; any other size runs them on rows padded to
+ * the next of those (with the RoPE pairs kept, so results are those of the
+ * call's own size).  Sizes padded to 256 run in GLACIER_ATTN_PREC_BF16 only
+ * (fp32 key/value tiles of 256 exceed the LDS), and the allocation-free
+ * backward takes the built sizes only.  Replaces
  * GpuLoraEngine.SupportsAttention (GpuLoraEngine.cs:111-112), which accepts
- * head_dim 1..1024; the other sizes keep the CPU path. */
+ * head_dim 1..1024; sizes above 256 keep the CPU path. */
 int glacier_attn_supports(int seq_len, int head_dim);
 
 /* ---- drop-in entry points: host fp32 tensors ----------------------------- */

@@ -99,8 +99,15 @@ void attention_descriptors() {
     expect(fn(&x), GLACIER_ATTN_ERR_INVALID_ARGUMENT, "Hkv = 0");
     x = desc(9, 1, nullptr, 4, 2, 2000);
     expect(fn(&x), GLACIER_ATTN_ERR_INVALID_ARGUMENT, "head_dim > 1024");
+    x = desc(9, 1, nullptr, 4, 2, 300);
+    expect(fn(&x), GLACIER_ATTN_ERR_UNSUPPORTED, "head_dim 300");
+    // 80 runs on padded rows (only the context is missing), except in the
+    // allocation-free backward, which takes the built sizes only
     x = desc(9, 1, nullptr, 4, 2, 80);
-    expect(fn(&x), GLACIER_ATTN_ERR_UNSUPPORTED, "head_dim 80");
+    expect(fn(&x), fn == call_noalloc ? GLACIER_ATTN_ERR_UNSUPPORTED : GLACIER_ATTN_ERR_INVALID_ARGUMENT,
+           "head_dim 80");
+    x = desc(9, 1, nullptr, 4, 2, 200, GLACIER_ATTN_PREC_FP32, GLACIER_ATTN_IO_F32);
+    expect(fn(&x), GLACIER_ATTN_ERR_UNSUPPORTED, "head_dim 200 (padded to 256) in the fp32 mode");
     x = desc(9, 1, nullptr, 4, 2, 256, GLACIER_ATTN_PREC_FP32, GLACIER_ATTN_IO_F32);
     expect(fn(&x), GLACIER_ATTN_ERR_UNSUPPORTED, "head_dim 256 in the fp32 mode");
     x = desc(9, 1, nullptr, 4, 2, 64, 7);
@@ -126,8 +133,8 @@ void host_entry_points() {
                                    3, 2, 64, 1e4f),
          GLACIER_ATTN_ERR_INVALID_ARGUMENT, "forward_host Hq % Hkv");
   expect(glacier_attn_forward_host(nullptr, 0, q.data(), k.data(), k.data(), out.data(), nullptr, 8,
-                                   2, 2, 80, 1e4f),
-         GLACIER_ATTN_ERR_UNSUPPORTED, "forward_host head_dim 80");
+                                   2, 2, 300, 1e4f),
+         GLACIER_ATTN_ERR_UNSUPPORTED, "forward_host head_dim 300");
   expect(glacier_attn_forward_host(nullptr, 0, q.data(), k.data(), k.data(), out.data(), nullptr, 8,
                                    2, 2, 64, 1e4f),
          GLACIER_ATTN_ERR_INVALID_ARGUMENT, "forward_host without a context");
@@ -191,8 +198,8 @@ void norms_and_lmhead() {
 }
 
 void queries_and_context() {
-  if (glacier_attn_supports(512, 128) != 1 || glacier_attn_supports(512, 80) != 0 ||
-      glacier_attn_supports(0, 64) != 0) {
+  if (glacier_attn_supports(512, 128) != 1 || glacier_attn_supports(512, 80) != 1 ||
+      glacier_attn_supports(512, 300) != 0 || glacier_attn_supports(0, 64) != 0) {
     std::fprintf(stderr, "glacier_attn_supports gate\n");
     g_fail = 1;
   }

@@ -34,7 +34,10 @@ def test_supports_attention_gate():
     assert ga.supports_attention(1, 128)
     for d in (32, 96, 256):
         assert ga.supports_attention(512, d)
-    for d in (80, 160, 512, 1024):
+    # other sizes up to 256 run the kernels on padded rows
+    for d in (1, 7, 80, 127, 160, 255):
+        assert ga.supports_attention(512, d)
+    for d in (0, 257, 512, 1024):
         assert not ga.supports_attention(512, d)
     assert not ga.supports_attention(0, 128)
     assert not ga.supports_attention(65537, 128)
@@ -54,10 +57,14 @@ def test_argument_errors_come_before_any_device_work():
     assert rc == ga.ERR_INVALID_ARGUMENT and "multiple" in msg
     rc, msg = _fwd_host_rc(8, 2, 2, 2000)
     assert rc == ga.ERR_INVALID_ARGUMENT and "headDim" in msg
-    rc, msg = _fwd_host_rc(8, 2, 2, 80)
-    assert rc == ga.ERR_UNSUPPORTED and "80" in msg
+    rc, msg = _fwd_host_rc(8, 2, 2, 300)
+    assert rc == ga.ERR_UNSUPPORTED and "300" in msg
     rc, msg = _fwd_host_rc(8, 2, 2, 256)  # fp32 operands: 256 is bf16-only
     assert rc == ga.ERR_UNSUPPORTED and "BF16" in msg
+    rc, msg = _fwd_host_rc(8, 2, 2, 200)  # padded to 256: bf16-only too
+    assert rc == ga.ERR_UNSUPPORTED and "BF16" in msg
+    rc, msg = _fwd_host_rc(8, 2, 2, 80)  # runs on padded rows: only the context is missing
+    assert rc == ga.ERR_INVALID_ARGUMENT and "ctx" in msg
     rc, msg = _fwd_host_rc(8, 0, 2, 64)
     assert rc == ga.ERR_INVALID_ARGUMENT
     rc, msg = _fwd_host_rc(8, 2, 2, 64, base=-1.0)

@@ -351,16 +351,23 @@ def test_small_and_ragged_shapes(engines, S, Hq, Hkv, D, prec):
     assert all(e <= gate for e in err.values()), err
 
 
+# sizes the kernels are built for (32, 96, 256: the generic 16-row kernels;
+# 64 and 128 are covered above) and sizes that run on padded rows: odd ones
+# (an unrotated last element), one element, and one in each padding range
+HEAD_DIMS = [32, 96, 256, 1, 16, 48, 80, 100, 127, 200]
+
+
 @pytest.mark.parametrize("mode", ["fp32", "bf16_host", "bf16_device"])
-@pytest.mark.parametrize("D", [32, 96, 256])
+@pytest.mark.parametrize("D", HEAD_DIMS)
 def test_head_dims_match_oracle(engines, D, mode):
-    """head_dim 32, 96 and 256 (the generic 16-row kernels; 64 and 128 are
-    covered above): a ragged S=200 (three full tiles and a partial one),
-    GQA 4:1, in each mode.  fp32 operands stop at 128 (UNSUPPORTED above)."""
+    """Head sizes other than 64 and 128: a ragged S=200 (three full tiles and
+    a partial one), GQA 4:1, in each mode; the post-RoPE q and k bit-exact in
+    the fp32 mode and q in the bf16 host mode, as at the built sizes.  fp32
+    operands stop at a padded size of 128 (UNSUPPORTED above)."""
     S, Hq, Hkv, base = 200, 8, 2, 1.0e4
     bf = mode != "fp32"
     _say(f"[head_dim] D={D} mode={mode}")
-    if D > 128 and not bf:
+    if D > 128 and not bf:  # padded to 256
         q = np.zeros((S, Hq, D), np.float32)
         with pytest.raises(ga.Unsupported):
             engines[ga.PREC_FP32].forward_attention(0, q, q[:, :Hkv].copy(), q[:, :Hkv].copy(),
@@ -382,7 +389,7 @@ def test_head_dims_match_oracle(engines, D, mode):
         assert np.array_equal(got["q_rot"], ref["q_rot"])
 
 
-@pytest.mark.parametrize("D", [32, 96, 256])
+@pytest.mark.parametrize("D", [32, 96, 256, 80, 127])
 def test_head_dims_packed_batch_matches_oracle(engines, D):
     """Packed sequences (a one-token one among them) at the new head sizes,
     bf16 device tensors, against the oracle per segment."""
@@ -737,11 +744,11 @@ def test_invalid_arguments_raise(engines):
     out = np.empty_like(q)
     with pytest.raises(ga.InvalidArgument):
         eng.forward_attention(0, q, k, k, out, None, 8, 3, 2, 64, 1e4)  # Hq % Hkv != 0
-    q = np.zeros((8, 2, 80), np.float32)
+    q = np.zeros((8, 2, 300), np.float32)
     with pytest.raises(ga.Unsupported):
-        eng.forward_attention(0, q, q, q, np.empty_like(q), None, 8, 2, 2, 80, 1e4)
-    assert not ga.supports_attention(512, 80)
-    assert ga.supports_attention(512, 128) and ga.supports_attention(512, 96)
+        eng.forward_attention(0, q, q, q, np.empty_like(q), None, 8, 2, 2, 300, 1e4)
+    assert not ga.supports_attention(512, 300)
+    assert ga.supports_attention(512, 128) and ga.supports_attention(512, 80)
 
 
 def test_empty_sequence_is_a_no_op(engines):

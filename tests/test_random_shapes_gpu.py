@@ -35,7 +35,7 @@ BF16_GATE = 2e-2
 EDGE_LENS = [1, 15, 16, 17, 31, 32, 33, 63, 64, 65, 127, 128, 129, 191, 255, 256, 257, 383,
              384, 385, 511, 512, 513]
 HEADS = [(1, 1), (2, 1), (3, 3), (4, 2), (6, 3), (7, 1), (8, 2), (12, 3), (14, 2), (28, 4)]
-DIMS = [32, 64, 96, 128, 256]
+DIMS = [32, 64, 96, 128, 256, 80, 112, 72]
 MODES = ["fp32", "bf16", "bf16_f32io", "rows16", "rows32", "mfma32", "mfma32_pairs"]
 
 
