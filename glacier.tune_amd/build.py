@@ -27,16 +27,19 @@ OBJDIR = os.path.join(HERE, "_build")
 
 # source -> extra hipcc flags.  attn_fwd.hip, attn_bwd.hip: the MFMAs the
 # compiler emits write VGPRs (their results feed VALU code); the long-lived
-# accumulators are pinned to AGPRs by inline assembly.  attn_fwd.hip: its
-# kernel's first 9 arguments (14 dwords) arrive preloaded in SGPRs, so its
-# first loads need no kernarg-segment round trip.  attn_kernels.hip: the
-# head_dim 256 backward asks for more full unrolling than the compiler
-# grants (it runs those loops rolled), which it reports as a failed pass.
+# accumulators are pinned to AGPRs by inline assembly.  Preload count N: the
+# first N arguments of each kernel of the file (as many as fit in 14 dwords)
+# arrive preloaded in SGPRs, so its first loads need no kernarg-segment round
+# trip; the kernels take the arguments they need first in front.
+# attn_kernels.hip: the head_dim 256 backward asks for more full unrolling
+# than the compiler grants (it runs those loops rolled), which it reports as
+# a failed pass.
+PRELOAD = ("-mllvm", "-amdgpu-kernarg-preload-count=9")
 SOURCES = {
-    "attn_kernels.hip": ("-Wno-pass-failed",),
-    "attn_fwd.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form", "-mllvm", "-amdgpu-kernarg-preload-count=9"),
+    "attn_kernels.hip": ("-Wno-pass-failed", *PRELOAD),
+    "attn_fwd.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form", *PRELOAD),
     "attn_bwd.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form"),
-    "attn_bwd3.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form"),
+    "attn_bwd3.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form", "-mllvm", "-amdgpu-kernarg-preload-count=10"),
     "attn_noalloc.hip": (),
     "attn_pad.hip": (),
     "blas_lt.cpp": (),

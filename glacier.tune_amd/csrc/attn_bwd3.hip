@@ -908,13 +908,14 @@ __device__ inline void b4_dq(const TileDesc td, const bf16* __restrict__ q_rot,
 // walks both heads' queries into the same accumulators (one partial per
 // pair); the table then holds each dQ tile twice, kTileDq for head 2x and
 // kTileDqSecond for head 2x + 1.
+// The arguments needed first lead (preloaded in SGPRs: build.py).
 template <int D>
 __global__ __launch_bounds__(kNT3) void attn_bwd3_kernel(
+    const TileDesc* __restrict__ tiles_bwd, int ratio, int head_pairs, int total_tokens, float c2,
     const bf16* __restrict__ q_rot, const bf16* __restrict__ d_out, const bf16* __restrict__ k_rot,
     const bf16* __restrict__ v, const float2* __restrict__ stats, bf16* __restrict__ dq,
-    bf16* __restrict__ wk, bf16* __restrict__ wv, const TileDesc* __restrict__ tiles_bwd,
-    const int32_t* __restrict__ pos_of, int total_tokens, float c2, float scale,
-    const float* __restrict__ cos_t, const float* __restrict__ sin_t, int ratio, int head_pairs) {
+    bf16* __restrict__ wk, bf16* __restrict__ wv, const int32_t* __restrict__ pos_of, float scale,
+    const float* __restrict__ cos_t, const float* __restrict__ sin_t) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   const int n_heads_kv = gridDim.y, n_heads_q = ratio * n_heads_kv;
   // Head pairs: the x index is rotated by the entry index, so that with an
@@ -960,13 +961,12 @@ hipError_t launch_bwd3(const BwdLaunch& a, hipStream_t st, KernelTimer* tm) {
     LaunchTiming t(tm, kKernBwd);
     const bool pairs = a.dkdv_head_pairs && ratio > 1;
     GL_LAUNCH(t, fn, dim3(pairs ? (ratio + 1) / 2 : ratio, a.n_heads_kv, a.n_wide_entries), dim3(kNT3),
-              lds, st,
+              lds, st, a.tiles_wide, ratio, pairs ? 1 : 0, a.total_tokens, a.scale * kLog2e,
               static_cast<const bf16*>(a.q_rot), static_cast<const bf16*>(a.d_out),
               static_cast<const bf16*>(a.k_rot), static_cast<const bf16*>(a.v),
               static_cast<const float2*>(stats), static_cast<bf16*>(a.dq),
-              static_cast<bf16*>(a.wk), static_cast<bf16*>(a.wv), a.tiles_wide,
-              a.single_seq ? nullptr : a.pos_of, a.total_tokens, a.scale * kLog2e, a.scale,
-              a.cos_t, a.sin_t, ratio, pairs ? 1 : 0);
+              static_cast<bf16*>(a.wk), static_cast<bf16*>(a.wv),
+              a.single_seq ? nullptr : a.pos_of, a.scale, a.cos_t, a.sin_t);
     GL_CHECK(hipGetLastError());
     t.launched();
   }

@@ -38,12 +38,12 @@ namespace glacier {
 // pos_of == nullptr: one sequence, the token index is the position (no table
 // load before the cos/sin loads).
 // ---------------------------------------------------------------------------
+// The arguments its loads need come first (preloaded in SGPRs: build.py).
 template <typename IO, typename T, int D>
 __global__ __launch_bounds__(kThreads) void rope_k_kernel(
-    const IO* __restrict__ k, IO* __restrict__ k_rot, T* __restrict__ kc,
-    const IO* __restrict__ v, T* __restrict__ vc,
-    const int32_t* __restrict__ pos_of, int total_tokens, int n_heads_kv,
-    const float* __restrict__ cos_t, const float* __restrict__ sin_t) {
+    const IO* __restrict__ k, const float* __restrict__ cos_t, const float* __restrict__ sin_t,
+    const int32_t* __restrict__ pos_of, int total_tokens, int n_heads_kv, IO* __restrict__ k_rot,
+    T* __restrict__ kc, const IO* __restrict__ v, T* __restrict__ vc) {
   constexpr int H = D / 2;
   constexpr int CH = H / 8;  // 8-pair chunks per head
   const int idx = blockIdx.x * kThreads + threadIdx.x;
@@ -885,11 +885,11 @@ __device__ inline void bwd_dkdv_tile(
 // table is read through the scalar cache (one uniform load per workgroup).
 template <typename IO, typename T, int D>
 __global__ __launch_bounds__((kThreads * bwd_groups<T, D>())) void attn_bwd_kernel(
-    const IO* __restrict__ q_rot, const IO* __restrict__ d_out, const IO* __restrict__ out,
-    const IO* __restrict__ k_rot, const IO* __restrict__ v, const float* __restrict__ lse,
+    const TileDesc* __restrict__ tiles_bwd, const IO* __restrict__ q_rot,
+    const IO* __restrict__ d_out, const IO* __restrict__ out, const IO* __restrict__ k_rot,
+    const IO* __restrict__ v, int total_tokens, float scale_log2, const float* __restrict__ lse,
     IO* __restrict__ dq, IO* __restrict__ wk, IO* __restrict__ wv, IO* __restrict__ wk2,
-    IO* __restrict__ wv2, const TileDesc* __restrict__ tiles_bwd, int total_tokens,
-    float scale_log2, float scale, const float* __restrict__ cos_t,
+    IO* __restrict__ wv2, float scale, const float* __restrict__ cos_t,
     const float* __restrict__ sin_t) {
   const TileDesc td = tiles_bwd[blockIdx.z];
   if (td.kind == kTileDq) {
@@ -917,12 +917,13 @@ __device__ inline f32x4 load_partial4(const bf16* p) {
 // SPLIT: the call split dK/dV tiles (bf16 partials), so rows below
 // split_rows have second partials.  hstep: the partials sit at every
 // hstep-th head of the group (2 after the wide backward's head pairs).
+// The arguments its loads need come first (preloaded in SGPRs: build.py).
 template <typename IO, typename T, int D, bool SPLIT>
 __global__ __launch_bounds__(kRedThreads) void attn_bwd_reduce_kernel(
-    const IO* __restrict__ wk, const IO* __restrict__ wv, IO* __restrict__ dk,
-    IO* __restrict__ dv, const IO* __restrict__ wk2, const IO* __restrict__ wv2,
-    int split_rows, const int32_t* __restrict__ pos_of, int total_tokens, int ratio,
-    int n_heads_kv, const float* __restrict__ cos_t, const float* __restrict__ sin_t, int hstep) {
+    const IO* __restrict__ wk, const IO* __restrict__ wv, const int32_t* __restrict__ pos_of,
+    const float* __restrict__ cos_t, const float* __restrict__ sin_t, int total_tokens, int ratio,
+    int n_heads_kv, int hstep, IO* __restrict__ dk, IO* __restrict__ dv,
+    const IO* __restrict__ wk2, const IO* __restrict__ wv2, int split_rows) {
   constexpr int H = D / 2;
   constexpr int CH = H / 4;  // 4-pair chunks per row
   constexpr int ROWS = kRedThreads / CH;
@@ -1053,11 +1054,10 @@ hipError_t forward_impl(const FwdLaunch& a, hipStream_t st, KernelTimer* tm) {
     IO* k_rot = static_cast<IO*>(a.k_rot);
     LaunchTiming t(tm, kKernRopeK);
     GL_LAUNCH(t, (rope_k_kernel<IO, T, D>), grid, blk, 0, st,
-                          static_cast<const IO*>(a.k), k_rot,
+                          static_cast<const IO*>(a.k), a.cos_t, a.sin_t,
+                          a.single_seq ? nullptr : a.pos_of, a.total_tokens, a.n_heads_kv, k_rot,
                           (static_cast<void*>(kc) == static_cast<void*>(k_rot)) ? nullptr : kc,
-                          static_cast<const IO*>(a.v), static_cast<T*>(a.vc),
-                          a.single_seq ? nullptr : a.pos_of, a.total_tokens, a.n_heads_kv,
-                          a.cos_t, a.sin_t);
+                          static_cast<const IO*>(a.v), static_cast<T*>(a.vc));
     GL_CHECK(hipGetLastError());
     t.launched();
   }
@@ -1108,14 +1108,13 @@ hipError_t backward_impl(const BwdLaunch& a, hipStream_t st, KernelTimer* tm) {
     LaunchTiming t(tm, kKernBwd);
     GL_LAUNCH(t, fn, dim3(ratio, a.n_heads_kv, split ? a.n_split_entries : 2 * a.n_tiles),
                           dim3(kThreads * bwd_groups<T, D>()), lds, st,
-                          static_cast<const IO*>(a.q_rot), static_cast<const IO*>(a.d_out),
-                          static_cast<const IO*>(a.out), static_cast<const IO*>(a.k_rot),
-                          static_cast<const IO*>(a.v), a.lse, static_cast<IO*>(a.dq),
+                          split ? a.tiles_split : a.tiles_bwd, static_cast<const IO*>(a.q_rot),
+                          static_cast<const IO*>(a.d_out), static_cast<const IO*>(a.out),
+                          static_cast<const IO*>(a.k_rot), static_cast<const IO*>(a.v),
+                          a.total_tokens, a.scale_log2, a.lse, static_cast<IO*>(a.dq),
                           static_cast<IO*>(a.wk), static_cast<IO*>(a.wv),
                           static_cast<IO*>(split ? a.wk2 : nullptr),
-                          static_cast<IO*>(split ? a.wv2 : nullptr),
-                          split ? a.tiles_split : a.tiles_bwd, a.total_tokens, a.scale_log2,
-                          a.scale, a.cos_t, a.sin_t);
+                          static_cast<IO*>(split ? a.wv2 : nullptr), a.scale, a.cos_t, a.sin_t);
     GL_CHECK(hipGetLastError());
     t.launched();
   }
@@ -1129,13 +1128,13 @@ hipError_t backward_impl(const BwdLaunch& a, hipStream_t st, KernelTimer* tm) {
       if (split) fn = attn_bwd_reduce_kernel<IO, T, D, true>;
     }
     GL_LAUNCH(t, fn, grid, dim3(kRedThreads), 0, st,
-                          static_cast<const IO*>(a.wk),
-                          static_cast<const IO*>(a.wv), static_cast<IO*>(a.dk),
-                          static_cast<IO*>(a.dv), static_cast<const IO*>(split ? a.wk2 : nullptr),
+                          static_cast<const IO*>(a.wk), static_cast<const IO*>(a.wv),
+                          a.single_seq ? nullptr : a.pos_of, a.cos_t, a.sin_t, a.total_tokens,
+                          ratio, a.n_heads_kv, mfma32 && a.dkdv_head_pairs && ratio > 1 ? 2 : 1,
+                          static_cast<IO*>(a.dk), static_cast<IO*>(a.dv),
+                          static_cast<const IO*>(split ? a.wk2 : nullptr),
                           static_cast<const IO*>(split ? a.wv2 : nullptr),
-                          split ? kTile * a.split : 0, a.single_seq ? nullptr : a.pos_of,
-                          a.total_tokens, ratio, a.n_heads_kv, a.cos_t, a.sin_t,
-                          mfma32 && a.dkdv_head_pairs && ratio > 1 ? 2 : 1);
+                          split ? kTile * a.split : 0);
     GL_CHECK(hipGetLastError());
     t.launched();
   }
