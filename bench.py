@@ -323,8 +323,8 @@ def run_proj(args):
             "lora_scaling": s, "io": "bf16 x/W/y/dY/dX, fp32 bias/adapters/gradients",
             "parallelism": "1 GPU", "algorithmic_gflop_per_step": round(flops / 1e9, 4),
         },
-        "roofline": {"bound": "mfma", "kernel": "whole step (hipBLASLt q GEMMs, the library's own k/v "
-                     "GEMMs and low-rank kernels)", "achieved": round(tflops, 3), "peak": PEAK_BF16_TFLOPS,
+        "roofline": {"bound": "mfma", "kernel": "whole step (the library's own q/k/v GEMMs "
+                     "and low-rank kernels)", "achieved": round(tflops, 3), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 5),
                      "traffic": None},
         "cpu_baseline": cpu,

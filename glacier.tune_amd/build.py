@@ -87,7 +87,7 @@ def build(verbose: bool = False, out: str = OUT, stamps: bool = False) -> str:
     with cf.ThreadPoolExecutor(max_workers=len(SOURCES)) as ex:
         objs = list(ex.map(lambda src: _compile(src, objdir, extra + SOURCES[src]), SOURCES))
     tmp = out + ".tmp"
-    # hipBLASLt runs the base projections' GEMMs (proj_lora.hip)
+    # hipBLASLt runs the LM head's logits GEMMs (lmhead.hip)
     rocm_lib = os.path.join(os.path.dirname(os.path.dirname(os.path.realpath(hipcc()))), "lib")
     cmd = [hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp,
            "-L" + rocm_lib, "-Wl,-rpath," + rocm_lib, "-lhipblaslt"]
