@@ -123,6 +123,14 @@ __device__ inline void store8(bf16* p, const float (&x)[8]) {
 __device__ inline void store4(float* p, f32x4 v) {
   *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
 }
+// 16 bytes from src (any address space) to global dst with the nontemporal
+// hint (global_store_dwordx4 ... nt): the line is streamed out as it is
+// written instead of staying dirty in the XCD's L2 until the end-of-kernel
+// write-back.  For results no later work of the same kernel reads.
+__device__ inline void store16_nt(void* dst, const void* src) {
+  typedef unsigned u32x4_nt __attribute__((ext_vector_type(4)));
+  __builtin_nontemporal_store(*reinterpret_cast<const u32x4_nt*>(src), reinterpret_cast<u32x4_nt*>(dst));
+}
 __device__ inline void store4(bf16* p, f32x4 v) {
   bf16x4 b;
 #pragma unroll

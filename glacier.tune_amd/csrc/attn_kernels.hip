@@ -593,7 +593,10 @@ __device__ inline void bwd_dq_tile(
     }
   };
   // The [64][D] dQ tile is staged in LDS in the output dtype (row stride
-  // D + 8), then every thread stores 16-byte pieces of consecutive rows.
+  // D + 8), then every thread stores 16-byte pieces of consecutive rows,
+  // streamed (store16_nt), like the dK/dV partials: at S=512 that shortened
+  // the step by 0.5-0.7 µs at most head counts (the kernel no longer ends on
+  // the write-back of its dirty L2 lines).
   constexpr int SR = D + 8;
   IO* const stq = reinterpret_cast<IO*>(smem_raw);
   auto finish = [&](auto grc) {
@@ -646,9 +649,8 @@ __device__ inline void bwd_dq_tile(
   for (int i = tid; i < kTile * PPR; i += kThreads * G) {
     const int r = i / PPR, pc = i % PPR;
     if (kTile * td.tile + r < td.len)
-      *reinterpret_cast<uint4*>(dq + ((long)(td.tok0 + kTile * td.tile + r) * n_heads_q + h) * D +
-                                pc * EPC) =
-          *reinterpret_cast<const uint4*>(stq + r * SR + pc * EPC);
+      store16_nt(dq + ((long)(td.tok0 + kTile * td.tile + r) * n_heads_q + h) * D + pc * EPC,
+                 stq + r * SR + pc * EPC);
   }
   GL_STAMP(kKernBwd, 22);
 }
@@ -827,7 +829,8 @@ __device__ inline void bwd_dkdv_tile(
   // sum first either way) and stages that tensor's [64 keys][D] rows in the
   // partials' dtype, so the row stores read a quarter of the fp32 bytes
   // back for bf16.  Then every thread stores 16-byte pieces of consecutive
-  // rows.  Lane (g, c) holds d = 16 db + 4 g + 0..3 of key 16 wq + c.
+  // rows (streamed, as dQ).  Lane (g, c) holds d = 16 db + 4 g + 0..3 of
+  // key 16 wq + c.
   constexpr int SR = D + 4;
   constexpr int SRO = D + (sizeof(IO) == 4 ? 4 : 8);  // row stride of the staged rows
   constexpr size_t MERGE = G == 2 ? 2 * kTile * SR * sizeof(float) : 0;
@@ -874,8 +877,8 @@ __device__ inline void bwd_dkdv_tile(
     const int key = kTile * td.tile + r;
     if (key < td.len) {
       const long wb = ((long)(td.tok0 + key) * n_heads_q + h) * D + pc * EPC;
-      *reinterpret_cast<uint4*>(wk + wb) = *reinterpret_cast<const uint4*>(sok + r * SRO + pc * EPC);
-      *reinterpret_cast<uint4*>(wv + wb) = *reinterpret_cast<const uint4*>(sov + r * SRO + pc * EPC);
+      store16_nt(wk + wb, sok + r * SRO + pc * EPC);
+      store16_nt(wv + wb, sov + r * SRO + pc * EPC);
     }
   }
   GL_STAMP(kKernBwd, 22);
