@@ -918,11 +918,20 @@ __global__ __launch_bounds__(kNT3) void attn_bwd3_kernel(
     const float* __restrict__ cos_t, const float* __restrict__ sin_t) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   const int n_heads_kv = gridDim.y, n_heads_q = ratio * n_heads_kv;
-  // Head pairs: the x index is rotated by the entry index, so that with an
-  // odd group the pair holding one head (half a dK/dV tile's work, no second
-  // dQ tile) does not always land on the same XCDs (workgroup ids are dealt
-  // to the XCDs in turn).
-  const int x = head_pairs ? 2 * (((int)blockIdx.x + (int)blockIdx.z) % (int)gridDim.x) : (int)blockIdx.x;
+  // Head pairs: the x index is rotated so that with an odd group the pair
+  // holding one head (half a dK/dV tile's work, no second dQ tile) falls to
+  // every dispatch queue in turn.  The hardware deals workgroup ids to the 8
+  // XCDs and, within each, to its 4 shader engines in turn: id mod 32 fixes
+  // the 8 CUs that run a workgroup.  An odd group rotates by the id's round
+  // of 32 (rotated by the entry index, a queue saw the entries of one parity
+  // only, i.e. two of the four pairs of a 7-head group, and the engines'
+  // loads differed by a quarter: S=4096 backward 434 -> 417 us with the
+  // round); an even group, whose pairs cost the same, keeps the entry index
+  // (0.6% faster at Llama-3 B=2 S=2048).  Either rotation is the same for
+  // all x of one (y, z), so it permutes the pairs.
+  const int rot = (ratio & 1) ? static_cast<int>((gridDim.x * (blockIdx.z * gridDim.y + blockIdx.y)) >> 5)
+                              : static_cast<int>(blockIdx.z);
+  const int x = head_pairs ? 2 * (((int)blockIdx.x + rot) % (int)gridDim.x) : (int)blockIdx.x;
   const int kvh = blockIdx.y;
   const TileDesc td = tiles_bwd[blockIdx.z];
   if (td.kind == kTileDkDv) {
@@ -935,6 +944,15 @@ __global__ __launch_bounds__(kNT3) void attn_bwd3_kernel(
     b4_dq<D>(td, q_rot, d_out, k_rot, v, stats, dq, pos_of, total_tokens, n_heads_q, n_heads_kv,
              kvh * ratio + hq, kvh, c2, scale, cos_t, sin_t, smem_raw);
   }
+#ifdef GLACIER_PHASE_STAMPS
+  // profiling builds: the workgroup's end is its last wave's (slot 22 is
+  // wave 0's)
+  __syncthreads();
+  GL_STAMP(kKernBwd, 25);
+  // where it ran: HW_ID (CU, shader array, engine) and XCC_ID
+  GL_STAMP_VALUE(kKernBwd, 26, __builtin_amdgcn_s_getreg((31 << 11) | 4));
+  GL_STAMP_VALUE(kKernBwd, 27, __builtin_amdgcn_s_getreg((31 << 11) | 20));
+#endif
 }
 
 }  // namespace

@@ -607,14 +607,19 @@ class GpuAttentionEngine {
   // backward calls): 32/8 heads, B=2 x S=1024 132 -> 120 us, B=2 x S=2048
   // 370 -> 337 us, S=4096 580 -> 551 us; slower where halving the dK/dV
   // workgroups leaves the chip short of them (16/2 heads at S=2048: 72 ->
-  // 118 us) and no gain with an odd group (28/4 heads: one head of every
-  // group alone, S=1024 60 -> 75 us, S=4096 511 -> 514 us).  So: an even
-  // group and at least one pair workgroup per CU.
-  bool head_pairs_for(int n_heads_q, int n_heads_kv, int wide_tiles) const {
+  // 118 us).  An odd group leaves one head of every group alone (half-length
+  // workgroups); fwd+bwd steps, two rounds: 28/4 heads D=128 S=2048 226 ->
+  // 219 us, S=4096 646 -> 633, two sequences of 2048 even; but 14/2 heads
+  // D=64 S=4096 254 -> 270, 40/8 heads S=4096 908 -> 955, and every shape
+  // with fewer pair workgroups than CUs slower.  So: an even group with at
+  // least one pair workgroup per CU, or a group of 7 or more heads at
+  // D=128 with at least two per CU.
+  bool head_pairs_for(int n_heads_q, int n_heads_kv, int head_dim, int wide_tiles) const {
     if (bwd_pairs_mode_ >= 0) return bwd_pairs_mode_ == 1;
     const int ratio = n_heads_q / n_heads_kv;
-    return ratio >= 2 && ratio % 2 == 0 &&
-           static_cast<long long>(ratio / 2) * n_heads_kv * wide_tiles >= n_cu_;
+    const long long pair_wgs = static_cast<long long>((ratio + 1) / 2) * n_heads_kv * wide_tiles;
+    if (ratio >= 2 && ratio % 2 == 0) return pair_wgs >= n_cu_;
+    return ratio >= 7 && head_dim == 128 && pair_wgs >= 2LL * n_cu_;
   }
 
   // Shape part of a backward launch (pointers are filled by the caller).
@@ -692,7 +697,7 @@ class GpuAttentionEngine {
     if (s.io_bf16) a.stats = stats_.ensure((T * Hq + 64) * 2 * sizeof(float), "row stats");
     const TileDesc* t = static_cast<const TileDesc*>(ts.tiles.ptr);
     a.tiles_bwd = t + ts.n_tiles;
-    a.dkdv_head_pairs = head_pairs_for(s.n_heads_q, s.n_heads_kv, ts.wide_tiles);
+    a.dkdv_head_pairs = head_pairs_for(s.n_heads_q, s.n_heads_kv, s.head_dim, ts.wide_tiles);
     a.tiles_wide = t + (a.dkdv_head_pairs ? ts.wide2_at : ts.wide_at);
     a.n_wide_entries = a.dkdv_head_pairs ? ts.wide2_entries : ts.wide_entries;
     // the longest dK/dV tiles in query halves while the launch fits the CUs
@@ -735,7 +740,7 @@ class GpuAttentionEngine {
     int wide_tiles = 0;
     for (int b = 0; b < s.n_seqs; ++b)
       wide_tiles += (s.seq_start(b + 1) - s.seq_start(b) + kWideTile - 1) / kWideTile;
-    const bool head_pairs = head_pairs_for(s.n_heads_q, s.n_heads_kv, wide_tiles);
+    const bool head_pairs = head_pairs_for(s.n_heads_q, s.n_heads_kv, s.head_dim, wide_tiles);
     NoAllocBwd w = noalloc_bwd_workspace(device_, base, s, n_cu_, split_ok_, head_pairs);
     BwdLaunch a = bwd_launch_of(BwdCall{s.total_tokens, s.n_heads_q, s.n_heads_kv, s.head_dim,
                                         s.precision, s.io_bf16, s.n_seqs == 1, w.n_tiles,
