@@ -904,6 +904,14 @@ __global__ __launch_bounds__((kThreads * bwd_groups<T, D>())) void attn_bwd_kern
     bwd_dkdv_tile<IO, T, D>(td, q_rot, d_out, out, k_rot, v, lse, second ? wk2 : wk,
                             second ? wv2 : wv, total_tokens, scale_log2, scale);
   }
+#ifdef GLACIER_PHASE_STAMPS
+  // profiling builds: the workgroup's end (its last wave's) and where it ran
+  // (HW_ID: CU, shader array, engine; XCC_ID)
+  __syncthreads();
+  GL_STAMP(kKernBwd, 25);
+  GL_STAMP_VALUE(kKernBwd, 26, __builtin_amdgcn_s_getreg((31 << 11) | 4));
+  GL_STAMP_VALUE(kKernBwd, 27, __builtin_amdgcn_s_getreg((31 << 11) | 20));
+#endif
 }
 
 // Threads of a reduction workgroup; each finishes 4 rotation pairs of one
