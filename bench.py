@@ -23,6 +23,12 @@ roofline = the dominant kernel (largest share of device time), its average
          (profiles/attn_kernels_<config>[_fp32]_pmc.md).
 cpu_baseline = the C restatement of the reference CPU path (oracle/), fp32,
          on this host's cores, over a bounded sample.
+timing = before the W warmup steps the step runs untimed for --settle-ms of
+         wall clock (default 200 ms), so that the K timed steps see the GPU's
+         steady state after sustained work, not its ramp from idle (at
+         --steps 20 --warmup 5 the headline read 39.5-39.8 us per step without
+         it, 36.6-37.2 us with 100-300 ms of it); the timed region is exactly
+         the K steps either way, and timing.settle reports the steps it ran.
 
 --precision fp32 runs the same step in the fp32-operand mode (fp32 device
 tensors, v_mfma_f32_16x16x4f32 with fp32 accumulation) and prices it against
@@ -519,6 +525,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--settle-ms", type=float, default=200.0,
+                    help="untimed steps for this long before the warmup steps (attention step; 0: none)")
     ap.add_argument("--config", default="qwen7b_s512", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--precision", default="bf16", choices=["bf16", "fp32"],
@@ -615,6 +623,20 @@ def main():
         for c in calls:
             c()
 
+    # Settle: the step itself, untimed, for args.settle_ms of wall clock
+    # before the W warmup steps, so that the timed steps see the GPU's
+    # steady state (its clocks and caches after sustained work) rather than
+    # its ramp from idle: with W = 30 the headline read 37.7-38.1 us per step,
+    # after ~0.1 s of steps 36.5-36.7 us, same library and box.  Batches of
+    # steps keep the device busy while the host enqueues the next batch.
+    settle_steps = 0
+    if args.settle_ms > 0:
+        t_end = time.perf_counter() + args.settle_ms / 1e3
+        while time.perf_counter() < t_end and settle_steps < 100000:
+            for _ in range(16):
+                step()
+            settle_steps += 16
+            torch.cuda.synchronize()
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -726,6 +748,7 @@ def main():
                        "eager: K steps enqueued back to back between two events (faster than "
                        "the graph replay of the same step)"),
             "graph_error": graph_error,
+            "settle": {"ms": args.settle_ms, "steps": settle_steps},
             "ms_per_step_graph": None if ms_graph is None else round(ms_graph, 6),
             "ms_per_step_eager": round(ms_eager, 6),
             "host_enqueue_ms_per_step": round(host_ms, 6),
