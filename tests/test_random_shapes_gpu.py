@@ -4,8 +4,10 @@ RoPEKernel, per packed segment as the reference runs one sequence per call).
 
 Each case draws 1-4 sequences (half of the lengths at tile edges: 1, 15-17,
 31-33, 63-65, 127-129, 191, 255-257, 383-385, 511-513; the rest uniform in
-[1, 600]), a (Hq, Hkv) pair with Hq % Hkv == 0, a head size, a RoPE base and
-one mode:
+[1, 600]), or, one case in ten, a single sequence of 1000-3000 tokens (the
+long-sequence backward kernels), a (Hq, Hkv) pair with Hq % Hkv == 0, a head
+size (1 to 256; sizes the kernels are not built for run on padded rows), a
+RoPE base and one mode:
   fp32         fp32 device tensors, fp32 math: gate 1e-4 on O, lse, dQ, dK,
                dV; post-RoPE q and k bit-exact
   bf16         bf16 device tensors, bf16 MFMA math (inputs rounded to bf16
@@ -16,6 +18,8 @@ one mode:
   mfma32_pairs with dK/dV tiles over head pairs) and 64-query forward
                workgroups: 2e-2
 The same seed always gives the same cases; each prints its draw first.
+GLACIER_RANDOM_CASES and GLACIER_RANDOM_SEED (default 60 and 20261202)
+draw a larger or another sweep.
 """
 import os
 import sys
@@ -34,8 +38,9 @@ BF16_GATE = 2e-2
 
 EDGE_LENS = [1, 15, 16, 17, 31, 32, 33, 63, 64, 65, 127, 128, 129, 191, 255, 256, 257, 383,
              384, 385, 511, 512, 513]
-HEADS = [(1, 1), (2, 1), (3, 3), (4, 2), (6, 3), (7, 1), (8, 2), (12, 3), (14, 2), (28, 4)]
-DIMS = [32, 64, 96, 128, 256, 80, 112, 72]
+HEADS = [(1, 1), (2, 1), (3, 3), (4, 2), (6, 3), (7, 1), (8, 2), (12, 3), (14, 2), (28, 4),
+         (32, 8), (40, 8), (21, 3), (16, 16)]
+DIMS = [32, 64, 96, 128, 256, 80, 112, 72, 1, 7, 48, 100, 127, 200]
 MODES = ["fp32", "bf16", "bf16_f32io", "rows16", "rows32", "mfma32", "mfma32_pairs"]
 
 
@@ -43,8 +48,11 @@ def _draw_cases(n=60, seed=20261202):
     rng = np.random.default_rng(seed)
     cases = []
     for i in range(n):
-        lens = [int(rng.choice(EDGE_LENS)) if rng.random() < 0.5 else int(rng.integers(1, 601))
-                for _ in range(int(rng.integers(1, 5)))]
+        if rng.random() < 0.1:
+            lens = [int(rng.integers(1000, 3001))]
+        else:
+            lens = [int(rng.choice(EDGE_LENS)) if rng.random() < 0.5 else int(rng.integers(1, 601))
+                    for _ in range(int(rng.integers(1, 5)))]
         hq, hkv = HEADS[int(rng.integers(len(HEADS)))]
         d = DIMS[int(rng.integers(len(DIMS)))]
         mode = MODES[i % len(MODES)]
@@ -52,14 +60,17 @@ def _draw_cases(n=60, seed=20261202):
             d = 128  # fp32 operands stop at 128
         if mode in ("rows16", "rows32", "mfma32", "mfma32_pairs") and d not in (64, 128):
             d = 64 if d < 128 else 128  # the pinned kernels' head sizes
-        if d == 256 and hq > 8:
+        if d >= 200 and hq > 8:
             hq, hkv = 8, 2  # keeps the oracle's share of the run short
+        if sum(lens) > 1000 and hq > 16:
+            hq, hkv = 16, 2  # likewise
         base = [1.0e4, 5.0e5, 1.0e6][int(rng.integers(3))]
         cases.append((i, tuple(lens), hq, hkv, d, base, mode))
     return cases
 
 
-CASES = _draw_cases()
+CASES = _draw_cases(int(os.environ.get("GLACIER_RANDOM_CASES", "60")),
+                    int(os.environ.get("GLACIER_RANDOM_SEED", "20261202")))
 
 
 def _say(msg):
