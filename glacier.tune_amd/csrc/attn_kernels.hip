@@ -1096,9 +1096,10 @@ hipError_t backward_impl(const BwdLaunch& a, hipStream_t st, KernelTimer* tm) {
   const int ratio = a.n_heads_q / a.n_heads_kv;
   bool rows32 = false, mfma32 = false;
   if constexpr (std::is_same<IO, bf16>::value && (D == 64 || D == 128)) {
-    const long long min_wide = D == 128 ? kBwdMfma32MinPairsD128 : kBwdMfma32MinPairsD64;
+    const long long min_work = D == 128 ? kBwdMfma32MinWorkD128 : kBwdMfma32MinWorkD64;
     mfma32 = a.tiles_wide != nullptr &&
-             (a.variant == kBwdMfma32 || (a.variant == kBwdAuto && a.pairs >= min_wide));
+             (a.variant == kBwdMfma32 ||
+              (a.variant == kBwdAuto && a.pairs * a.n_heads_q >= min_work));
     rows32 = !mfma32 && a.variant == kBwdRows32;
   }
   if (mfma32) {

@@ -157,14 +157,20 @@ struct FwdLaunch {
 };
 
 // Backward kernel choice for bf16 tensors.  kBwdAuto takes the 32x32x16-MFMA
-// kernel (attn_bwd3.hip) once a head's causal pair count reaches the measured
-// break-even below, the 16-row-wave kernel (attn_kernels.hip) under it: the
-// wide kernel's extra row-stats launch and larger per-workgroup fixed costs
-// only pay off on long sequences.  The 32-row-wave kernel (attn_bwd.hip),
-// slower than the wide one at every length measured, runs only when pinned.
+// kernel (attn_bwd3.hip) once the call's work, query heads times causal pairs
+// per head, reaches the measured break-even below, the 16-row-wave kernel
+// (attn_kernels.hip) under it: the wide kernel's extra row-stats launch, its
+// larger per-workgroup fixed costs and its 128-row tiles (fewer workgroups)
+// only pay off on large calls.  Steady-state fwd+bwd steps, both kernels
+// pinned: D=128 the 16-row kernel ahead up to 23e6 (28/4 heads at S=1280)
+// and the wide one from 33e6 (S=1536; two 1024-token sequences at 32/8
+// heads); D=64 the 16-row kernel ahead up to 117e6 (14/2 heads at S=4096),
+// the wide one from 132e6 (28/4 heads at S=3072), within 1% between.  The
+// 32-row-wave kernel (attn_bwd.hip), slower than the wide one at every length
+// measured, runs only when pinned.
 enum BwdVariant : int { kBwdAuto = 0, kBwdRows16 = 1, kBwdRows32 = 2, kBwdMfma32 = 3 };
-constexpr long long kBwdMfma32MinPairsD128 = 1024LL * 1025 / 2;  // one S=1024 sequence
-constexpr long long kBwdMfma32MinPairsD64 = 2048LL * 2049 / 2;   // one S=2048 sequence
+constexpr long long kBwdMfma32MinWorkD128 = 29000000LL;
+constexpr long long kBwdMfma32MinWorkD64 = 125000000LL;
 
 struct BwdLaunch {
   int precision;
