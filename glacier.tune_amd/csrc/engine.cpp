@@ -588,18 +588,21 @@ class GpuAttentionEngine {
     check_hip(launch_forward(a, stream(), &timer_), "attention forward launch");
   }
 
-  // Query rows per workgroup of the bf16 forward: the fewest of 16 and 32
-  // whose workgroups still fit the chip at once (two per CU where head_dim
-  // 64 leaves room in the LDS, one at 128; 32 rows only one per CU), else
-  // 64.  Measured (bench.py, one box): qwen05b S=512 forward 9.5 -> 7.2 us at
-  // 32 rows -> 6.6-6.9 us at 16; where the 64-row grid already fills the chip
-  // fewer rows are slower (qwen7b S=512: 13.3, 14.2 and 19.8 us at 64, 32
-  // and 16 rows).
+  // Query rows per workgroup of the bf16 forward: 16 when those workgroups
+  // still fit the chip at once (two per CU where head_dim 64 leaves room in
+  // the LDS, one at 128), 32 when those fill at most one and a half rounds of
+  // the CUs, else 64.  Measured (bench.py, one box): qwen05b S=512 forward
+  // 9.5 -> 7.2 us at 32 rows -> 6.6-6.9 us at 16; where the 64-row grid
+  // already fills the chip fewer rows are slower (qwen7b S=512: 13.3, 14.2
+  // and 19.8 us at 64, 32 and 16 rows, its 32-row grid 1.75 rounds).  Steady-
+  // state fwd+bwd steps at 1-1.5 rounds, 32 against 64 rows: 12/2 heads
+  // S=1024 48.3 -> 47.0 us, 14/2 heads D=64 S=768 31.4 -> 30.1, 8/2 heads
+  // S=1536 61.1 -> 57.7; 28/4 heads S=384 31.8 -> 32.1.
   int fwd_rows_for(int n_heads_q, int n_tiles, int head_dim) const {
     const long long units = static_cast<long long>(n_heads_q) * n_tiles;  // 64-row tiles
     const int per_cu = head_dim <= 64 ? 2 : 1;
     if (4 * units <= static_cast<long long>(per_cu) * n_cu_) return 16;
-    if (2 * units <= n_cu_) return 32;
+    if (4 * units <= 3LL * n_cu_) return 32;
     return 64;
   }
 
