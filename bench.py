@@ -69,6 +69,21 @@ CONFIG_LABEL = {
 }
 
 
+def settle(step, ms, sync):
+    """Runs step() untimed for ms of wall clock (batches of 16, one sync per
+    batch so the device stays busy while the host enqueues the next batch);
+    returns the steps run.  The timed steps then see the GPU's steady state."""
+    n = 0
+    if ms > 0:
+        t_end = time.perf_counter() + ms / 1e3
+        while time.perf_counter() < t_end and n < 100000:
+            for _ in range(16):
+                step()
+            n += 16
+            sync()
+    return n
+
+
 def metric_name(config, precision):
     """BASELINE.json's metric for its own config and mode; the same form,
     naming the shape and the peak priced against, for the others."""
@@ -295,6 +310,7 @@ def run_proj(args):
         eng.proj_forward(x, projs, rank)
         eng.proj_backward(x, projs, rank, dx=dx)
 
+    settle_steps = settle(step, args.settle_ms, torch.cuda.synchronize)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -334,6 +350,7 @@ def run_proj(args):
                      "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 5),
                      "traffic": None},
         "cpu_baseline": cpu,
+        "timing": {"settle": {"ms": args.settle_ms, "steps": settle_steps}},
     }
     print(json.dumps(res), flush=True)
     eng.close()
@@ -411,8 +428,12 @@ def run_norm(args):
     def bwd():
         eng.rmsnorm_backward(dy, x1, w, eps, d_residual=dres, dx=dx)
 
-    for _ in range(args.warmup):
+    def both():
         fwd(); bwd()
+
+    settle_steps = settle(both, args.settle_ms, torch.cuda.synchronize)
+    for _ in range(args.warmup):
+        both()
     torch.cuda.synchronize()
 
     def timed(fn):
@@ -465,6 +486,7 @@ def run_norm(args):
                      "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_HBM_GBS, 5), "traffic": norm_traffic(dom)},
         "cpu_baseline": cpu,
+        "timing": {"settle": {"ms": args.settle_ms, "steps": settle_steps}},
     }
     print(json.dumps(res), flush=True)
     eng.close()
@@ -526,7 +548,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--settle-ms", type=float, default=200.0,
-                    help="untimed steps for this long before the warmup steps (attention step; 0: none)")
+                    help="untimed steps for this long before the warmup steps (0: none)")
     ap.add_argument("--config", default="qwen7b_s512", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--precision", default="bf16", choices=["bf16", "fp32"],
@@ -629,14 +651,7 @@ def main():
     # its ramp from idle: with W = 30 the headline read 37.7-38.1 us per step,
     # after ~0.1 s of steps 36.5-36.7 us, same library and box.  Batches of
     # steps keep the device busy while the host enqueues the next batch.
-    settle_steps = 0
-    if args.settle_ms > 0:
-        t_end = time.perf_counter() + args.settle_ms / 1e3
-        while time.perf_counter() < t_end and settle_steps < 100000:
-            for _ in range(16):
-                step()
-            settle_steps += 16
-            torch.cuda.synchronize()
+    settle_steps = settle(step, args.settle_ms, torch.cuda.synchronize)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
