@@ -25,9 +25,14 @@ CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libglacier_attn.so")
 OBJDIR = os.path.join(HERE, "_build")
 
-# source -> extra hipcc flags.  attn_fwd.hip, attn_bwd.hip: the MFMAs the
-# compiler emits write VGPRs (their results feed VALU code); the long-lived
-# accumulators are pinned to AGPRs by inline assembly.  Preload count N: the
+# source -> extra hipcc flags.  -amdgpu-mfma-vgpr-form: the MFMAs the
+# compiler emits write VGPRs (their results feed VALU code); in attn_fwd.hip,
+# attn_bwd.hip and attn_bwd3.hip the long-lived accumulators are pinned to
+# AGPRs by inline assembly.  In attn_kernels.hip (the 16-row kernels) it
+# leaves the bf16 head_dim 64/128 instances instruction-for-instruction
+# unchanged and made steady-state steps faster at 256
+# (66.3 -> 63.4 us, 8/2 heads S=512), 96 (52.5 -> 51.0 us) and in the fp32
+# mode (161.3 -> 158.5 us at the Qwen2.5-7B S=512 shape).  Preload count N: the
 # first N arguments of each kernel of the file (as many as fit in 14 dwords)
 # arrive preloaded in SGPRs, so its first loads need no kernarg-segment round
 # trip; the kernels take the arguments they need first in front.
@@ -36,7 +41,7 @@ OBJDIR = os.path.join(HERE, "_build")
 # a failed pass.
 PRELOAD = ("-mllvm", "-amdgpu-kernarg-preload-count=9")
 SOURCES = {
-    "attn_kernels.hip": ("-Wno-pass-failed", *PRELOAD),
+    "attn_kernels.hip": ("-Wno-pass-failed", "-mllvm", "-amdgpu-mfma-vgpr-form", *PRELOAD),
     "attn_fwd.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form", *PRELOAD),
     "attn_bwd.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form"),
     "attn_bwd3.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form", "-mllvm", "-amdgpu-kernarg-preload-count=10"),
