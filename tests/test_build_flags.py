@@ -1,4 +1,4 @@
-"""The build's guard against packed FP32 arithmetic (CPU only).
+"""The build's guards against packed FP32 arithmetic and other device traps (CPU only).
 
 Every HIP source is compiled with the packed-fp32-ops target feature off, so
 the compiler emits no packed FP32 add/mul/FMA (some of their forms have given
@@ -46,6 +46,25 @@ def test_every_hip_source_is_built():
     for src, extra in build.SOURCES.items():
         # no per-source flag may turn the feature back on
         assert "+packed-fp32-ops" not in extra, src
+
+
+def test_sources_avoid_device_traps():
+    # Streams stay at the default priority (work on streams of different
+    # priorities has hung on this device class), pinned host memory is
+    # allocated rather than registered, and no memset node can be recorded
+    # into a captured graph (fill kernels clear memory instead).
+    banned = re.compile(r"hipStreamCreateWithPriority|priority\s*=|is_high_priority_stream|"
+                        r"hipHostRegister|hipMemsetAsync|hipMemsetD\d+Async")
+    files = [os.path.join(ROOT, "bench.py"), os.path.join(ROOT, "__graft_entry__.py")]
+    for ext in ("hip", "cpp", "hpp", "py"):
+        files += glob.glob(os.path.join(PKG, "**", "*." + ext), recursive=True)
+    hits = []
+    for path in files:
+        with open(path, encoding="utf-8") as f:
+            for n, line in enumerate(f, 1):
+                if banned.search(line):
+                    hits.append(f"{os.path.relpath(path, ROOT)}:{n}: {line.strip()}")
+    assert not hits, "\n".join(hits)
 
 
 @pytest.mark.skipif(not (os.path.exists(LIB) and os.access(OBJDUMP, os.X_OK)),
